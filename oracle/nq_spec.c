@@ -1,0 +1,299 @@
+/*
+ * Tier-B oracle: the row quantizer restated in plain C with a fixed arithmetic
+ * order.  TEST INFRASTRUCTURE ONLY -- the product library never links it.
+ *
+ * It restates the reference's per-row pipeline
+ *   keys  : inverse RoPE -> Hadamard -> relaxed E8 (per-row scale) -> Hadamard -> RoPE
+ *   values:                 Hadamard -> relaxed E8 (per-row scale) -> Hadamard
+ * (jagmarques/nexusquant pipeline.py:232-265, e8_lattice.py:27-124,
+ *  rope_utils.py:75-249, hadamard.py:23-43) and fixes every rounding step so
+ * that the HIP kernel can be compared with it bit for bit:
+ *
+ *  1. Inverse RoPE exactly as the reference (separate fp32 products and sums,
+ *     no FMA contraction): lo' = lo*c + hi*s ; hi' = (-lo)*s + hi*c.
+ *  2. Zero-pad to D = next power of two (the reference raises for d = 96,
+ *     hadamard.py:35-36; padding is this build's definition).
+ *  3. Unnormalised Walsh-Hadamard butterflies, stages on index bit 0,1,...,
+ *     log2(D)-1 in that order, each (a, b) -> (a + b, a - b) in fp32, then one
+ *     multiply by the reference's normalisation constant h_D.  The reference
+ *     uses a dense fp32 GEMM here, so the two differ in the last ulp; the
+ *     resulting code disagreement is measured in tests (about 1e-6 of groups).
+ *  4. amax over all D rotated values, clamped at fp32(1e-8); scale = amax/(L/2)
+ *     (exact); xn = z / scale, correctly rounded (e8_lattice.py:114-116).
+ *  5. Relaxed E8 per 8-group (e8_lattice.py:36-69): r = rint(x); on odd sum
+ *     the first smallest |x - r| coordinate steps toward x (zero gap: +1);
+ *     h = rint(x - 0.5) + 0.5.  The choice d_half < d_int is evaluated in the
+ *     algebraically identical closed form (d_half - d_int = 2 - sum|x - r| on
+ *     even sums, 1 + 2 min|x - r| - sum|x - r| on odd sums), with the sum of
+ *     |x - r| added as ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)) in fp32.  It differs
+ *     from the reference's rounded fp32 distance sums only when the two
+ *     distances are within about 1e-6 of each other (a near tie).
+ *  6. Clamp to [-L/2, L/2] after the choice (e8_lattice.py:120).
+ *  7. Reconstruction: w = S * p is exact in fp32 for every order (p is a
+ *     half-integer of magnitude <= 8), then recon = w * fl(h_D * scale),
+ *     forward RoPE as the reference (lo*c - hi*s ; lo*s + hi*c), keep the first
+ *     d outputs, round to fp16 (round to nearest even).
+ *
+ * Code symbols: the group's coset bit is 1 when the half-integer candidate was
+ * chosen.  Integer coset: sym = p + L/2.  Half coset: the clamp folds one edge
+ * point onto +-L/2 (the top edge when L/2 is even, the bottom edge when L/2 is
+ * odd, because rint rounds half to even), so sym = floor(p) + L/2 when L/2 is
+ * even and ceil(p) + L/2 when L/2 is odd; sym is always in [0, L].  Decoding:
+ * p = sym - L/2 (integer), min(sym - L/2 + 1/2, L/2) (half, L/2 even),
+ * max(sym - L/2 - 1/2, -L/2) (half, L/2 odd).
+ *
+ * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#include <stdlib.h>
+
+#define NQS_MAXD 256
+
+/* ---------------------------------------------------------------- fp16 -- */
+
+uint16_t nqs_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t absx = x & 0x7fffffffu;
+    if (absx >= 0x7f800000u) {                      /* inf / nan */
+        return (uint16_t)(sign | 0x7c00u | (absx > 0x7f800000u ? 0x200u : 0u));
+    }
+    if (absx >= 0x477ff000u) {                      /* rounds to >= 65520: overflow */
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    if (absx < 0x38800000u) {                       /* below fp16 normal range */
+        if (absx < 0x33000000u) return (uint16_t)sign;       /* < 2^-25: rounds to 0 */
+        uint32_t e = absx >> 23;
+        uint32_t m = (absx & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - e;                  /* 14 - (e - 127) + ... */
+        /* value = m * 2^(e-150); fp16 subnormal unit 2^-24 -> q = m >> (126-e) */
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t e = (absx >> 23) - 112u;              /* rebias 127 -> 15 */
+    uint32_t m = absx & 0x7fffffu;
+    uint32_t q = (e << 10) | (m >> 13);
+    uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+float nqs_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    uint32_t x;
+    if (e == 0) {
+        if (m == 0) {
+            x = sign;
+        } else {
+            float v = (float)m * 0x1p-24f;
+            memcpy(&x, &v, 4);
+            x |= sign;
+        }
+    } else if (e == 31) {
+        x = sign | 0x7f800000u | (m << 13);
+    } else {
+        x = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* ------------------------------------------------------------------ E8 -- */
+
+/* One 8-group.  x: normalised coordinates.  Outputs clamped lattice point p,
+ * coset flag, and a tie margin: the smallest distance of this group's input to
+ * any decision boundary of the rule (rint boundaries, argmin runner-up, the
+ * half/integer choice).  Returns nothing; all outputs by pointer. */
+void nqs_e8_group(const float* x, float half_levels, float* p, int* coset, float* margin) {
+    float r[8], e[8], a[8], hh[8];
+    int parity = 0;
+    for (int j = 0; j < 8; ++j) {
+        r[j] = rintf(x[j]);
+        e[j] = x[j] - r[j];
+        a[j] = fabsf(e[j]);
+        parity += (int)r[j];
+        float t = x[j] - 0.5f;
+        hh[j] = rintf(t) + 0.5f;
+    }
+    int odd = parity & 1;
+    int imin = 0;
+    float amin = a[0];
+    for (int j = 1; j < 8; ++j) {
+        if (a[j] < amin) { amin = a[j]; imin = j; }
+    }
+    float asum = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+    float thr = odd ? (1.0f + 2.0f * amin) : 2.0f;
+    int use_half = asum > thr;
+    for (int j = 0; j < 8; ++j) {
+        float v;
+        if (use_half) {
+            v = hh[j];
+        } else {
+            v = r[j];
+            if (odd && j == imin) v += (e[j] >= 0.0f) ? 1.0f : -1.0f;
+        }
+        if (v > half_levels) v = half_levels;
+        if (v < -half_levels) v = -half_levels;
+        p[j] = v;
+    }
+    *coset = use_half;
+    if (margin) {
+        float m = fabsf(asum - thr);
+        for (int j = 0; j < 8; ++j) {
+            float b1 = fabsf(a[j] - 0.5f);           /* rint boundary of r */
+            if (b1 < m) m = b1;
+            /* rint boundary of h; the row's amax coordinate is exactly +-L/2 in
+             * every implementation, so it is not a perturbable boundary */
+            if (fabsf(x[j]) != half_levels && a[j] < m) m = a[j];
+            if (odd && j != imin) {
+                float b3 = a[j] - amin;              /* argmin runner-up */
+                if (b3 < m) m = b3;
+            }
+        }
+        *margin = m;
+    }
+}
+
+/* ----------------------------------------------------------- row quant -- */
+
+static int coset_of(const uint8_t* flags, int i) { return flags[i >> 3]; }
+
+static void fwht_inplace(float* v, int D) {
+    for (int len = 1; len < D; len <<= 1) {
+        for (int i = 0; i < D; ++i) {
+            if (i & len) continue;
+            float a = v[i], b = v[i + len];
+            v[i] = a + b;
+            v[i + len] = a - b;
+        }
+    }
+}
+
+/*
+ * Quantize n rows.
+ *   x        [n][d] fp32 input rows (exact conversions of fp16/bf16/fp32)
+ *   cos_in, sin_in   [n][d/2] tables at each row's source position (keys) or NULL
+ *   cos_out, sin_out [n][d/2] tables at each row's output position (keys) or NULL
+ *   D        padded power-of-two width (>= d, <= 256), L levels (2,4,8,16)
+ *   hD       Hadamard normalisation constant for width D
+ * Outputs (any may be NULL):
+ *   xn_out   [n][D] normalised rotated rows
+ *   p_out    [n][D] clamped lattice points
+ *   sym_out  [n][D] uint8 symbols floor(p) + L/2
+ *   coset_out[n][D/8] uint8 coset flags
+ *   scale_out[n] fp32 row scale
+ *   recon_out[n][d] fp16 bits of the reconstruction
+ *   margin_out [n][D/8] tie margins
+ */
+void nqs_quant_rows(int64_t n, int d, int D, int L, float hD,
+                    const float* x,
+                    const float* cos_in, const float* sin_in,
+                    const float* cos_out, const float* sin_out,
+                    float* xn_out, float* p_out, uint8_t* sym_out, uint8_t* coset_out,
+                    float* scale_out, uint16_t* recon_out, float* margin_out) {
+    const int half = d / 2;
+    const float half_levels = (float)(L / 2);
+    const int G = D / 8;
+#pragma omp parallel for schedule(static)
+    for (int64_t row = 0; row < n; ++row) {
+        float v[NQS_MAXD], xn[NQS_MAXD], p[NQS_MAXD];
+        const float* xr = x + row * d;
+        for (int i = 0; i < D; ++i) v[i] = 0.0f;
+        if (cos_in) {
+            const float* c = cos_in + row * half;
+            const float* s = sin_in + row * half;
+            for (int i = 0; i < half; ++i) {
+                float lo = xr[i], hi = xr[i + half];
+                float t1 = lo * c[i];
+                float t2 = hi * s[i];
+                float t3 = (-lo) * s[i];
+                float t4 = hi * c[i];
+                v[i] = t1 + t2;
+                v[i + half] = t3 + t4;
+            }
+        } else {
+            for (int i = 0; i < d; ++i) v[i] = xr[i];
+        }
+        fwht_inplace(v, D);
+        float amax = 0.0f;
+        for (int i = 0; i < D; ++i) {
+            v[i] = v[i] * hD;
+            float av = fabsf(v[i]);
+            if (av > amax) amax = av;
+        }
+        if (!(amax >= 1e-8f)) amax = 1e-8f;
+        float scale = amax / half_levels;
+        for (int i = 0; i < D; ++i) xn[i] = v[i] / scale;
+        uint8_t coset_flags[NQS_MAXD / 8];
+        for (int g = 0; g < G; ++g) {
+            int cs;
+            float mg;
+            nqs_e8_group(xn + 8 * g, half_levels, p + 8 * g, &cs, &mg);
+            coset_flags[g] = (uint8_t)cs;
+            if (coset_out) coset_out[row * G + g] = (uint8_t)cs;
+            if (margin_out) margin_out[row * G + g] = mg;
+        }
+        if (xn_out) memcpy(xn_out + row * D, xn, sizeof(float) * D);
+        if (p_out) memcpy(p_out + row * D, p, sizeof(float) * D);
+        if (sym_out) {
+            const int odd_hl = (L / 2) & 1;
+            for (int i = 0; i < D; ++i) {
+                int half_cs = coset_of(coset_flags, i);
+                float f = (half_cs && odd_hl) ? ceilf(p[i]) : floorf(p[i]);
+                sym_out[row * D + i] = (uint8_t)(int)(f + half_levels);
+            }
+        }
+        if (scale_out) scale_out[row] = scale;
+        if (recon_out) {
+            float w[NQS_MAXD];
+            memcpy(w, p, sizeof(float) * D);
+            fwht_inplace(w, D);
+            float g = hD * scale;
+            for (int i = 0; i < D; ++i) w[i] = w[i] * g;
+            uint16_t* out = recon_out + row * d;
+            if (cos_out) {
+                const float* c = cos_out + row * half;
+                const float* s = sin_out + row * half;
+                for (int i = 0; i < half; ++i) {
+                    float lo = w[i], hi = w[i + half];
+                    float t1 = lo * c[i];
+                    float t2 = hi * s[i];
+                    float t3 = lo * s[i];
+                    float t4 = hi * c[i];
+                    out[i] = nqs_f32_to_f16(t1 - t2);
+                    out[i + half] = nqs_f32_to_f16(t3 + t4);
+                }
+            } else {
+                for (int i = 0; i < d; ++i) out[i] = nqs_f32_to_f16(w[i]);
+            }
+        }
+    }
+}
+
+/* Correctly rounded division check helper: q = fl(z / s) via the reciprocal
+ * refinement the HIP kernel uses (y = fl(1/s); q0 = z*y; r = fma(-q0, s, z);
+ * q = fma(r, y, q0)).  Returns the count of inputs where it differs from z/s. */
+int64_t nqs_check_markstein(int64_t n, const float* z, const float* s) {
+    int64_t bad = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        float y = 1.0f / s[i];
+        float q0 = z[i] * y;
+        float r = fmaf(-q0, s[i], z[i]);
+        float q = fmaf(r, y, q0);
+        float ref = z[i] / s[i];
+        uint32_t a, b;
+        memcpy(&a, &q, 4);
+        memcpy(&b, &ref, 4);
+        if (a != b) ++bad;
+    }
+    return bad;
+}

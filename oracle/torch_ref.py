@@ -1,0 +1,551 @@
+"""Tier-A oracle: op-for-op torch-CPU restatement of the reference KV-compression path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product package (`nexusquant_amd/`)
+may import this module; only `tests/`, `__graft_entry__.smoke()` and the
+`cpu_baseline` leg of `bench.py` use it, and only as the checker / CPU timing
+baseline.
+
+Every function repeats the reference's torch operator sequence (same ops, same
+dtypes, same reduction shapes) so that on a given CPU its results equal the
+reference's bit for bit; `tests/golden/` holds fixtures written by the real
+reference that pin this claim.  Citations are `path:line` inside the reference
+repository (jagmarques/nexusquant v0.5.0).
+
+Pinning (see tests/test_oracle_*.py):
+  e8_nearest_point        golden fixtures + Appendix-B known answers + invariants
+  e8_quantize_perhead     golden fixtures + closed-form invariants
+  hadamard_matrix         closed form (orthonormal, +-1/sqrt(n) entries)
+  rope tables / rotation  golden fixtures + round-trip identities
+  quant_only_compress     golden fixtures (reference NexusQuantEvict rate 0)
+  score_keykey            golden fixtures + brute-force softmax on tiny inputs
+  build_keep_mask         golden fixtures + reference test properties
+  evict_mask_compress     golden fixtures
+  evict_truncate_compress golden fixtures
+  score_real_from_qk      golden fixtures written through transformers' eager
+                          attention (third-party formula, transformers 5.15.0)
+  delta_encode/decode     closed form + lossless round trip
+"""
+
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+import torch.nn.functional as F
+
+
+# ---------------------------------------------------------------------------
+# Hadamard  (nexusquant/core/hadamard.py:15-43)
+# ---------------------------------------------------------------------------
+
+def next_power_of_2(n: int) -> int:
+    """Smallest power of two >= n (hadamard.py:15-20)."""
+    p = 1
+    while p < n:
+        p <<= 1
+    return p
+
+
+def hadamard_matrix(n: int) -> torch.Tensor:
+    """Orthonormal Sylvester matrix built by recursive doubling (hadamard.py:23-43).
+
+    Each doubling divides by the Python float sqrt(2) in fp32, exactly as the
+    reference does, so the entries equal the reference's bit for bit.
+    """
+    if n & (n - 1):
+        raise ValueError(f"n must be power of 2, got {n}. Use pad_to_power_of_2() first.")
+    mat = torch.tensor([[1.0]])
+    size = 1
+    while size < n:
+        top = torch.cat([mat, mat], dim=1)
+        bottom = torch.cat([mat, -mat], dim=1)
+        mat = torch.cat([top, bottom], dim=0) / math.sqrt(2)
+        size *= 2
+    return mat
+
+
+# ---------------------------------------------------------------------------
+# RoPE  (nexusquant/core/rope_utils.py:34-249)
+# ---------------------------------------------------------------------------
+
+def rope_scaled_inv_freq(inv_freq: torch.Tensor, rope_scaling: Optional[dict]) -> torch.Tensor:
+    """Frequency scaling for linear / dynamic / llama3 configs (rope_utils.py:34-72)."""
+    if rope_scaling is None:
+        return inv_freq
+    kind = rope_scaling.get("type", rope_scaling.get("rope_type", "linear"))
+    factor = float(rope_scaling.get("factor", 1.0))
+    if factor == 1.0:
+        return inv_freq
+    if kind in ("linear", "dynamic"):
+        return inv_freq / factor
+    if kind == "llama3":
+        lo = float(rope_scaling.get("low_freq_factor", 1.0))
+        hi = float(rope_scaling.get("high_freq_factor", 4.0))
+        old_len = int(rope_scaling.get("original_max_position_embeddings", 8192))
+        lo_wl = old_len / lo
+        hi_wl = old_len / hi
+        out = []
+        for f in inv_freq:
+            wl = 2.0 * math.pi / f.item()
+            if wl < hi_wl:
+                out.append(f)
+            elif wl > lo_wl:
+                out.append(f / factor)
+            else:
+                t = (old_len / wl - lo) / (hi - lo)
+                out.append((1.0 - t) * f / factor + t * f)
+        return torch.stack(out)
+    return inv_freq
+
+
+def rope_inv_freq(d: int, base: float, rope_scaling: Optional[dict] = None) -> torch.Tensor:
+    """inv_freq = 1 / base**(arange(0,d,2)/d) in fp32 on the CPU (rope_utils.py:106-108)."""
+    inv = 1.0 / (base ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    return rope_scaled_inv_freq(inv, rope_scaling)
+
+
+def rope_cos_sin(positions: torch.Tensor, d: int, base: float,
+                 rope_scaling: Optional[dict] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """fp32 cos/sin tables [len(positions), d/2] (rope_utils.py:109-112, 151-154)."""
+    inv = rope_inv_freq(d, base, rope_scaling)
+    ang = torch.outer(positions.to(torch.float32), inv)
+    return ang.cos(), ang.sin()
+
+
+def _rot_inverse(keys: torch.Tensor, cos_f: torch.Tensor, sin_f: torch.Tensor) -> torch.Tensor:
+    half = keys.shape[-1] // 2
+    lo = keys[..., :half]
+    hi = keys[..., half:]
+    out = keys.clone()
+    out[..., :half] = lo * cos_f + hi * sin_f
+    out[..., half:] = -lo * sin_f + hi * cos_f
+    return out
+
+
+def _rot_forward(keys: torch.Tensor, cos_f: torch.Tensor, sin_f: torch.Tensor) -> torch.Tensor:
+    half = keys.shape[-1] // 2
+    lo = keys[..., :half].clone()
+    hi = keys[..., half:].clone()
+    out = keys.clone()
+    out[..., :half] = lo * cos_f - hi * sin_f
+    out[..., half:] = lo * sin_f + hi * cos_f
+    return out
+
+
+def inverse_rope(keys: torch.Tensor, seq_offset: int = 0, base: float = 10000.0,
+                 rope_scaling: Optional[dict] = None) -> torch.Tensor:
+    """Split-half RoPE removal at positions offset..offset+s-1 (rope_utils.py:75-122)."""
+    squeeze = keys.dim() == 3
+    k4 = keys.unsqueeze(0) if squeeze else keys
+    s, d = k4.shape[2], k4.shape[3]
+    pos = torch.arange(s, dtype=torch.float32) + seq_offset
+    c, sn = rope_cos_sin(pos, d, base, rope_scaling)
+    out = _rot_inverse(k4, c.to(k4.device, k4.dtype), sn.to(k4.device, k4.dtype))
+    return out.squeeze(0) if squeeze else out
+
+
+def forward_rope(keys: torch.Tensor, seq_offset: int = 0, base: float = 10000.0,
+                 rope_scaling: Optional[dict] = None) -> torch.Tensor:
+    """Split-half RoPE application (rope_utils.py:203-249)."""
+    squeeze = keys.dim() == 3
+    k4 = keys.unsqueeze(0) if squeeze else keys
+    s, d = k4.shape[2], k4.shape[3]
+    pos = torch.arange(s, dtype=torch.float32) + seq_offset
+    c, sn = rope_cos_sin(pos, d, base, rope_scaling)
+    out = _rot_forward(k4, c.to(k4.device, k4.dtype), sn.to(k4.device, k4.dtype))
+    return out.squeeze(0) if squeeze else out
+
+
+def inverse_rope_at_positions(keys: torch.Tensor, positions: torch.Tensor, base: float = 10000.0,
+                              rope_scaling: Optional[dict] = None) -> torch.Tensor:
+    """RoPE removal at explicit positions, keys [h, s, d] (rope_utils.py:125-162)."""
+    d = keys.shape[-1]
+    c, sn = rope_cos_sin(positions.float(), d, base, rope_scaling)
+    return _rot_inverse(keys, c.to(keys.dtype), sn.to(keys.dtype))
+
+
+def forward_rope_at_positions(keys: torch.Tensor, positions: torch.Tensor, base: float = 10000.0,
+                              rope_scaling: Optional[dict] = None) -> torch.Tensor:
+    """RoPE application at explicit positions, keys [h, s, d] (rope_utils.py:165-200)."""
+    d = keys.shape[-1]
+    c, sn = rope_cos_sin(positions.float(), d, base, rope_scaling)
+    return _rot_forward(keys, c.to(keys.dtype), sn.to(keys.dtype))
+
+
+# ---------------------------------------------------------------------------
+# Relaxed E8 lattice  (nexusquant/core/e8_lattice.py:27-124)
+# ---------------------------------------------------------------------------
+
+def e8_nearest_point(x: torch.Tensor) -> torch.Tensor:
+    """Reference relaxed-E8 rule on (..., 8) fp32 (e8_lattice.py:27-69).
+
+    Integer candidate: round-half-even, and when the coordinate sum is odd the
+    FIRST smallest-gap coordinate steps one unit toward x (a zero gap steps +1).
+    Half candidate: round(x - 0.5) + 0.5 with no parity repair (the reference's
+    repair branch at :55-62 can never fire).  The half candidate wins only when
+    its squared distance is strictly smaller.
+    """
+    r = x.round()
+    odd = (r.sum(dim=-1) % 2) != 0
+    if odd.any():
+        gap = (x - r).abs()
+        where = gap[odd].argmin(dim=-1, keepdim=True)
+        step = torch.zeros_like(r[odd]).scatter_(-1, where, 1.0)
+        direction = ((x[odd] - r[odd]).gather(-1, where) >= 0).float() * 2 - 1
+        r[odd] = r[odd] + step * direction
+    h = (x - 0.5).round() + 0.5
+    d_int = ((x - r) ** 2).sum(dim=-1)
+    d_half = ((x - h) ** 2).sum(dim=-1)
+    out = r.clone()
+    take = d_half < d_int
+    out[take] = h[take]
+    return out
+
+
+def e8_quantize_perhead_parts(x: torch.Tensor, levels: int):
+    """Per-row quantizer split into its parts (e8_lattice.py:97-124).
+
+    Returns (lattice points p [rows, d] after clamp, scale [rows, 1]); the
+    reference's output is `p * scale`.
+    """
+    d = x.shape[-1]
+    flat = x.reshape(-1, d)
+    amax = flat.abs().amax(dim=-1, keepdim=True).clamp(min=1e-8)
+    scale = amax / (levels / 2)
+    norm = flat / scale
+    pad = (8 - d % 8) % 8
+    if pad:
+        norm = F.pad(norm, (0, pad))
+    lp = e8_nearest_point(norm.reshape(-1, 8)).clamp(-levels / 2, levels / 2)
+    p = lp.reshape(norm.shape)
+    if pad:
+        p = p[..., :d]
+    return p, scale
+
+
+def e8_quantize_perhead(x: torch.Tensor, levels: int = 8) -> torch.Tensor:
+    """x -> p*scale, same shape (e8_lattice.py:97-124)."""
+    p, scale = e8_quantize_perhead_parts(x, levels)
+    return (p * scale).reshape(x.shape)
+
+
+def e8_quantize_pergroup(x: torch.Tensor, levels: int = 8) -> torch.Tensor:
+    """Per-8-group scaled variant (e8_lattice.py:72-94)."""
+    shape = x.shape
+    pad = (8 - shape[-1] % 8) % 8
+    if pad:
+        x = F.pad(x, (0, pad))
+    flat = x.reshape(-1, 8)
+    amax = flat.abs().amax(dim=-1, keepdim=True).clamp(min=1e-8)
+    sc = amax / (levels / 2)
+    lp = e8_nearest_point(flat / sc).clamp(-levels / 2, levels / 2) * sc
+    res = lp.reshape(x.shape)
+    if pad:
+        res = res[..., :shape[-1]]
+    return res.reshape(shape)
+
+
+def lattice_codes_2p(p: torch.Tensor) -> torch.Tensor:
+    """Stored int8 code = round(2p), the vLLM page format (vllm_backend.py:309-314)."""
+    return (p * 2).round().clamp(-127, 127).to(torch.int8)
+
+
+# ---------------------------------------------------------------------------
+# Cache access  (nexusquant/pipeline.py:25-66)
+# ---------------------------------------------------------------------------
+
+def get_layer_kv(cache, i):
+    if hasattr(cache, "key_cache") and hasattr(cache, "value_cache"):
+        return cache.key_cache[i], cache.value_cache[i]
+    layer = cache.layers[i]
+    return layer.keys, layer.values
+
+
+def set_layer_kv(cache, i, k, v):
+    if hasattr(cache, "key_cache") and hasattr(cache, "value_cache"):
+        cache.key_cache[i] = k
+        cache.value_cache[i] = v
+        return
+    cache.layers[i].keys = k
+    cache.layers[i].values = v
+
+
+def num_layers(cache) -> int:
+    if hasattr(cache, "key_cache"):
+        return len(cache.key_cache)
+    return len(cache.layers)
+
+
+# ---------------------------------------------------------------------------
+# Per-layer quantization bodies
+# ---------------------------------------------------------------------------
+
+def _quant_keys(k: torch.Tensor, H: torch.Tensor, levels: int, base: float,
+                rope_scaling: Optional[dict]) -> torch.Tensor:
+    """Keys of one layer, looped over batch (pipeline.py:245-255)."""
+    b, h, s, d = k.shape
+    outs = []
+    for bi in range(b):
+        k_nr = inverse_rope(k[bi], base=base, rope_scaling=rope_scaling)
+        k_rot = torch.einsum('hsd,de->hse', k_nr, H)
+        k_q = e8_quantize_perhead(k_rot.reshape(-1, d), levels=levels)
+        k_back = torch.einsum('hsd,ed->hse', k_q.reshape(h, s, d), H)
+        outs.append(forward_rope(k_back, base=base, rope_scaling=rope_scaling))
+    return torch.stack(outs, dim=0)
+
+
+def _quant_values(v: torch.Tensor, H: torch.Tensor, levels: int) -> torch.Tensor:
+    """Values of one layer, batched (pipeline.py:257-261)."""
+    b, h, s, d = v.shape
+    v_rot = torch.einsum('bhsd,de->bhse', v, H)
+    v_q = e8_quantize_perhead(v_rot.reshape(-1, d), levels=levels)
+    return torch.einsum('bhsd,ed->bhse', v_q.reshape(b, h, s, d), H)
+
+
+def quant_only_compress(cache, key_levels: int = 8, value_levels: int = 8,
+                        rope_base: float = 10000.0, rope_scaling: Optional[dict] = None,
+                        skip_layers: Sequence[int] = ()):
+    """NexusQuantQuantOnly.compress with independent K/V levels (pipeline.py:232-265).
+
+    With key_levels == value_levels this is the reference class exactly; with
+    K8/V4 it equals NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0)
+    (every token kept, mask multiply by 1.0 is exact, pipeline.py:1190-1242).
+    """
+    for li in range(num_layers(cache)):
+        if li in skip_layers:
+            continue
+        k, v = get_layer_kv(cache, li)
+        k = k.float()
+        v = v.float()
+        d = k.shape[-1]
+        H = hadamard_matrix(d).to(k.device).float()
+        k_out = _quant_keys(k, H, key_levels, rope_base, rope_scaling).half()
+        v_out = _quant_values(v, H, value_levels).half()
+        set_layer_kv(cache, li, k_out, v_out)
+    return cache
+
+
+# ---------------------------------------------------------------------------
+# Importance scoring  (pipeline.py:756-836)
+# ---------------------------------------------------------------------------
+
+def score_keykey(keys: torch.Tensor, obs_window: int = 32) -> torch.Tensor:
+    """SnapKV-style key-key proxy (pipeline.py:756-782): [b,h,s,d] -> [b,s]."""
+    b, h, s, d = keys.shape
+    scale = d ** -0.5
+    obs = min(obs_window, s)
+    q = keys[:, :, -obs:, :]
+    kk = keys[:, :, :s, :]
+    att = torch.einsum('bhqd,bhkd->bhqk', q.float(), kk.float()) * scale
+    att = torch.softmax(att, dim=-1)
+    return att.sum(dim=2).mean(dim=1)
+
+
+def eager_attention_probs(q: torch.Tensor, k: torch.Tensor, scaling: float) -> torch.Tensor:
+    """HF eager attention probabilities for one layer.
+
+    transformers 5.15.0 models/llama/modeling_llama.py:179-213: repeat_kv for
+    GQA, matmul(Q, K^T) * scaling in the model dtype, add the causal mask
+    (dtype minimum above the diagonal), softmax in fp32, cast back.
+    q [b, hq, s, d], k [b, hkv, s, d] -> probs [b, hq, s, s] in q.dtype.
+    """
+    b, hq, s, d = q.shape
+    rep = hq // k.shape[1]
+    kr = k[:, :, None, :, :].expand(b, k.shape[1], rep, s, d).reshape(b, hq, s, d)
+    w = torch.matmul(q, kr.transpose(2, 3)) * scaling
+    mask = torch.full((s, s), torch.finfo(q.dtype).min, dtype=q.dtype, device=q.device).triu(1)
+    w = w + mask
+    return torch.softmax(w, dim=-1, dtype=torch.float32).to(q.dtype)
+
+
+def score_real_from_qk(q_layers: Sequence[torch.Tensor], k_layers: Sequence[torch.Tensor],
+                       scaling: Optional[float] = None) -> torch.Tensor:
+    """Importance from real attention (pipeline.py:822-836) given per-layer Q, K."""
+    b, _, s, d = q_layers[0].shape
+    if scaling is None:
+        scaling = d ** -0.5
+    imp = torch.zeros(b, s, dtype=torch.float32)
+    for q, k in zip(q_layers, k_layers):
+        probs = eager_attention_probs(q, k, scaling).float()
+        imp += probs.sum(dim=2).mean(dim=1)
+    return imp / len(q_layers)
+
+
+# ---------------------------------------------------------------------------
+# Keep mask  (pipeline.py:895-959) and rate adjustments (:1083-1100)
+# ---------------------------------------------------------------------------
+
+def adaptive_context_rate(rate: float, seq: int) -> float:
+    """Short-prefix rate scaling (pipeline.py:1093-1100)."""
+    if seq < 256:
+        return 0.0
+    if seq < 512:
+        return rate * 0.5
+    if seq < 1024:
+        return rate * 0.75
+    return rate
+
+
+def auto_eviction_rate(importance: torch.Tensor, seq: int) -> float:
+    """Entropy-driven rate (pipeline.py:838-861)."""
+    probs = importance[0] / (importance[0].sum() + 1e-8)
+    ent = -(probs * (probs + 1e-8).log()).sum().item()
+    norm = ent / math.log(max(seq, 2))
+    return max(0.1, min(0.7, 0.7 - 0.5 * norm))
+
+
+def build_keep_mask(importance: torch.Tensor, seq: int, rate: float, sliding_window: int = 32,
+                    protected_positions=None, distance_graduated: bool = False) -> torch.Tensor:
+    """BOS + recent window + top-k of the evictable prefix (pipeline.py:895-959)."""
+    b = importance.shape[0]
+    prefix = max(seq - sliding_window, 0)
+    n_keep = max(1, int(prefix * (1.0 - rate)))
+    keep = torch.zeros(b, seq, dtype=torch.bool, device=importance.device)
+    keep[:, 0] = True
+    if sliding_window > 0 and seq > 0:
+        keep[:, max(0, seq - sliding_window):] = True
+    if distance_graduated and prefix > 1:
+        ramp = torch.linspace(0.0, 1.0, prefix - 1, device=importance.device)
+        boost = ramp * importance[:, 1:prefix].max() * 0.25
+        importance = importance.clone()
+        importance[:, 1:prefix] = importance[:, 1:prefix] + boost
+    if prefix > 1 and n_keep > 0:
+        scores = importance[:, 1:prefix]
+        k = min(n_keep, scores.shape[1])
+        if k > 0:
+            _, idx = torch.topk(scores, k=k, dim=1)
+            keep.scatter_(1, idx + 1, True)
+    if protected_positions is not None:
+        for pos in protected_positions:
+            i = int(pos)
+            if 0 <= i < seq:
+                keep[:, i] = True
+    return keep
+
+
+def boundary_skip_layers(n_layers: int, n_protect: int, protected_layers=()) -> set:
+    """Boundary + explicit protected layers (pipeline.py:1110-1121)."""
+    skip = set(protected_layers or ())
+    for i in range(min(max(n_protect, 0), n_layers)):
+        skip.add(i)
+        skip.add(n_layers - 1 - i)
+    return skip
+
+
+def resolve_layer_levels(layer: int, n_layers: int, key_levels: int, value_levels: int,
+                         profile: str = "uniform") -> Tuple[int, int]:
+    """Graduated bit profile (pipeline.py:740-754)."""
+    if profile == "graduated":
+        edge = max(1, int(n_layers * 0.15))
+        if layer < edge or layer >= n_layers - edge:
+            return 8, 8
+    return key_levels, value_levels
+
+
+# ---------------------------------------------------------------------------
+# Eviction pipelines
+# ---------------------------------------------------------------------------
+
+def evict_mask_compress(cache, key_levels: int, value_levels: int, rate: float,
+                        sliding_window: int = 32, obs_window: int = 32, rope_base: float = 10000.0,
+                        rope_scaling: Optional[dict] = None, importance: Optional[torch.Tensor] = None,
+                        skip_layers: Sequence[int] = (), protected_positions=None,
+                        layer_bit_profile: str = "uniform"):
+    """Hard-eviction mask path of NexusQuantEvict.compress (pipeline.py:1050-1244).
+
+    Returns (cache, mask [b, s] float).  `importance` overrides the key-key
+    scorer (used for the real-attention scorer).
+    """
+    n = num_layers(cache)
+    k0, _ = get_layer_kv(cache, 0)
+    b, _, seq, _ = k0.shape
+    if importance is None:
+        importance = score_keykey(k0.float(), obs_window)
+    keep = build_keep_mask(importance, seq, rate, sliding_window, protected_positions)
+    mask_out = keep.float()
+    for li in range(n):
+        k, v = get_layer_kv(cache, li)
+        k = k.float()
+        v = v.float()
+        _, h, s_l, d = k.shape
+        m4 = keep[:, :s_l].unsqueeze(1).unsqueeze(-1).float()
+        k = k * m4
+        v = v * m4
+        if li in skip_layers:
+            set_layer_kv(cache, li, k.to(torch.float16), v.to(torch.float16))
+            continue
+        H = hadamard_matrix(d).to(k.device).float()
+        kl, vl = resolve_layer_levels(li, n, key_levels, value_levels, layer_bit_profile)
+        k_out = _quant_keys(k, H, kl, rope_base, rope_scaling).to(torch.float16)
+        v_out = _quant_values(v, H, vl).to(torch.float16)
+        k_out = k_out * m4.half()
+        v_out = v_out * m4.half()
+        set_layer_kv(cache, li, k_out, v_out)
+    return cache, mask_out
+
+
+def evict_truncate_compress(cache, key_levels: int, value_levels: int, rate: float,
+                            sliding_window: int = 32, obs_window: int = 32,
+                            rope_base: float = 10000.0, rope_scaling: Optional[dict] = None,
+                            skip_layers: Sequence[int] = (), protected_positions=None,
+                            layer_bit_profile: str = "uniform"):
+    """NexusQuantEvictTruncate.compress (pipeline.py:1270-1406): returns (cache, n_kept)."""
+    n = num_layers(cache)
+    k0, _ = get_layer_kv(cache, 0)
+    b, _, seq, _ = k0.shape
+    if b > 1:
+        raise ValueError(
+            f"NexusQuantEvictTruncate does not support batch_size > 1 (got {b}).")
+    importance = score_keykey(k0.float(), obs_window)
+    keep = build_keep_mask(importance, seq, rate, sliding_window, protected_positions)
+    kept = keep[0].nonzero(as_tuple=True)[0]
+    n_kept = kept.shape[0]
+    for li in range(n):
+        k, v = get_layer_kv(cache, li)
+        _, h, s_l, d = k.shape
+        lk = kept[kept < s_l]
+        nk = lk.shape[0]
+        k_kept = k[:, :, lk, :].float()
+        v_kept = v[:, :, lk, :].float()
+        if li in skip_layers:
+            set_layer_kv(cache, li, k_kept.to(torch.float16), v_kept.to(torch.float16))
+            continue
+        H = hadamard_matrix(d).to(k.device).float()
+        kl, vl = resolve_layer_levels(li, n, key_levels, value_levels, layer_bit_profile)
+        pos_in = lk.float()
+        pos_out = torch.arange(nk, dtype=torch.float32)
+        outs = []
+        for bi in range(b):
+            k_nr = inverse_rope_at_positions(k_kept[bi], pos_in, base=rope_base, rope_scaling=rope_scaling)
+            k_rot = torch.einsum('hsd,de->hse', k_nr, H)
+            k_q = e8_quantize_perhead(k_rot.reshape(-1, d), levels=kl)
+            k_back = torch.einsum('hsd,ed->hse', k_q.reshape(h, nk, d), H)
+            outs.append(forward_rope_at_positions(k_back, pos_out, base=rope_base, rope_scaling=rope_scaling))
+        k_out = torch.stack(outs, dim=0).to(torch.float16)
+        v_rot = torch.einsum('bhsd,de->bhse', v_kept, H)
+        v_q = e8_quantize_perhead(v_rot.reshape(-1, d), levels=vl)
+        v_out = torch.einsum('bhsd,ed->bhse', v_q.reshape(b, h, nk, d), H).to(torch.float16)
+        set_layer_kv(cache, li, k_out, v_out)
+    return cache, n_kept
+
+
+# ---------------------------------------------------------------------------
+# Temporal delta stream  (nexusquant/core/compression_accounting.py:49-77)
+# ---------------------------------------------------------------------------
+
+def delta_encode(codes: torch.Tensor) -> torch.Tensor:
+    """int8 codes [streams, tokens, coords] -> deltas along tokens (int8 wrap)."""
+    import numpy as np
+    x = codes.numpy().astype(np.int8)
+    out = np.zeros_like(x)
+    out[:, 0, :] = x[:, 0, :]
+    out[:, 1:, :] = x[:, 1:, :] - x[:, :-1, :]
+    return torch.from_numpy(out.astype(np.int8))
+
+
+def delta_decode(delta: torch.Tensor) -> torch.Tensor:
+    """Inverse of delta_encode: cumulative sum along tokens, wrapped to int8."""
+    import numpy as np
+    x = delta.numpy()
+    return torch.from_numpy(np.cumsum(x, axis=1).astype(np.int8))

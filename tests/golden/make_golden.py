@@ -1,0 +1,180 @@
+"""Write golden fixtures from the real reference (run in the build container only).
+
+The reference (jagmarques/nexusquant v0.5.0, mounted read-only at
+/root/reference) is imported here, on the CPU, to record input/output vectors
+for the functions whose exact results no closed form pins: the end-to-end
+pipelines (dense-GEMM Hadamard and torch reduction order), the key-key scorer,
+torch.topk keep masks, and the real-attention scorer through transformers'
+eager attention.  Nothing under /root/reference is copied; only the numbers it
+produces are stored, as small .npz files next to this script.
+
+Usage:  python tests/golden/make_golden.py [/root/reference]
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REF = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+sys.path.insert(0, REF)
+
+from nexusquant.pipeline import (NexusQuantEvict, NexusQuantEvictTruncate,  # noqa: E402
+                                 NexusQuantQuantOnly, compress_kv_cache)
+from nexusquant.core.e8_lattice import E8Lattice  # noqa: E402
+from nexusquant.core.rope_utils import inverse_rope, forward_rope  # noqa: E402
+
+
+class ListCache:
+    def __init__(self, ks, vs):
+        self.key_cache = list(ks)
+        self.value_cache = list(vs)
+
+
+def synth_kv(seed, n_layers, b, h, s, d, base, sink=False, dtype=torch.float16):
+    """Keys: N(0,1) with 4 outlier channels x8 per head, then RoPE; values N(0, 0.5^2)."""
+    g = torch.Generator().manual_seed(seed)
+    ks, vs = [], []
+    for _ in range(n_layers):
+        kp = torch.randn(b, h, s, d, generator=g)
+        for hi in range(h):
+            ch = torch.randperm(d, generator=g)[:4]
+            kp[:, hi, :, ch] *= 8
+        if sink:
+            kp[:, :, 0, :] *= 4
+        k = forward_rope(kp, base=base)
+        v = torch.randn(b, h, s, d, generator=g) * 0.5
+        ks.append(k.to(dtype))
+        vs.append(v.to(dtype))
+    return ks, vs
+
+
+def save(name, **arrays):
+    path = os.path.join(HERE, name + ".npz")
+    np.savez_compressed(path, **{k: (v.numpy() if torch.is_tensor(v) else np.asarray(v))
+                                 for k, v in arrays.items()})
+    print("wrote", path, os.path.getsize(path), "bytes")
+
+
+def stack(ts):
+    return torch.stack([t for t in ts])
+
+
+def main():
+    torch.manual_seed(0)
+
+    # 1. E8 nearest point and per-row quantizer.
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(16384, 8, generator=g) * 1.7
+    x[:64] = torch.round(x[:64] * 2) / 2          # exact half/integer ties
+    x[64:128] = torch.round(x[64:128])           # integer points
+    save("e8_nearest", x=x, p=E8Lattice.nearest_point(x.clone()))
+    rows = torch.randn(512, 128, generator=g)
+    rows[0] = 0.0
+    save("e8_perhead", x=rows, q8=E8Lattice.quantize_perhead(rows.clone(), levels=8),
+         q4=E8Lattice.quantize_perhead(rows.clone(), levels=4),
+         q2=E8Lattice.quantize_perhead(rows.clone(), levels=2),
+         q16=E8Lattice.quantize_perhead(rows.clone(), levels=16))
+
+    # 2. RoPE at large positions (pins the host cos/sin table construction).
+    kk = torch.randn(2, 64, 128, generator=g)
+    save("rope_far", x=kk,
+         inv=inverse_rope(kk, seq_offset=131008, base=500000.0),
+         fwd=forward_rope(kk, seq_offset=131008, base=500000.0),
+         inv_scaled=inverse_rope(kk, seq_offset=40000, base=500000.0,
+                                 rope_scaling={"rope_type": "llama3", "factor": 8.0,
+                                               "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                                               "original_max_position_embeddings": 8192}))
+
+    # 3. Quant-only K3V2 (== NexusQuantEvict rate 0) and symmetric QuantOnly.
+    for base, tag in ((10000.0, "b1e4"), (500000.0, "b5e5")):
+        ks, vs = synth_kv(21, 2, 1, 2, 256, 128, base)
+        c = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+        nq = NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.0, rope_base=base)
+        _, mask = nq.compress(c)
+        c3 = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+        compress_kv_cache(c3, mode="quant_only", rope_base=base)
+        save(f"quant_only_{tag}", k_in=stack(ks), v_in=stack(vs),
+             k_k3v2=stack(c.key_cache), v_k3v2=stack(c.value_cache), mask=mask,
+             k_k3v3=stack(c3.key_cache), v_k3v3=stack(c3.value_cache), base=base)
+
+    # 4. d = 256 quant-only K2V2; bf16 input K3V2.
+    ks, vs = synth_kv(31, 1, 1, 2, 128, 256, 10000.0)
+    c = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+    NexusQuantEvict(bits=2, eviction_rate=0.0, rope_base=10000.0).compress(c)
+    save("quant_only_d256", k_in=stack(ks), v_in=stack(vs), k_out=stack(c.key_cache),
+         v_out=stack(c.value_cache))
+    ks, vs = synth_kv(32, 1, 1, 2, 256, 128, 500000.0, dtype=torch.bfloat16)
+    c = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+    NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.0, rope_base=500000.0).compress(c)
+    save("quant_only_bf16", k_in=stack(ks).float(), v_in=stack(vs).float(),
+         k_out=stack(c.key_cache), v_out=stack(c.value_cache))
+
+    # 5. Key-key scorer and keep masks, mask-mode eviction, b = 4 with a sink.
+    ks, vs = synth_kv(41, 2, 4, 2, 256, 128, 10000.0, sink=True)
+    nq = NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.25, sliding_window=32,
+                         obs_window=32, rope_base=10000.0)
+    imp = nq._score_importance(ks[0].float())
+    c = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+    _, mask = nq.compress(c)
+    save("evict_mask_b4", k_in=stack(ks), v_in=stack(vs), importance=imp, mask=mask,
+         k_out=stack(c.key_cache), v_out=stack(c.value_cache))
+
+    # 6. Rate 0.6 K2V2, b = 1, plus boundary protection on 6 layers.
+    ks, vs = synth_kv(51, 6, 1, 2, 128, 128, 10000.0, sink=True)
+    nq = NexusQuantEvict(bits=2, eviction_rate=0.6, sliding_window=16, rope_base=10000.0,
+                         protect_boundary=2)
+    c = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+    _, mask = nq.compress(c)
+    save("evict_mask_boundary", k_in=stack(ks), v_in=stack(vs), mask=mask,
+         k_out=stack(c.key_cache), v_out=stack(c.value_cache))
+
+    # 7. Truncation (b = 1) at two rates.
+    for rate in (0.25, 0.6):
+        ks, vs = synth_kv(61, 2, 1, 2, 256, 128, 10000.0, sink=True)
+        nq = NexusQuantEvictTruncate(key_bits=3, value_bits=2, eviction_rate=rate,
+                                     sliding_window=32, rope_base=10000.0)
+        c = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+        _, n_kept = nq.compress(c)
+        save(f"evict_truncate_r{int(rate * 100)}", k_in=stack(ks), v_in=stack(vs),
+             n_kept=n_kept, k_out=stack(c.key_cache), v_out=stack(c.value_cache))
+
+    # 8. Real-attention scorer through transformers' eager attention (tiny Llama).
+    real_scorer_fixture()
+
+
+def real_scorer_fixture():
+    from transformers import LlamaConfig, LlamaForCausalLM
+    import transformers.models.llama.modeling_llama as ml
+
+    torch.manual_seed(71)
+    cfg = LlamaConfig(vocab_size=128, hidden_size=256, intermediate_size=512,
+                      num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                      max_position_embeddings=512, rope_theta=10000.0)
+    cfg._attn_implementation = "eager"
+    model = LlamaForCausalLM(cfg).eval()
+    captured = []
+    orig = ml.eager_attention_forward
+
+    def spy(module, query, key, value, attention_mask, scaling, dropout=0.0, **kw):
+        captured.append((query.detach().clone(), key.detach().clone(), float(scaling)))
+        return orig(module, query, key, value, attention_mask, scaling, dropout, **kw)
+
+    ml.eager_attention_forward = spy
+    try:
+        ids = torch.randint(0, 128, (1, 96), generator=torch.Generator().manual_seed(72))
+        nq = NexusQuantEvict(scorer="real")
+        imp = nq._score_importance_real(model, ids)
+    finally:
+        ml.eager_attention_forward = orig
+    qs = torch.stack([q for q, _, _ in captured])
+    kss = torch.stack([k for _, k, _ in captured])
+    save("real_scorer", q=qs, k=kss, scaling=captured[0][2], importance=imp)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,205 @@
+"""Pin the Tier-B C oracle (the kernel spec) and the packed-code format.
+
+The spec fixes the arithmetic order the HIP kernel follows.  It is pinned by
+the reference's known answers, by brute force on the E8 decision, by closed
+form invariants, and against the reference fixtures within the parity
+tolerance (codes agree except at near ties; reconstructions to 1e-3 rel L2).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codes as C
+from oracle import spec as S
+from oracle import torch_ref as T
+
+KATS = [  # (x, expected clamped p, levels)  -- derived from e8_lattice.py:27-69
+    ((0.6, 0, 0, 0, 0, 0, 0, 0), (1, 1, 0, 0, 0, 0, 0, 0), 8),
+    ((0.6, 0.6, 0, 0, 0, 0, 0, 0), (1, 1, 0, 0, 0, 0, 0, 0), 8),
+    ((4, 0.7, 0.7, 0.7, 0, 0, 0, 0), (4, 1, 1, 1, 0, 0, 0, 0), 8),
+    ((-4, 0.7, 0.7, 0.7, 0, 0, 0, 0), (-3, 1, 1, 1, 0, 0, 0, 0), 8),
+    ((0.4,) * 8, (0.5,) * 8, 8),
+    ((0.4,) * 7 + (-0.4,), (0.5,) * 7 + (-0.5,), 8),
+    ((0.5, 0, 0, 0, 0, 0, 0, 0), (0,) * 8, 8),
+    ((1.5, 0, 0, 0, 0, 0, 0, 0), (2, 0, 0, 0, 0, 0, 0, 0), 8),
+    ((0,) * 8, (0,) * 8, 8),
+    ((2, 0.7, 0.7, 0.7, 0, 0, 0, 0), (2, 1, 1, 1, 0, 0, 0, 0), 4),
+    ((-2, 0.7, 0.7, 0.7, 0, 0, 0, 0), (-1, 1, 1, 1, 0, 0, 0, 0), 4),
+]
+
+
+@pytest.mark.parametrize("x,want,L", KATS)
+def test_known_answers_spec_and_torch(x, want, L):
+    p, _, _ = S.e8_groups(np.array([x], np.float32), L)
+    assert p[0].tolist() == [float(w) for w in want]
+    pt = T.e8_nearest_point(torch.tensor([x], dtype=torch.float32)).clamp(-L / 2, L / 2)
+    assert pt[0].tolist() == [float(w) for w in want]
+
+
+def _textbook_e8(x):
+    """Conway-Sloane nearest E8 point (flip the LARGEST gap, parity-fix both cosets)."""
+    def fix(c, xx):
+        if int(round(c.sum() * (2 if abs(c[0] - round(c[0])) > 0.25 else 1))) % 2:
+            j = np.argmax(np.abs(xx - c))
+            c = c.copy()
+            c[j] += 1.0 if xx[j] > c[j] else -1.0
+        return c
+    r = fix(np.round(x), x)
+    h = np.floor(x) + 0.5
+    if int(h.sum()) % 2:
+        j = np.argmax(np.abs(x - h))
+        h[j] += 1.0 if x[j] > h[j] else -1.0
+    return h if ((x - h) ** 2).sum() < ((x - r) ** 2).sum() else r
+
+
+def test_known_answers_reject_textbook_e8():
+    # A plausible mistake (textbook E8) must fail the known answers the reference fixes.
+    failed = 0
+    for x, want, L in KATS:
+        p = np.clip(_textbook_e8(np.array(x, np.float64)), -L / 2, L / 2)
+        failed += int(p.tolist() != [float(w) for w in want])
+    assert failed >= 3
+
+
+def test_e8_spec_matches_reference_fixture_except_near_ties(golden):
+    g = golden("e8_nearest")
+    p, _, margin = S.e8_groups(g["x"], 64)          # L=64: no clamping in range
+    diff = (p != g["p"]).any(axis=1)
+    assert diff.mean() < 1e-4
+    assert np.all(margin[diff] < 1e-6)
+
+
+def test_e8_decision_by_brute_force():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((20000, 8)) * 1.3).astype(np.float32)
+    p, coset, margin = S.e8_groups(x, 64)
+    xd = x.astype(np.float64)
+    r = np.rint(xd)
+    odd = (r.sum(1) % 2) != 0
+    gap = np.abs(xd - r)
+    i = np.argmin(gap, axis=1)
+    rr = r.copy()
+    step = np.where((xd - r)[np.arange(len(x)), i] >= 0, 1.0, -1.0)
+    rr[np.arange(len(x))[odd], i[odd]] += step[odd]
+    h = np.rint(xd - 0.5) + 0.5
+    dr = ((xd - rr) ** 2).sum(1)
+    dh = ((xd - h) ** 2).sum(1)
+    want = np.where((dh < dr)[:, None], h, rr)
+    bad = (want != p).any(1)
+    assert np.all(np.abs(dh - dr)[bad] < 1e-6)
+    assert np.array_equal(coset[~bad].astype(bool), (dh < dr)[~bad])
+
+
+def test_quantizer_invariants():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((4096, 128)).astype(np.float32)
+    x[7] = 0.0
+    for L in (2, 4, 8, 16):
+        o = S.quant_rows(x, L)
+        p, xn = o["p"], o["xn"]
+        assert np.all(np.abs(p) <= L / 2)
+        assert np.all((p * 2) == np.round(p * 2))
+        # exactly one coordinate per non-zero row sits at |xn| == L/2
+        hits = (np.abs(xn) == L / 2).sum(1)
+        nz = np.abs(x).max(1) > 0
+        assert np.all(hits[nz] >= 1)
+        assert np.all(p[7] == 0) and o["scale"][7] == np.float32(1e-8) / (L / 2)
+        # symbols decode back to the lattice points
+        assert np.array_equal(C.decode_points(o["sym"], o["coset"], L), p)
+        assert o["sym"].max() <= L
+
+
+def test_markstein_division_is_correctly_rounded():
+    rng = np.random.default_rng(5)
+    s = np.exp(rng.uniform(-30, 30, 500000)).astype(np.float32)
+    z = (rng.uniform(-1, 1, 500000) * s * 4).astype(np.float32)
+    assert S.markstein_mismatches(z, s) == 0
+    s2 = (np.float32(1e-8) / 4) * np.ones(1000, np.float32)
+    z2 = rng.standard_normal(1000).astype(np.float32) * np.float32(1e-8)
+    assert S.markstein_mismatches(z2, s2) == 0
+
+
+def test_fp16_rounding_matches_numpy():
+    rng = np.random.default_rng(6)
+    v = np.concatenate([rng.standard_normal(20000) * 300, rng.standard_normal(20000) * 1e-6,
+                        [65504.0, 65519.0, 65520.0, 1e9, 2.0 ** -25, 1.5 * 2.0 ** -24]]).astype(np.float32)
+    ours = np.array([S.lib().nqs_f32_to_f16(float(t)) for t in v], np.uint16)
+    assert np.array_equal(ours, v.astype(np.float16).view(np.uint16))
+
+
+def _spec_layer(k, v, base, kl, vl):
+    """Spec reconstruction of one layer [b, h, s, d] (positions 0..s-1)."""
+    b, h, s, d = k.shape
+    cs, sn = T.rope_cos_sin(torch.arange(s, dtype=torch.float32), d, base)
+    cos = np.tile(cs.numpy(), (b * h, 1))
+    sin = np.tile(sn.numpy(), (b * h, 1))
+    ok = S.quant_rows(k.reshape(-1, d), kl, cos_in=cos, sin_in=sin, cos_out=cos, sin_out=sin,
+                      margins=True)
+    ov = S.quant_rows(v.reshape(-1, d), vl, margins=True)
+    return ok, ov
+
+
+def _row_agree_rel_l2(got, ref, row_ok):
+    g = got.astype(np.float32)[row_ok]
+    r = ref.astype(np.float32)[row_ok]
+    return float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30))
+
+
+@pytest.mark.parametrize("tag", ["b1e4", "b5e5"])
+def test_spec_within_tolerance_of_reference_fixture(golden, tag):
+    g = golden(f"quant_only_{tag}")
+    base = float(g["base"])
+    for li in range(g["k_in"].shape[0]):
+        k = g["k_in"][li].astype(np.float32)
+        v = g["v_in"][li].astype(np.float32)
+        ok, ov = _spec_layer(k, v, base, 8, 4)
+        for o, ref, L, is_key in ((ok, g["k_k3v2"][li], 8, True), (ov, g["v_k3v2"][li], 4, False)):
+            d = ref.shape[-1]
+            ref2 = ref.reshape(-1, d)
+            # reference lattice points for the code comparison
+            x = torch.from_numpy((k if is_key else v).reshape(g["k_in"].shape[1:]))
+            if is_key:
+                x = T.inverse_rope(x.float()[0], base=base).reshape(-1, d)
+            else:
+                x = x.float().reshape(-1, d)
+            rot = torch.einsum('nd,de->ne', x, T.hadamard_matrix(d))
+            p_ref, _ = T.e8_quantize_perhead_parts(rot, L)
+            mism = (p_ref.numpy().reshape(-1, 8) != o["p"].reshape(-1, 8)).any(1)
+            assert mism.mean() <= 1e-4
+            assert np.all(o["margin"].reshape(-1)[mism] < 1e-5)
+            row_ok = ~mism.reshape(ref2.shape[0], -1).any(1)
+            assert _row_agree_rel_l2(o["recon"], ref2, row_ok) <= 1e-3
+
+
+def test_symbol_packing_roundtrip():
+    rng = np.random.default_rng(7)
+    for L in (2, 4, 8, 16):
+        for D in (64, 128, 256):
+            sym = rng.integers(0, L + 1, size=(33, D)).astype(np.uint8)
+            packed = C.pack_symbols(sym, L)
+            assert packed.shape == (33, D // 8 * C.bits_for(L))
+            assert np.array_equal(C.unpack_symbols(packed, L, D), sym)
+            cs = rng.integers(0, 2, size=(33, D // 8)).astype(np.uint8)
+            assert np.array_equal(C.unpack_cosets(C.pack_cosets(cs), D // 8), cs)
+
+
+def test_codes_2p_match_vllm_convention():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((512, 128)).astype(np.float32)
+    for L in (4, 8):
+        o = S.quant_rows(x, L)
+        two_p = C.codes_2p(o["sym"], o["coset"], L)
+        want = T.lattice_codes_2p(torch.from_numpy(o["p"])).numpy()
+        assert np.array_equal(two_p, want)
+
+
+def test_delta_stream_roundtrip():
+    rng = np.random.default_rng(9)
+    codes = rng.integers(-8, 9, size=(6, 300, 128)).astype(np.int8)
+    d = C.delta_tokens(codes)
+    assert np.array_equal(d[:, 0], codes[:, 0])
+    assert np.array_equal(C.undelta_tokens(d), codes)
+    dt = T.delta_encode(torch.from_numpy(codes)).numpy()
+    assert np.array_equal(dt, d)
+    assert np.array_equal(T.delta_decode(torch.from_numpy(d)).numpy(), codes)
