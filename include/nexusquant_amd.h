@@ -1,0 +1,95 @@
+/*
+ * nexusquant_amd -- C ABI of the MI355X (gfx950) KV-cache compression library.
+ *
+ * Every entry point is asynchronous on the HIP stream it is given, borrows the
+ * device pointers it is passed (no ownership transfer), allocates nothing, and
+ * returns 0 on success or a negative NQ_E* code; nq_last_error() then holds a
+ * message for the calling thread.  Tensors are row-major and contiguous.
+ *
+ * The reference (jagmarques/nexusquant v0.5.0) is pure Python/PyTorch; these
+ * entry points replace the torch operator sequences cited on each declaration.
+ */
+#ifndef NEXUSQUANT_AMD_H
+#define NEXUSQUANT_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NQ_ABI_VERSION 1
+
+/* status codes */
+#define NQ_OK 0
+#define NQ_EINVAL -1      /* bad argument (shape, levels, pointer) */
+#define NQ_EUNSUPPORTED -2 /* valid request this build does not implement */
+#define NQ_EHIP -3        /* HIP runtime error (launch, device) */
+
+/* element types of input tensors */
+#define NQ_F16 0
+#define NQ_BF16 1
+#define NQ_F32 2
+
+/*
+ * One fused quantizer launch over n_tensors tensors of identical geometry
+ * [batch, heads, seq_in, head_dim] and identical role (keys or values).
+ *
+ * Per row (one head vector of one token): optional inverse RoPE at the row's
+ * source position, zero-pad to the next power of two D, Walsh-Hadamard, per-row
+ * amax scale, relaxed-E8 nearest point at `levels` (2, 4, 8, 16), clamp; then
+ * write any of
+ *   recon  [batch, heads, seq_out, head_dim] fp16: inverse Hadamard, rescale,
+ *          forward RoPE at the output position (the reference's drop-in output);
+ *   syms   [batch, heads, seq_out, D/8 * bits] packed symbols (bits = 2,3,4,5
+ *          for levels 2,4,8,16);
+ *   cosets [batch, heads, seq_out, D/64] coset bitmaps;
+ *   scales [batch, heads, seq_out] fp32 row scales.
+ * Row selection: output row t of batch b reads source token gather[b*seq_out+t]
+ * (truncation) or token t (gather == NULL, then seq_out == seq_in); rows whose
+ * keep[b*seq_in + src] == 0 are zeroed before quantization (mask eviction).
+ * RoPE tables are fp32 [rope_n_pos, head_dim/2]; keys use row position
+ * src (inverse) and t (forward).
+ *
+ * Replaces: NexusQuantQuantOnly.compress            pipeline.py:232-265
+ *           NexusQuantEvict.compress (hard path)     pipeline.py:1190-1242
+ *           NexusQuantEvictTruncate.compress (loop)  pipeline.py:1343-1397
+ *           E8Lattice.quantize_perhead / nearest_point  e8_lattice.py:27-124
+ *           inverse_rope / forward_rope (+_at_positions) rope_utils.py:75-249
+ *           the dense Hadamard einsums               pipeline.py:250,253,258,261
+ *           VLLM code format (int8 2p + scale)       vllm_backend.py:267-338
+ */
+typedef struct nq_quant_desc {
+    int32_t n_tensors;
+    int32_t batch, heads, seq_in, seq_out, head_dim;
+    int32_t dtype;          /* NQ_F16 / NQ_BF16 / NQ_F32 */
+    int32_t levels;         /* 2, 4, 8 or 16 */
+    int32_t is_key;         /* 1: inverse/forward RoPE around the quantizer */
+    int32_t reserved;
+    /* device arrays of n_tensors base addresses (uint64); recon/syms/cosets/
+     * scales arrays may be NULL to skip that output */
+    const uint64_t* src;
+    const uint64_t* recon;
+    const uint64_t* syms;
+    const uint64_t* cosets;
+    const uint64_t* scales;
+    const int32_t* gather;  /* device [batch * seq_out] or NULL */
+    const uint8_t* keep;    /* device [batch * seq_in] or NULL */
+    const float* rope_cos;  /* device [rope_n_pos, head_dim/2] (keys) */
+    const float* rope_sin;
+    int64_t rope_n_pos;
+    float hadamard_scale;   /* h_D of the reference's Sylvester matrix */
+    float reserved_f;
+} nq_quant_desc;
+
+int nq_quantize(const nq_quant_desc* desc, void* stream);
+
+/* Library version and the last error message of the calling thread. */
+int nq_abi_version(void);
+const char* nq_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEXUSQUANT_AMD_H */

@@ -1,0 +1,98 @@
+"""ctypes binding of the gfx950 library (nexusquant_amd/lib/libnqamd.so).
+
+The library is the only compute path: when it is missing, or the tensors are
+not on a ROCm device, every entry point raises instead of falling back.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from .build import LIB_PATH
+
+NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
+_P = ctypes.c_void_p
+
+
+class QuantDesc(ctypes.Structure):
+    """Mirror of nq_quant_desc in include/nexusquant_amd.h."""
+    _fields_ = [
+        ("n_tensors", ctypes.c_int32),
+        ("batch", ctypes.c_int32), ("heads", ctypes.c_int32), ("seq_in", ctypes.c_int32),
+        ("seq_out", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32), ("levels", ctypes.c_int32), ("is_key", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("src", _P), ("recon", _P), ("syms", _P), ("cosets", _P), ("scales", _P),
+        ("gather", _P), ("keep", _P), ("rope_cos", _P), ("rope_sin", _P),
+        ("rope_n_pos", ctypes.c_int64),
+        ("hadamard_scale", ctypes.c_float), ("reserved_f", ctypes.c_float),
+    ]
+
+
+# Every exported symbol, with (argtypes, restype).  tests/test_abi.py checks
+# that this list and include/nexusquant_amd.h agree and that the library
+# exports all of them.
+SIGNATURES = {
+    "nq_abi_version": ([], ctypes.c_int),
+    "nq_last_error": ([], ctypes.c_char_p),
+    "nq_quantize": ([ctypes.POINTER(QuantDesc), _P], ctypes.c_int),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NexusQuantError(RuntimeError):
+    pass
+
+
+def load():
+    """Load the library (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise NexusQuantError(
+                    f"nexusquant_amd HIP library not found at {LIB_PATH}; build it with "
+                    "`python -m nexusquant_amd.build` (hipcc, gfx950)")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (args, res) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = args
+                fn.restype = res
+            _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().nq_last_error().decode(errors="replace")
+        if status == -1:
+            raise ValueError(f"{what}: {msg}")
+        raise NexusQuantError(f"{what} failed ({status}): {msg}")
+
+
+def dtype_code(dtype) -> int:
+    import torch
+    if dtype == torch.float16:
+        return NQ_F16
+    if dtype == torch.bfloat16:
+        return NQ_BF16
+    if dtype == torch.float32:
+        return NQ_F32
+    raise TypeError(f"unsupported KV dtype {dtype}; expected float16, bfloat16 or float32")
+
+
+def current_stream_handle(device) -> int:
+    import torch
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(t, what: str = "tensor") -> None:
+    if not t.is_cuda:
+        raise NexusQuantError(
+            f"nexusquant_amd runs on MI355X (ROCm) devices only; {what} is on {t.device}")

@@ -1,0 +1,154 @@
+"""Tensor-level wrappers of the gfx950 kernels (device tensors in, device tensors out)."""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from .hadamard import hadamard_constant, next_power_of_2
+from .rope import device_table
+
+SYM_BITS = {2: 2, 4: 3, 8: 4, 16: 5}
+
+
+@dataclass
+class PackedCodes:
+    """Lossless packed relaxed-E8 codes of one [batch, heads, seq, head_dim] tensor.
+
+    syms   uint8 [batch, heads, seq, D/8 * bits]  (bits = 2,3,4,5 for levels 2,4,8,16)
+    cosets uint8 [batch, heads, seq, D/64]        (bit g: group g is a half-integer point)
+    scales fp32  [batch, heads, seq]
+    D is head_dim padded to a power of two.  Slot k of a row's symbol bytes holds
+    group 4*(k mod D/32) + (k div D/32); symbol j of a group sits at bit j*bits.
+    """
+    syms: torch.Tensor
+    cosets: torch.Tensor
+    scales: torch.Tensor
+    levels: int
+    head_dim: int
+    padded_dim: int
+    is_key: bool
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.syms, self.cosets, self.scales))
+
+
+def _ptr_arrays(groups: Sequence[Optional[Sequence[torch.Tensor]]], device) -> List[Optional[torch.Tensor]]:
+    """Device int64 arrays of base addresses, staged through one pinned buffer and
+    one asynchronous copy (a pageable copy would block the host behind the
+    previous kernel on the stream)."""
+    flat = []
+    spans = []
+    for g in groups:
+        if g is None:
+            spans.append(None)
+            continue
+        spans.append((len(flat), len(g)))
+        flat.extend(t.data_ptr() for t in g)
+    if not flat:
+        return [None for _ in groups]
+    host = torch.tensor(flat, dtype=torch.int64).pin_memory()
+    dev = host.to(device, non_blocking=True)
+    return [None if sp is None else dev[sp[0]:sp[0] + sp[1]] for sp in spans]
+
+
+def _addr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: int,
+                     rope_base: float = 10000.0, rope_scaling: Optional[dict] = None,
+                     gather: Optional[torch.Tensor] = None, keep: Optional[torch.Tensor] = None,
+                     recon: bool = True, codes: bool = False, launch_events=None,
+                     ) -> Tuple[Optional[List[torch.Tensor]], Optional[List[PackedCodes]]]:
+    """Run the fused quantizer over same-shaped [b, h, s, d] tensors in one launch.
+
+    gather: int32/int64 [b, seq_out] source token per output row (truncation).
+    keep:   bool/uint8 [b, seq_in]; rows with keep == 0 are zeroed (mask eviction).
+    launch_events: optional (start, end) torch.cuda.Event pair recorded on the
+    launch stream immediately around the kernel launch.
+    Returns (fp16 reconstructions or None, PackedCodes or None), one per tensor.
+    """
+    lib = _lib.load()
+    if not tensors:
+        return ([] if recon else None), ([] if codes else None)
+    t0 = tensors[0]
+    _lib.require_device(t0, "KV tensor")
+    if t0.dim() != 4:
+        raise ValueError(f"expected [batch, heads, seq, head_dim] tensors, got shape {tuple(t0.shape)}")
+    b, h, s, d = t0.shape
+    for t in tensors:
+        if t.shape != t0.shape or t.dtype != t0.dtype or t.device != t0.device:
+            raise ValueError("all tensors of one launch must share shape, dtype and device")
+    if levels not in SYM_BITS:
+        raise ValueError(f"levels must be 2, 4, 8 or 16, got {levels}")
+    D = next_power_of_2(d)
+    if D != d or d not in (64, 128, 256):
+        raise NotImplementedError(f"head_dim {d} is not supported by the fused kernel yet")
+    dev = t0.device
+    # contiguous and 16-byte aligned (the kernel reads 16-byte vectors)
+    src = [t.contiguous() for t in tensors]
+    src = [t if t.data_ptr() % 16 == 0 else t.clone() for t in src]
+    seq_out = s
+    g = None
+    if gather is not None:
+        g = gather.to(device=dev, dtype=torch.int32).contiguous()
+        if g.dim() == 1:
+            g = g.unsqueeze(0).expand(b, -1).contiguous()
+        if g.shape[0] != b:
+            raise ValueError(f"gather must be [batch, seq_out], got {tuple(g.shape)}")
+        seq_out = g.shape[1]
+        if g.numel() and (int(g.min()) < 0 or int(g.max()) >= s):
+            raise ValueError(f"gather indices must lie in [0, {s})")
+    k = None
+    if keep is not None:
+        k = keep.to(device=dev, dtype=torch.uint8).contiguous()
+        if tuple(k.shape) != (b, s):
+            raise ValueError(f"keep must be [batch, seq] = {(b, s)}, got {tuple(k.shape)}")
+
+    n = len(src)
+    recon_t = [torch.empty(b, h, seq_out, d, dtype=torch.float16, device=dev) for _ in range(n)] if recon else None
+    codes_t = None
+    if codes:
+        codes_t = [PackedCodes(
+            syms=torch.empty(b, h, seq_out, D // 8 * SYM_BITS[levels], dtype=torch.uint8, device=dev),
+            cosets=torch.empty(b, h, seq_out, D // 64, dtype=torch.uint8, device=dev),
+            scales=torch.empty(b, h, seq_out, dtype=torch.float32, device=dev),
+            levels=levels, head_dim=d, padded_dim=D, is_key=is_key) for _ in range(n)]
+
+    cos = sin = None
+    n_pos = 0
+    if is_key:
+        cos, sin = device_table(max(s, seq_out), d, rope_base, rope_scaling, dev)
+        n_pos = cos.shape[0]
+
+    names = ("src", "recon", "syms", "cosets", "scales")
+    groups = [src, recon_t,
+              [c.syms for c in codes_t] if codes_t else None,
+              [c.cosets for c in codes_t] if codes_t else None,
+              [c.scales for c in codes_t] if codes_t else None]
+    arrays = dict(zip(names, _ptr_arrays(groups, dev)))
+    desc = _lib.QuantDesc(
+        n_tensors=n, batch=b, heads=h, seq_in=s, seq_out=seq_out, head_dim=d,
+        dtype=_lib.dtype_code(t0.dtype), levels=levels, is_key=int(is_key),
+        src=_addr(arrays["src"]), recon=_addr(arrays["recon"]), syms=_addr(arrays["syms"]),
+        cosets=_addr(arrays["cosets"]), scales=_addr(arrays["scales"]),
+        gather=_addr(g), keep=_addr(k), rope_cos=_addr(cos), rope_sin=_addr(sin),
+        rope_n_pos=n_pos, hadamard_scale=hadamard_constant(D))
+    with torch.cuda.device(dev):
+        if launch_events is not None:
+            launch_events[0].record()
+        status = lib.nq_quantize(ctypes.byref(desc), ctypes.c_void_p(_lib.current_stream_handle(dev)))
+        if launch_events is not None:
+            launch_events[1].record()
+    _lib.check(status, "nq_quantize")
+    # keep the pointer arrays and inputs alive until the kernel has consumed them
+    stream = torch.cuda.current_stream(dev)
+    for t in list(arrays.values()) + src + [g, k]:
+        if t is not None:
+            t.record_stream(stream)
+    return recon_t, codes_t

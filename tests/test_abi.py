@@ -1,0 +1,56 @@
+"""The C-ABI library builds, loads and exports every symbol include/nexusquant_amd.h declares.
+
+No compute call is made here (no GPU in the build container).
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+
+from nexusquant_amd import _lib
+from nexusquant_amd.build import LIB_PATH
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nexusquant_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_is_built_in_tree():
+    assert os.path.exists(LIB_PATH), "run python -m nexusquant_amd.build"
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = ctypes.CDLL(LIB_PATH)
+    names = declared_functions()
+    assert names, "header declares no functions"
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert sorted(_lib.SIGNATURES) == names, "ctypes signature table out of sync with the header"
+
+
+def test_struct_layout_matches_the_c_compiler(tmp_path):
+    """ctypes offsets of every descriptor field equal gcc's offsetof on the header."""
+    fields = [f[0] for f in _lib.QuantDesc._fields_]
+    prog = ["#include <stddef.h>", "#include <stdio.h>", f'#include "{HEADER}"', "int main(void){",
+            'printf("%zu\\n", sizeof(nq_quant_desc));']
+    prog += [f'printf("%zu\\n", offsetof(nq_quant_desc, {f}));' for f in fields]
+    prog += ["return 0;}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(prog))
+    exe = tmp_path / "layout"
+    subprocess.check_call(["gcc", "-o", str(exe), str(src)])
+    out = [int(x) for x in subprocess.check_output([str(exe)]).split()]
+    assert out[0] == ctypes.sizeof(_lib.QuantDesc)
+    assert out[1:] == [getattr(_lib.QuantDesc, f).offset for f in fields]
+
+
+def test_abi_version_and_error_calls_need_no_gpu():
+    lib = _lib.load()
+    assert lib.nq_abi_version() == 1
+    assert isinstance(lib.nq_last_error(), bytes)
