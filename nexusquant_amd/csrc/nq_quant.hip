@@ -30,6 +30,7 @@ struct QuantArgs {
     const float* rope_cos;
     const float* rope_sin;
     uint32_t heads, seq_in, seq_out, rows;
+    uint32_t n_tensors, bh, work, per_xcd;  // work items = ceil(seq_out/64) * bh * n_tensors
     float hscale;
 };
 
@@ -73,10 +74,30 @@ __device__ __forceinline__ void load8f(const float* p, float* out) {
 
 // ------------------------------------------------------------ Hadamard ----
 
+typedef __fp16 half2v __attribute__((ext_vector_type(2)));
+
+// Quad butterfly v <- v + c * partner(v) with the partner read through DPP in
+// the same v_fmac_f32 instruction.  The DPP read of a VGPR needs two wait
+// states after the VALU write that produced it; s_nop 1 provides them for the
+// first instruction, and the other seven read registers written before it.
+#define NQ_FMAC_DPP8(PERM, x, c)                                                       \
+    asm("s_nop 1\n\t"                                                                  \
+        "v_fmac_f32_dpp %0, %0, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+        "v_fmac_f32_dpp %1, %1, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+        "v_fmac_f32_dpp %2, %2, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+        "v_fmac_f32_dpp %3, %3, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+        "v_fmac_f32_dpp %4, %4, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+        "v_fmac_f32_dpp %5, %5, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+        "v_fmac_f32_dpp %6, %6, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+        "v_fmac_f32_dpp %7, %7, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1"     \
+        : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),       \
+          "+v"(x[6]), "+v"(x[7])                                                       \
+        : "v"(c))
+
 // Unnormalised Walsh-Hadamard over the quad's row.  Stage order follows
 // coordinate bits 0,1,2 (in chunk), 3,4 (across the quad), 5.. (across chunks).
-// The quad stages use v + c * partner with c = +-1 chosen per lane, which is
-// the exact butterfly up to a sign; every lane's values end multiplied by
+// The quad stages compute v + c * partner with c = +-1 per lane, the exact
+// butterfly up to a sign; every lane's values end multiplied by
 // sigma(q) = (-1)^popcount(q), which the caller folds into the next multiply.
 template <int C>
 __device__ __forceinline__ void fwht_row(float (&x)[C][8], int q) {
@@ -96,15 +117,9 @@ __device__ __forceinline__ void fwht_row(float (&x)[C][8], int q) {
     const float s3 = (q & 1) ? -1.0f : 1.0f;
     const float s4 = (q & 2) ? -1.0f : 1.0f;
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
+    for (int c = 0; c < C; ++c) NQ_FMAC_DPP8("quad_perm:[1,0,3,2]", x[c], s3);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[c][i] = __builtin_fmaf(s3, dpp_f32<kQuadXor1>(x[c][i]), x[c][i]);
-    }
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[c][i] = __builtin_fmaf(s4, dpp_f32<kQuadXor2>(x[c][i]), x[c][i]);
-    }
+    for (int c = 0; c < C; ++c) NQ_FMAC_DPP8("quad_perm:[2,3,0,1]", x[c], s4);
 #pragma unroll
     for (int len = 1; len < C; len <<= 1) {
 #pragma unroll
@@ -120,6 +135,61 @@ __device__ __forceinline__ void fwht_row(float (&x)[C][8], int q) {
     }
 }
 
+// The same transform on lattice points packed two per register as fp16
+// (coordinates 2k, 2k+1 of a chunk in register k).  Every value stays a
+// multiple of 1/2 of magnitude <= D*L/2 <= 1024, so fp16 holds it exactly and
+// the result equals the fp32 transform in any stage order.  Output carries the
+// same sigma(q) sign.
+template <int C>
+__device__ __forceinline__ void fwht_row_f16(half2v (&h)[C][4], int q) {
+    const half2v pm = {(__fp16)1.0f, (__fp16)-1.0f};
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) h[c][k] = __builtin_elementwise_fma(h[c][k], pm, h[c][k].yx);
+#pragma unroll
+        for (int len = 1; len < 4; len <<= 1) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (k & len) continue;
+                half2v a = h[c][k], b = h[c][k + len];
+                h[c][k] = a + b;
+                h[c][k + len] = a - b;
+            }
+        }
+    }
+    const __fp16 f3 = (q & 1) ? (__fp16)-1.0f : (__fp16)1.0f;
+    const __fp16 f4 = (q & 2) ? (__fp16)-1.0f : (__fp16)1.0f;
+    const half2v s3 = {f3, f3}, s4 = {f4, f4};
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            half2v p = __builtin_bit_cast(half2v, dpp_u32<kQuadXor1>(__builtin_bit_cast(uint32_t, h[c][k])));
+            h[c][k] = __builtin_elementwise_fma(s3, p, h[c][k]);
+        }
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            half2v p = __builtin_bit_cast(half2v, dpp_u32<kQuadXor2>(__builtin_bit_cast(uint32_t, h[c][k])));
+            h[c][k] = __builtin_elementwise_fma(s4, p, h[c][k]);
+        }
+#pragma unroll
+    for (int len = 1; len < C; len <<= 1) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            if (c & len) continue;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                half2v a = h[c][k], b = h[c + len][k];
+                h[c][k] = a + b;
+                h[c + len][k] = a - b;
+            }
+        }
+    }
+}
+
 __device__ __forceinline__ float quad_sign(int q) {
     return ((q ^ (q >> 1)) & 1) ? -1.0f : 1.0f;
 }
@@ -127,7 +197,9 @@ __device__ __forceinline__ float quad_sign(int q) {
 // ------------------------------------------------------------------ E8 ----
 
 // Relaxed E8 (oracle/nq_spec.c nqs_e8_group): returns the coset flag and
-// overwrites x with the clamped lattice point.
+// overwrites x with the clamped lattice point.  The odd-sum step goes to the
+// first coordinate whose |x - r| equals the group minimum, which is the
+// reference's first argmin.
 template <int L>
 __device__ __forceinline__ int e8_group(float (&x)[8]) {
     constexpr float HL = (float)(L / 2);
@@ -141,24 +213,20 @@ __device__ __forceinline__ int e8_group(float (&x)[8]) {
         isum += (int)r[j];
     }
     const bool odd = (isum & 1) != 0;
-    int imin = 0;
-    float amin = a[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) {
-        bool lt = a[j] < amin;
-        amin = lt ? a[j] : amin;
-        imin = lt ? j : imin;
-    }
+    const float amin = __builtin_fminf(__builtin_fminf(__builtin_fminf(a[0], a[1]), __builtin_fminf(a[2], a[3])),
+                                       __builtin_fminf(__builtin_fminf(a[4], a[5]), __builtin_fminf(a[6], a[7])));
     const float asum = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
     const float thr = odd ? (1.0f + 2.0f * amin) : 2.0f;
     const bool use_half = asum > thr;
+    bool pending = odd && !use_half;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        float h = __builtin_rintf(x[j] - 0.5f) + 0.5f;
-        float step = (odd && j == imin) ? (e[j] >= 0.0f ? 1.0f : -1.0f) : 0.0f;
-        float v = use_half ? h : (r[j] + step);
-        v = __builtin_fminf(__builtin_fmaxf(v, -HL), HL);
-        x[j] = v;
+        const float h = __builtin_rintf(x[j] - 0.5f) + 0.5f;
+        const bool hit = pending && (a[j] == amin);
+        pending = pending && !hit;
+        const float rs = r[j] + __builtin_copysignf(1.0f, e[j]);  // e is never -0
+        float v = use_half ? h : (hit ? rs : r[j]);
+        x[j] = __builtin_fminf(__builtin_fmaxf(v, -HL), HL);
     }
     return use_half ? 1 : 0;
 }
@@ -227,13 +295,20 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     constexpr int C = D / 32;
     constexpr int HALF = D / 2;
     const int q = threadIdx.x & 3;
-    const uint32_t tensor = blockIdx.y;
-    const uint32_t row_raw = blockIdx.x * 64u + (threadIdx.x >> 2);
-    const bool active = row_raw < a.rows;
-    const uint32_t row = active ? row_raw : a.rows - 1u;  // idle quads recompute a valid row
-
-    const uint32_t bh = row / a.seq_out;
-    const uint32_t t_out = row - bh * a.seq_out;
+    // Block -> work item.  Consecutive block ids go round-robin to the 8 XCDs, so
+    // block 8k + x takes work item x * per_xcd + k: each XCD walks a contiguous
+    // range.  Work items are ordered (token tile, batch*head, tensor) with the
+    // tensor fastest, so the blocks that read one token tile's RoPE rows run back
+    // to back on one XCD and find them in its L2.  The whole block exits together.
+    const uint32_t w = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
+    if (w >= a.work) return;
+    const uint32_t tensor = w % a.n_tensors;
+    const uint32_t rest = w / a.n_tensors;
+    const uint32_t bh = rest % a.bh;
+    const uint32_t tile = rest / a.bh;
+    const uint32_t t_raw = tile * 64u + (threadIdx.x >> 2);
+    const bool active = t_raw < a.seq_out;
+    const uint32_t t_out = active ? t_raw : a.seq_out - 1u;  // idle quads recompute a valid row
     const uint32_t b = bh / a.heads;
     uint32_t t_in = t_out;
     if (a.gather) {
@@ -328,12 +403,30 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     }
 
     if (!a.recon) return;
-    fwht_row<C>(x, q);  // exact on half-integer lattice points
     const float g = sigma * (a.hscale * scale);
+    constexpr bool EXACT_F16 = D * (L / 2) <= 1024;
+    if constexpr (EXACT_F16) {
+        half2v hp[C][4];
 #pragma unroll
-    for (int c = 0; c < C; ++c)
+        for (int c = 0; c < C; ++c)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[c][i] = x[c][i] * g;
+            for (int k = 0; k < 4; ++k)
+                hp[c][k] = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(x[c][2 * k], x[c][2 * k + 1]));
+        fwht_row_f16<C>(hp, q);
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                x[c][2 * k] = __builtin_fmaf((float)hp[c][k].x, g, 0.0f);
+                x[c][2 * k + 1] = __builtin_fmaf((float)hp[c][k].y, g, 0.0f);
+            }
+    } else {
+        fwht_row<C>(x, q);  // exact on half-integer lattice points
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[c][i] = x[c][i] * g;
+    }
 
     if constexpr (IS_KEY) {
         if (a.gather && t_out != t_in) {
@@ -350,21 +443,32 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 float lo = x[c][i], hi = x[c + C / 2][i];
-                x[c][i] = lo * cs[c][i] - hi * sn[c][i];
-                x[c + C / 2][i] = lo * sn[c][i] + hi * cs[c][i];
+                x[c][i] = __builtin_fmaf(lo, cs[c][i], -(hi * sn[c][i]));
+                x[c + C / 2][i] = __builtin_fmaf(lo, sn[c][i], hi * cs[c][i]);
             }
         }
     }
     if (!active) return;
-    uint16_t* dst = reinterpret_cast<uint16_t*>(a.recon[tensor]) + out_row * D;
+    half2v* dst = reinterpret_cast<half2v*>(reinterpret_cast<uint16_t*>(a.recon[tensor]) + out_row * D);
+    // The fp32 result is rounded to fp16 in a second step, as the reference does
+    // (fp32 tensor, then .half()).  The empty asm pins the fp32 value: without it
+    // the backend folds fma + convert into v_fma_mix{lo,hi}_f16, which rounds
+    // the exact product-sum to fp16 once and differs at fp16 rounding ties.
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) asm("" : "+v"(x[c][i]));
 #pragma unroll
     for (int c = 0; c < C; ++c) {
+        half2v o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = half2v{(__fp16)x[c][2 * k], (__fp16)x[c][2 * k + 1]};
         uint4 w;
-        w.x = f32_to_f16_bits(x[c][0]) | (f32_to_f16_bits(x[c][1]) << 16);
-        w.y = f32_to_f16_bits(x[c][2]) | (f32_to_f16_bits(x[c][3]) << 16);
-        w.z = f32_to_f16_bits(x[c][4]) | (f32_to_f16_bits(x[c][5]) << 16);
-        w.w = f32_to_f16_bits(x[c][6]) | (f32_to_f16_bits(x[c][7]) << 16);
-        *reinterpret_cast<uint4*>(dst + 32 * c + 8 * q) = w;
+        w.x = __builtin_bit_cast(uint32_t, o[0]);
+        w.y = __builtin_bit_cast(uint32_t, o[1]);
+        w.z = __builtin_bit_cast(uint32_t, o[2]);
+        w.w = __builtin_bit_cast(uint32_t, o[3]);
+        *reinterpret_cast<uint4*>(dst + (32 * c + 8 * q) / 2) = w;
     }
 }
 
@@ -372,7 +476,8 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
 
 template <int D, int L, bool K, int DT>
 static hipError_t launch_quant(const QuantArgs& a, uint32_t n_tensors, hipStream_t s) {
-    dim3 grid((a.rows + 63u) / 64u, n_tensors);
+    (void)n_tensors;
+    dim3 grid(a.per_xcd * 8u);
     hipLaunchKernelGGL((quant_rows_kernel<D, L, K, DT>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
@@ -443,6 +548,13 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     a.seq_out = (uint32_t)d->seq_out;
     a.rows = (uint32_t)rows;
     a.hscale = d->hadamard_scale;
+    a.n_tensors = (uint32_t)d->n_tensors;
+    a.bh = (uint32_t)d->batch * (uint32_t)d->heads;
+    const uint64_t work = (uint64_t)((d->seq_out + 63) / 64) * a.bh * a.n_tensors;
+    NQ_CHECK_ARG(work < (1ull << 32) - 8, "nq_quantize: %llu work items exceed the grid limit",
+                 (unsigned long long)work);
+    a.work = (uint32_t)work;
+    a.per_xcd = (uint32_t)((work + 7) / 8);
     hipStream_t s = (hipStream_t)stream;
     hipError_t e;
     switch (d->head_dim) {

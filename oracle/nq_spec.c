@@ -31,8 +31,10 @@
  *  6. Clamp to [-L/2, L/2] after the choice (e8_lattice.py:120).
  *  7. Reconstruction: w = S * p is exact in fp32 for every order (p is a
  *     half-integer of magnitude <= 8), then recon = w * fl(h_D * scale),
- *     forward RoPE as the reference (lo*c - hi*s ; lo*s + hi*c), keep the first
- *     d outputs, round to fp16 (round to nearest even).
+ *     forward RoPE lo' = fma(lo, c, -fl(hi*s)), hi' = fma(lo, s, fl(hi*c)) (the
+ *     reference rounds lo*c separately; the difference is below fp16
+ *     resolution except at fp16 rounding ties), keep the first d outputs,
+ *     round to fp16 (round to nearest even).
  *
  * Code symbols: the group's coset bit is 1 when the half-integer candidate was
  * chosen.  Integer coset: sym = p + L/2.  Half coset: the clamp folds one edge
@@ -264,13 +266,14 @@ void nqs_quant_rows(int64_t n, int d, int D, int L, float hD,
                 const float* c = cos_out + row * half;
                 const float* s = sin_out + row * half;
                 for (int i = 0; i < half; ++i) {
+                    /* output side: one fused multiply-add per coordinate; the result
+                     * is rounded to fp16 next, which hides the fp32 difference from
+                     * the reference's separate products except at fp16 ties */
                     float lo = w[i], hi = w[i + half];
-                    float t1 = lo * c[i];
                     float t2 = hi * s[i];
-                    float t3 = lo * s[i];
                     float t4 = hi * c[i];
-                    out[i] = nqs_f32_to_f16(t1 - t2);
-                    out[i + half] = nqs_f32_to_f16(t3 + t4);
+                    out[i] = nqs_f32_to_f16(fmaf(lo, c[i], -t2));
+                    out[i + half] = nqs_f32_to_f16(fmaf(lo, s[i], t4));
                 }
             } else {
                 for (int i = 0; i < d; ++i) out[i] = nqs_f32_to_f16(w[i]);
