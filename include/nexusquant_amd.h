@@ -84,6 +84,67 @@ typedef struct nq_quant_desc {
 
 int nq_quantize(const nq_quant_desc* desc, void* stream);
 
+/*
+ * Key-key importance (SnapKV-style proxy): keys [batch, heads, seq, head_dim]
+ * (dtype NQ_F16/NQ_BF16/NQ_F32, head_dim 64/96/128/256); queries are the last
+ * min(obs_window, seq) <= 32 keys; importance[batch, seq] = mean over heads of
+ * the per-key sum over queries of softmax(q . k * scale) over all keys.
+ * scale is the reference's fp32 d**-0.5.  workspace: device buffer of at least
+ * nq_score_keykey_workspace(batch, heads, seq) bytes (caller owned).
+ *
+ * Replaces: NexusQuantEvict._score_importance          pipeline.py:756-782
+ */
+int64_t nq_score_keykey_workspace(int32_t batch, int32_t heads, int32_t seq);
+int nq_score_keykey(const void* keys, int32_t dtype, int32_t batch, int32_t heads, int32_t seq,
+                    int32_t head_dim, int32_t obs_window, float scale, float* importance, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/*
+ * Real-attention importance of one layer, accumulated: importance[b, j] +=
+ * mean over q_heads of sum_{i >= j} p[b, h, i, j], with
+ * p = round(softmax_fp32(round(round(q . k) * scaling))) under the causal
+ * mask, round = rounding to the model dtype (fp16/bf16; none for fp32) as
+ * transformers' eager attention does; query head h reads key head
+ * h / (q_heads / kv_heads).  q [batch, q_heads, seq, head_dim],
+ * k [batch, kv_heads, seq, head_dim], both post-RoPE.  workspace: at least
+ * nq_score_real_workspace(batch, q_heads, seq) bytes (caller owned).
+ *
+ * Replaces: NexusQuantEvict._score_importance_real   pipeline.py:784-836
+ *           (eager_attention_forward + repeat_kv, transformers 5.15.0
+ *            models/llama/modeling_llama.py:179-213)
+ */
+int64_t nq_score_real_workspace(int32_t batch, int32_t q_heads, int32_t seq);
+int nq_score_real(const void* q, const void* k, int32_t dtype, int32_t batch, int32_t q_heads,
+                  int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, float* importance,
+                  void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Keep mask from importance[batch, seq] (fp32): position 0, the last
+ * sliding_window positions, the k most important positions of [1, prefix)
+ * (ties at the k-th value keep the lowest positions), and protected_pos.
+ * prefix = max(seq - sliding_window, 0) and k = min(n_keep, prefix - 1) are
+ * computed by the caller exactly as the reference does (Python double).
+ * Writes keep[batch, seq] (0/1), kept_idx[batch, seq] (ascending kept
+ * positions, first n_kept[b] entries valid) and n_kept[batch].
+ *
+ * Replaces: NexusQuantEvict._build_keep_mask (topk + scatter)  pipeline.py:895-959
+ *           keep_mask[0].nonzero() of the truncation path      pipeline.py:1319
+ */
+int nq_keep_mask(const float* importance, int32_t batch, int32_t seq, int32_t sliding_window,
+                 int32_t prefix, int32_t k, const int32_t* protected_pos, int32_t n_protected,
+                 uint8_t* keep, int32_t* kept_idx, int32_t* n_kept, void* stream);
+
+/*
+ * fp16 passthrough of protected layers: dst[t] = fp16(src[gather[b, t]]) or
+ * fp16(src[t]) * keep[b, t], for n_tensors tensors (device arrays of base
+ * addresses) of shape [batch, heads, seq_in, head_dim].
+ *
+ * Replaces: protected-layer branches  pipeline.py:1204-1210 (mask), 1359-1368 (truncate)
+ */
+int nq_gather_rows(const uint64_t* src, const uint64_t* dst, int32_t n_tensors, int32_t dtype, int32_t batch,
+                   int32_t heads, int32_t seq_in, int32_t seq_out, int32_t head_dim, const int32_t* gather,
+                   const uint8_t* keep, void* stream);
+
 /* Library version and the last error message of the calling thread. */
 int nq_abi_version(void);
 const char* nq_last_error(void);

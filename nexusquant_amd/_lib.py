@@ -34,10 +34,18 @@ class QuantDesc(ctypes.Structure):
 # Every exported symbol, with (argtypes, restype).  tests/test_abi.py checks
 # that this list and include/nexusquant_amd.h agree and that the library
 # exports all of them.
+_I32, _I64, _F32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+
 SIGNATURES = {
     "nq_abi_version": ([], ctypes.c_int),
     "nq_last_error": ([], ctypes.c_char_p),
     "nq_quantize": ([ctypes.POINTER(QuantDesc), _P], ctypes.c_int),
+    "nq_score_keykey_workspace": ([_I32, _I32, _I32], _I64),
+    "nq_score_keykey": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
+    "nq_keep_mask": ([_P, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P], ctypes.c_int),
+    "nq_gather_rows": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
+    "nq_score_real_workspace": ([_I32, _I32, _I32], _I64),
+    "nq_score_real": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
 }
 
 _lock = threading.Lock()

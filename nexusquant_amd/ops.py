@@ -152,3 +152,103 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
         if t is not None:
             t.record_stream(stream)
     return recon_t, codes_t
+
+
+# ---------------------------------------------------------------------------
+# Eviction: importance, keep mask, fp16 passthrough
+# ---------------------------------------------------------------------------
+
+def score_keykey(keys: torch.Tensor, obs_window: int = 32) -> torch.Tensor:
+    """Key-key importance [batch, seq] fp32 of keys [batch, heads, seq, d] (MFMA kernel)."""
+    lib = _lib.load()
+    _lib.require_device(keys, "keys")
+    if keys.dim() != 4:
+        raise ValueError(f"expected keys [batch, heads, seq, head_dim], got {tuple(keys.shape)}")
+    b, h, s, d = keys.shape
+    k = keys.contiguous()
+    if k.data_ptr() % 16:
+        k = k.clone()
+    dev = k.device
+    imp = torch.empty(b, s, dtype=torch.float32, device=dev)
+    if s == 0:
+        return imp
+    ws_bytes = lib.nq_score_keykey_workspace(b, h, s)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    scale = float(d) ** -0.5
+    with torch.cuda.device(dev):
+        st = lib.nq_score_keykey(_addr(k), _lib.dtype_code(k.dtype), b, h, s, d, int(obs_window),
+                                 ctypes.c_float(scale), _addr(imp), _addr(ws), ws_bytes,
+                                 ctypes.c_void_p(_lib.current_stream_handle(dev)))
+    _lib.check(st, "nq_score_keykey")
+    return imp
+
+
+def keep_plan(seq: int, rate: float, sliding_window: int) -> Tuple[int, int]:
+    """(prefix, k) of the keep mask, in Python double as pipeline.py:924-925, 944-946."""
+    prefix = max(seq - sliding_window, 0)
+    n_keep = max(1, int(prefix * (1.0 - rate)))
+    k = min(n_keep, prefix - 1) if (prefix > 1 and n_keep > 0) else 0
+    return prefix, max(k, 0)
+
+
+def keep_mask(importance: torch.Tensor, rate: float, sliding_window: int = 32,
+              protected_positions=None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(keep uint8 [b, s], kept_idx int32 [b, s], n_kept int32 [b]) on the device."""
+    lib = _lib.load()
+    _lib.require_device(importance, "importance")
+    imp = importance.to(torch.float32).contiguous()
+    b, s = imp.shape
+    dev = imp.device
+    prefix, k = keep_plan(s, rate, sliding_window)
+    keep = torch.empty(b, s, dtype=torch.uint8, device=dev)
+    kept = torch.empty(b, s, dtype=torch.int32, device=dev)
+    n_kept = torch.empty(b, dtype=torch.int32, device=dev)
+    prot = None
+    n_prot = 0
+    if protected_positions is not None:
+        pl = [int(p) for p in (protected_positions.tolist() if torch.is_tensor(protected_positions)
+                               else protected_positions)]
+        if pl:
+            prot = torch.tensor(pl, dtype=torch.int32, device=dev)
+            n_prot = len(pl)
+    with torch.cuda.device(dev):
+        st = lib.nq_keep_mask(_addr(imp), b, s, int(sliding_window), prefix, k, _addr(prot), n_prot,
+                              _addr(keep), _addr(kept), _addr(n_kept),
+                              ctypes.c_void_p(_lib.current_stream_handle(dev)))
+    _lib.check(st, "nq_keep_mask")
+    return keep, kept, n_kept
+
+
+def gather_rows(tensors: Sequence[torch.Tensor], *, gather: Optional[torch.Tensor] = None,
+                keep: Optional[torch.Tensor] = None) -> List[torch.Tensor]:
+    """fp16 passthrough of same-shaped tensors: gathered rows or zeroed evicted rows."""
+    lib = _lib.load()
+    if not tensors:
+        return []
+    t0 = tensors[0]
+    _lib.require_device(t0, "KV tensor")
+    b, h, s, d = t0.shape
+    dev = t0.device
+    src = [t.contiguous() for t in tensors]
+    src = [t if t.data_ptr() % 16 == 0 else t.clone() for t in src]
+    g = None
+    seq_out = s
+    if gather is not None:
+        g = gather.to(device=dev, dtype=torch.int32).contiguous()
+        if g.dim() == 1:
+            g = g.unsqueeze(0).expand(b, -1).contiguous()
+        seq_out = g.shape[1]
+        if g.numel() and (int(g.min()) < 0 or int(g.max()) >= s):
+            raise ValueError(f"gather indices must lie in [0, {s})")
+    k = None
+    if keep is not None:
+        k = keep.to(device=dev, dtype=torch.uint8).contiguous()
+        if tuple(k.shape) != (b, s):
+            raise ValueError(f"keep must be [batch, seq] = {(b, s)}")
+    out = [torch.empty(b, h, seq_out, d, dtype=torch.float16, device=dev) for _ in src]
+    arr_src, arr_dst = _ptr_arrays([src, out], dev)
+    with torch.cuda.device(dev):
+        st = lib.nq_gather_rows(_addr(arr_src), _addr(arr_dst), len(src), _lib.dtype_code(t0.dtype), b, h, s,
+                                seq_out, d, _addr(g), _addr(k), ctypes.c_void_p(_lib.current_stream_handle(dev)))
+    _lib.check(st, "nq_gather_rows")
+    return out

@@ -1,0 +1,267 @@
+"""GPU parity of the eviction path: MFMA scorers, top-k keep mask, mask and
+truncation pipelines, and the nexusquant_evict hook, against the Tier-A torch
+oracle and the reference's own fixtures (tests/golden)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import torch_ref as T
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+class Cache:
+    def __init__(self, ks, vs):
+        self.key_cache, self.value_cache = list(ks), list(vs)
+
+
+def _keys(b, h, s, d, dtype, seed, sink=True):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(b, h, s, d, generator=g)
+    k[..., ::32] *= 8
+    if sink:
+        k[:, :, 0, :] *= 4
+    return k.to(dtype)
+
+
+def _keep_sets_match(imp_gpu, imp_ref, keep_gpu, keep_ref, tol=1e-6, window=32):
+    """Keep sets identical except positions whose reference score lies within tol
+    of the k-th largest prefix score (a tie the two scorers may break differently)."""
+    diff = keep_gpu != keep_ref
+    for bi in range(keep_gpu.shape[0]):
+        idx = np.nonzero(diff[bi])[0]
+        if idx.size == 0:
+            continue
+        s = keep_ref.shape[1]
+        prefix = max(s - window, 0)
+        scores = np.sort(imp_ref[bi][1:prefix])[::-1]
+        k = int(keep_ref[bi][1:prefix].sum())
+        kth = scores[k - 1] if k > 0 else np.inf
+        if np.any(np.abs(imp_ref[bi][idx] - kth) > tol):
+            return False
+    return True
+
+
+@pytest.mark.parametrize("dtype,d,s", [(torch.float16, 128, 1000), (torch.bfloat16, 128, 777),
+                                       (torch.float32, 128, 512), (torch.float16, 64, 300),
+                                       (torch.float16, 256, 400), (torch.float16, 96, 333),
+                                       (torch.float16, 128, 20)])
+def test_keykey_scorer_matches_oracle(dtype, d, s):
+    from nexusquant_amd.ops import score_keykey
+    print(f"[gpu] keykey {dtype} d={d} s={s}", flush=True)
+    k = _keys(3, 4, s, d, dtype, seed=s + d)
+    imp = score_keykey(k.to(DEV), 32).cpu()
+    ref = T.score_keykey(k.float(), 32)
+    # logits reach |x| ~ 1e2 here (outlier channels, sink), so a 1e-7 relative
+    # difference of the fp32 dot products (MFMA vs MKL summation order) becomes
+    # ~1e-5 relative after exp; the parity criterion is the keep set.
+    assert torch.allclose(imp, ref, rtol=1e-4, atol=1e-8), (imp - ref).abs().max()
+    for rate in (0.25, 0.6):
+        km = T.build_keep_mask(imp, s, rate, 32).numpy()
+        kr = T.build_keep_mask(ref, s, rate, 32).numpy()
+        assert _keep_sets_match(imp.numpy(), ref.numpy(), km, kr)
+
+
+def test_keykey_scorer_matches_reference_fixture(golden):
+    from nexusquant_amd.ops import score_keykey
+    g = golden("evict_mask_b4")
+    imp = score_keykey(torch.from_numpy(g["k_in"][0]).to(DEV), 32).cpu().numpy()
+    assert np.allclose(imp, g["importance"], rtol=2e-5, atol=1e-8)
+
+
+@pytest.mark.parametrize("s,rate,sw", [(8192, 0.25, 32), (1000, 0.6, 32), (300, 0.8, 8), (50, 0.5, 4),
+                                       (33, 0.6, 32), (4096, 0.35, 0)])
+def test_keep_mask_matches_oracle(s, rate, sw):
+    from nexusquant_amd.ops import keep_mask
+    print(f"[gpu] keep mask s={s} rate={rate}", flush=True)
+    g = torch.Generator().manual_seed(s)
+    imp = torch.rand(4, s, generator=g)
+    keep, kept, n_kept = keep_mask(imp.to(DEV), rate, sw)
+    ref = T.build_keep_mask(imp, s, rate, sw)
+    assert torch.equal(keep.cpu().bool(), ref)
+    kk, nk = kept.cpu(), n_kept.cpu()
+    for bi in range(4):
+        want = ref[bi].nonzero(as_tuple=True)[0].to(torch.int32)
+        assert int(nk[bi]) == want.numel()
+        assert torch.equal(kk[bi, :want.numel()], want)
+
+
+def test_keep_mask_ties_keep_lowest_positions_and_protected():
+    from nexusquant_amd.ops import keep_mask
+    s = 400
+    imp = torch.zeros(2, s)
+    imp[:, 1:368] = 0.5          # all-equal prefix scores: pure tie
+    imp[1, 100:110] = 0.9
+    keep, kept, n_kept = keep_mask(imp.to(DEV), 0.6, 32, protected_positions=[5, 399, 390, 250])
+    keep = keep.cpu().bool()
+    prefix = s - 32
+    k = min(max(1, int(prefix * 0.4)), prefix - 1)
+    # row 0: ties only -> positions 1..k kept
+    assert keep[0, 1:1 + k].all() and not keep[0, 1 + k:prefix].any() or keep[0, 250]
+    assert keep[:, 0].all() and keep[:, s - 32:].all() and keep[:, 5].all() and keep[:, 250].all()
+    # row 1: the ten high scores, then the lowest tied positions
+    assert keep[1, 100:110].all()
+    assert int(n_kept[0]) == int(keep[0].sum()) and int(n_kept[1]) == int(keep[1].sum())
+
+
+def _assert_close_rows(got, ref, max_flip_frac=1e-4):
+    got = got.float().cpu().numpy().reshape(-1, got.shape[-1])
+    ref = np.asarray(ref, np.float32).reshape(-1, got.shape[-1])
+    num = np.linalg.norm(got - ref, axis=1)
+    den = np.maximum(np.linalg.norm(ref, axis=1), 1e-30)
+    flipped = (num / den) > 1e-2
+    assert flipped.sum() <= max(1, int(max_flip_frac * got.size / 8)), flipped.sum()
+    ok = ~flipped
+    if ok.any() and np.linalg.norm(ref[ok]) > 0:
+        assert np.linalg.norm(got[ok] - ref[ok]) / np.linalg.norm(ref[ok]) <= 1e-3
+
+
+def test_mask_eviction_matches_reference_fixture(golden):
+    import nexusquant_amd as nq
+    print("[gpu] evict mask fixture", flush=True)
+    g = golden("evict_mask_b4")
+    c = Cache([torch.from_numpy(k).to(DEV) for k in g["k_in"]], [torch.from_numpy(v).to(DEV) for v in g["v_in"]])
+    comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.25, sliding_window=32,
+                              obs_window=32, rope_base=10000.0)
+    _, mask = comp.compress(c)
+    assert np.array_equal(mask.cpu().numpy(), g["mask"])
+    for li in range(len(c.key_cache)):
+        assert c.key_cache[li].dtype == torch.float16
+        _assert_close_rows(c.key_cache[li], g["k_out"][li])
+        _assert_close_rows(c.value_cache[li], g["v_out"][li])
+
+
+def test_boundary_protection_matches_reference_fixture(golden):
+    import nexusquant_amd as nq
+    print("[gpu] boundary fixture", flush=True)
+    g = golden("evict_mask_boundary")
+    c = Cache([torch.from_numpy(k).to(DEV) for k in g["k_in"]], [torch.from_numpy(v).to(DEV) for v in g["v_in"]])
+    comp = nq.NexusQuantEvict(bits=2, eviction_rate=0.6, sliding_window=16, rope_base=10000.0,
+                              protect_boundary=2)
+    _, mask = comp.compress(c)
+    assert np.array_equal(mask.cpu().numpy(), g["mask"])
+    n = len(c.key_cache)
+    for li in range(n):
+        if li in (0, 1, n - 2, n - 1):          # fp16 passthrough: exact
+            assert np.array_equal(c.key_cache[li].cpu().numpy(), g["k_out"][li])
+            assert np.array_equal(c.value_cache[li].cpu().numpy(), g["v_out"][li])
+        else:
+            _assert_close_rows(c.key_cache[li], g["k_out"][li])
+            _assert_close_rows(c.value_cache[li], g["v_out"][li])
+
+
+@pytest.mark.parametrize("rate", [25, 60])
+def test_truncation_matches_reference_fixture(golden, rate):
+    import nexusquant_amd as nq
+    print(f"[gpu] truncate fixture {rate}", flush=True)
+    g = golden(f"evict_truncate_r{rate}")
+    c = Cache([torch.from_numpy(k).to(DEV) for k in g["k_in"]], [torch.from_numpy(v).to(DEV) for v in g["v_in"]])
+    comp = nq.NexusQuantEvictTruncate(key_bits=3, value_bits=2, eviction_rate=rate / 100,
+                                      sliding_window=32, rope_base=10000.0)
+    _, n_kept = comp.compress(c)
+    assert n_kept == int(g["n_kept"])
+    for li in range(len(c.key_cache)):
+        assert c.key_cache[li].shape == g["k_out"][li].shape
+        _assert_close_rows(c.key_cache[li], g["k_out"][li])
+        _assert_close_rows(c.value_cache[li], g["v_out"][li])
+
+
+def test_truncation_with_protected_layers_gathers_fp16_exactly():
+    import nexusquant_amd as nq
+    ks = [_keys(1, 2, 200, 128, torch.bfloat16, seed=i) for i in range(4)]
+    vs = [_keys(1, 2, 200, 128, torch.bfloat16, seed=10 + i, sink=False) for i in range(4)]
+    c = Cache([k.to(DEV) for k in ks], [v.to(DEV) for v in vs])
+    comp = nq.NexusQuantEvictTruncate(bits=2, eviction_rate=0.5, sliding_window=16, protected_layers={0, 3})
+    _, n_kept = comp.compress(c)
+    ref = Cache([k.clone() for k in ks], [v.clone() for v in vs])
+    _, n_ref = T.evict_truncate_compress(ref, 4, 4, 0.5, sliding_window=16, skip_layers={0, 3})
+    assert n_kept == n_ref
+    for li in (0, 3):
+        assert torch.equal(c.key_cache[li].cpu(), ref.key_cache[li])
+        assert torch.equal(c.value_cache[li].cpu(), ref.value_cache[li])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_real_scorer_kernel_matches_eager_oracle(dtype):
+    from nexusquant_amd.scoring import score_real_accumulate
+    print(f"[gpu] real scorer {dtype}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    s, d = 300, 64
+    q = [(torch.randn(1, 8, s, d, generator=g) * 0.7).to(dtype) for _ in range(2)]
+    k = [(torch.randn(1, 2, s, d, generator=g) * 0.7).to(dtype) for _ in range(2)]
+    imp = torch.zeros(1, s, device=DEV)
+    for ql, kl in zip(q, k):
+        score_real_accumulate(ql.to(DEV), kl.to(DEV), imp, d ** -0.5)
+    imp = (imp / 2).cpu()
+    ref = T.score_real_from_qk([x.float() if dtype == torch.float32 else x for x in q],
+                               [x.float() if dtype == torch.float32 else x for x in k], d ** -0.5)
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    assert torch.allclose(imp, ref, rtol=tol, atol=1e-6), (imp - ref).abs().max()
+
+
+def test_real_scorer_matches_reference_fixture(golden):
+    from nexusquant_amd.scoring import score_real_accumulate
+    g = golden("real_scorer")
+    q, k = torch.from_numpy(g["q"]), torch.from_numpy(g["k"])
+    imp = torch.zeros(q.shape[1], q.shape[3], device=DEV)
+    for li in range(q.shape[0]):
+        score_real_accumulate(q[li].to(DEV), k[li].to(DEV), imp, float(g["scaling"]))
+    imp = (imp / q.shape[0]).cpu().numpy()
+    assert np.allclose(imp, g["importance"], rtol=1e-5, atol=1e-7)
+
+
+def _tiny_llama(attn="eager", dtype=torch.float16, layers=2, kv_heads=2):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    torch.manual_seed(5)
+    cfg = LlamaConfig(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=layers,
+                      num_attention_heads=4, num_key_value_heads=kv_heads, max_position_embeddings=1024,
+                      rope_theta=10000.0)
+    cfg._attn_implementation = attn
+    return LlamaForCausalLM(cfg).to(DEV, dtype).eval()
+
+
+def test_nexusquant_evict_hook_compresses_each_layer():
+    import nexusquant_amd as nq
+    from transformers import DynamicCache
+    print("[gpu] hook key-key", flush=True)
+    model = _tiny_llama()
+    ids = torch.randint(0, 256, (1, 200), generator=torch.Generator().manual_seed(1)).to(DEV)
+    with torch.no_grad():
+        plain = DynamicCache()
+        model(ids, past_key_values=plain, use_cache=True)
+        cache = DynamicCache()
+        with nq.nexusquant_evict(model, quality="high", verbose=False) as comp:
+            model(ids, past_key_values=cache, use_cache=True)
+    assert comp.last_mask is not None and comp.last_mask.shape == (1, 200)
+    k0 = cache.layers[0].keys
+    assert k0.dtype == torch.float16 and k0.shape == plain.layers[0].keys.shape
+    # layer 0 sees uncompressed inputs: compare with the oracle on the same K/V
+    ref = Cache([plain.layers[0].keys.cpu()], [plain.layers[0].values.cpu()])
+    T.evict_mask_compress(ref, 8, 4, 0.35, sliding_window=32, obs_window=32, rope_base=10000.0)
+    m = comp.last_mask.cpu()
+    assert m[0, 0] == 1 and torch.all(m[0, -32:] == 1)
+    assert int(m.sum()) == 1 + min(max(1, int(168 * 0.65)), 167) + 32
+    _assert_close_rows(k0, ref.key_cache[0].numpy())
+    _assert_close_rows(cache.layers[0].values, ref.value_cache[0].numpy())
+
+
+def test_nexusquant_evict_real_scorer_matches_eager_attentions():
+    import nexusquant_amd as nq
+    from transformers import DynamicCache
+    print("[gpu] hook real scorer", flush=True)
+    model = _tiny_llama(layers=3)
+    ids = torch.randint(0, 256, (1, 160), generator=torch.Generator().manual_seed(2)).to(DEV)
+    with torch.no_grad():
+        out = model(ids, use_cache=False, output_attentions=True)
+        ref = torch.zeros(1, 160, device=DEV)
+        for a in out.attentions:
+            ref += a.float().sum(dim=2).mean(dim=1)
+        ref /= len(out.attentions)
+        cache = DynamicCache()
+        with nq.nexusquant_evict(model, quality="high", scorer="real", input_ids=ids, verbose=False) as comp:
+            model(ids, past_key_values=cache, use_cache=True)
+    imp = comp._cached_real_importance
+    assert torch.allclose(imp, ref, rtol=2e-3, atol=1e-5), (imp - ref).abs().max()
+    assert comp.last_mask.shape == (1, 160)
