@@ -145,6 +145,57 @@ int nq_gather_rows(const uint64_t* src, const uint64_t* dst, int32_t n_tensors, 
                    int32_t heads, int32_t seq_in, int32_t seq_out, int32_t head_dim, const int32_t* gather,
                    const uint8_t* keep, void* stream);
 
+/*
+ * Packed codes of n_tensors tensors [batch, heads, seq, head_dim] written by
+ * nq_quantize (syms / cosets / scales arrays of base addresses).
+ */
+typedef struct nq_codes_desc {
+    int32_t n_tensors;
+    int32_t batch, heads, seq, head_dim;
+    int32_t levels;
+    int32_t is_key;          /* dequantize: forward RoPE at positions 0..seq-1 */
+    int32_t reserved;
+    const uint64_t* syms;
+    const uint64_t* cosets;
+    const uint64_t* scales;
+    const uint64_t* out;     /* per tensor output base address */
+    const float* rope_cos;   /* [rope_n_pos, head_dim/2], keys only */
+    const float* rope_sin;
+    int64_t rope_n_pos;
+    float hadamard_scale;
+    float reserved_f;
+} nq_codes_desc;
+
+/*
+ * Codes -> fp16 reconstruction [batch, heads, seq, head_dim]; identical to the
+ * reconstruction nq_quantize writes for the same rows.
+ *
+ * Replaces: _dequantize_perhead + inverse Hadamard + forward_rope
+ *           vllm_backend.py:319-338, pipeline.py:253-255
+ */
+int nq_dequantize(const nq_codes_desc* desc, void* stream);
+
+/*
+ * Codes -> int8 code = 2p per coordinate [batch, heads, seq, D] (delta = 0), or
+ * the temporal delta stream of those codes along tokens, first token raw,
+ * int8 wrap (delta = 1).
+ *
+ * Replaces: _quantize_perhead_with_scales code output  vllm_backend.py:309-314
+ *           _compress_with_delta_zstd delta step        compression_accounting.py:56-60
+ *           temporal_delta_encode                       temporal_codec.py:30-52
+ */
+int nq_codes_to_int8(const nq_codes_desc* desc, int32_t delta, void* stream);
+
+/*
+ * Inverse of the delta stream: out[s, t, :] = sum_{u <= t} deltas[s, u, :]
+ * (int8 wrap) for n_tensors tensors of `streams` x seq x coords int8.
+ *
+ * Replaces: _decompress_with_delta cumsum  compression_accounting.py:70-77
+ *           temporal_delta_decode          temporal_codec.py:55-73
+ */
+int nq_delta_decode(const uint64_t* deltas, const uint64_t* out, int32_t n_tensors, int32_t streams, int32_t seq,
+                    int32_t coords, void* stream);
+
 /* Library version and the last error message of the calling thread. */
 int nq_abi_version(void);
 const char* nq_last_error(void);

@@ -31,6 +31,19 @@ class QuantDesc(ctypes.Structure):
     ]
 
 
+class CodesDesc(ctypes.Structure):
+    """Mirror of nq_codes_desc in include/nexusquant_amd.h."""
+    _fields_ = [
+        ("n_tensors", ctypes.c_int32),
+        ("batch", ctypes.c_int32), ("heads", ctypes.c_int32), ("seq", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("levels", ctypes.c_int32), ("is_key", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("syms", _P), ("cosets", _P), ("scales", _P), ("out", _P),
+        ("rope_cos", _P), ("rope_sin", _P), ("rope_n_pos", ctypes.c_int64),
+        ("hadamard_scale", ctypes.c_float), ("reserved_f", ctypes.c_float),
+    ]
+
+
 # Every exported symbol, with (argtypes, restype).  tests/test_abi.py checks
 # that this list and include/nexusquant_amd.h agree and that the library
 # exports all of them.
@@ -44,6 +57,9 @@ SIGNATURES = {
     "nq_score_keykey": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
     "nq_keep_mask": ([_P, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P], ctypes.c_int),
     "nq_gather_rows": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
+    "nq_dequantize": ([ctypes.POINTER(CodesDesc), _P], ctypes.c_int),
+    "nq_codes_to_int8": ([ctypes.POINTER(CodesDesc), _I32, _P], ctypes.c_int),
+    "nq_delta_decode": ([_P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "nq_score_real_workspace": ([_I32, _I32, _I32], _I64),
     "nq_score_real": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
 }

@@ -1,0 +1,318 @@
+// Packed-code kernels for gfx950: dequantize to the fp16 reconstruction,
+// convert to int8 2p codes (the reference's vLLM page format,
+// vllm_backend.py:267-338), the temporal delta stream of those codes
+// (compression_accounting.py:49-62) and its inverse (:70-77).
+//
+// Rows use the quantizer's quad layout (lane q owns chunks c of coordinates
+// 32c + 8q .. +7; its symbol slots are the q-th run of C slots of the row), so
+// dequantization repeats the quantizer's reconstruction arithmetic exactly.
+#include "nq_rowmath.h"
+
+namespace nq {
+
+struct CodecArgs {
+    const uint64_t* syms;
+    const uint64_t* cosets;
+    const uint64_t* scales;
+    const uint64_t* out;
+    const float* rope_cos;
+    const float* rope_sin;
+    uint32_t heads, seq, n_tensors, bh, work, per_xcd;
+    float hscale;
+};
+
+// Lattice points of this lane's C groups from the packed row.
+template <int D, int L>
+__device__ __forceinline__ void unpack_points(const CodecArgs& a, uint32_t tensor, size_t row, int q,
+                                             float (&p)[D / 32][8], int (&coset)[D / 32], float& scale) {
+    constexpr int C = D / 32;
+    constexpr int B = SymBits<L>::value;
+    constexpr int NB = C * B;
+    constexpr int HL = L / 2;
+    constexpr int ROW_BYTES = D / 8 * B;
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.syms[tensor]) + row * ROW_BYTES + q * NB;
+    uint8_t bytes[NB];
+    if constexpr (NB % 4 == 0) {
+#pragma unroll
+        for (int k = 0; k < NB; k += 4) {
+            uint32_t w = *reinterpret_cast<const uint32_t*>(src + k);
+            bytes[k] = (uint8_t)w;
+            bytes[k + 1] = (uint8_t)(w >> 8);
+            bytes[k + 2] = (uint8_t)(w >> 16);
+            bytes[k + 3] = (uint8_t)(w >> 24);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NB; k += 2) {
+            uint16_t w = *reinterpret_cast<const uint16_t*>(src + k);
+            bytes[k] = (uint8_t)w;
+            bytes[k + 1] = (uint8_t)(w >> 8);
+        }
+    }
+    const uint8_t* cb = reinterpret_cast<const uint8_t*>(a.cosets[tensor]) + row * (D / 64);
+    uint32_t cbits;
+    if constexpr (D == 64) cbits = *cb;
+    else if constexpr (D == 128) cbits = *reinterpret_cast<const uint16_t*>(cb);
+    else cbits = *reinterpret_cast<const uint32_t*>(cb);
+    scale = reinterpret_cast<const float*>(a.scales[tensor])[row];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        uint64_t v = 0;
+#pragma unroll
+        for (int m = 0; m < B; ++m) v |= (uint64_t)bytes[c * B + m] << (8 * m);
+        coset[c] = (int)((cbits >> (4 * c + q)) & 1u);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int sym = (int)((v >> (B * j)) & ((1u << B) - 1u));
+            float x = (float)(sym - HL);
+            if (coset[c]) {
+                if constexpr ((HL & 1) == 0) x = __builtin_fminf(x + 0.5f, (float)HL);
+                else x = __builtin_fmaxf(x - 0.5f, (float)-HL);
+            }
+            p[c][j] = x;
+        }
+    }
+}
+
+template <int D, int L, bool IS_KEY>
+__global__ __launch_bounds__(256) void dequant_kernel(CodecArgs a) {
+    constexpr int C = D / 32;
+    constexpr int HALF = D / 2;
+    const int q = threadIdx.x & 3;
+    const uint32_t w = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
+    if (w >= a.work) return;
+    const uint32_t tensor = w % a.n_tensors;
+    const uint32_t rest = w / a.n_tensors;
+    const uint32_t bh = rest % a.bh;
+    const uint32_t t_raw = (rest / a.bh) * 64u + (threadIdx.x >> 2);
+    const bool active = t_raw < a.seq;
+    const uint32_t t = active ? t_raw : a.seq - 1u;
+    const size_t row = (size_t)bh * a.seq + t;
+
+    float x[C][8];
+    int coset[C];
+    float scale;
+    unpack_points<D, L>(a, tensor, row, q, x, coset, scale);
+    const float g = quad_sign(q) * (a.hscale * scale);
+    constexpr bool EXACT_F16 = D * (L / 2) <= 1024;
+    if constexpr (EXACT_F16) {
+        half2v hp[C][4];
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                hp[c][k] = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(x[c][2 * k], x[c][2 * k + 1]));
+        fwht_row_f16<C>(hp, q);
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                x[c][2 * k] = __builtin_fmaf((float)hp[c][k].x, g, 0.0f);
+                x[c][2 * k + 1] = __builtin_fmaf((float)hp[c][k].y, g, 0.0f);
+            }
+    } else {
+        fwht_row<C>(x, q);
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[c][i] = x[c][i] * g;
+    }
+    if constexpr (IS_KEY) {
+        const float* ct = a.rope_cos + (size_t)t * HALF;
+        const float* st = a.rope_sin + (size_t)t * HALF;
+#pragma unroll
+        for (int c = 0; c < C / 2; ++c) {
+            float cs[8], sn[8];
+            load8f(ct + 32 * c + 8 * q, cs);
+            load8f(st + 32 * c + 8 * q, sn);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float lo = x[c][i], hi = x[c + C / 2][i];
+                x[c][i] = __builtin_fmaf(lo, cs[i], -(hi * sn[i]));
+                x[c + C / 2][i] = __builtin_fmaf(lo, sn[i], hi * cs[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) asm("" : "+v"(x[c][i]));  // keep the fp32 rounding (see quantizer)
+    if (!active) return;
+    half2v* dst = reinterpret_cast<half2v*>(reinterpret_cast<uint16_t*>(a.out[tensor]) + row * D);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        uint4 o;
+        half2v h0 = {(__fp16)x[c][0], (__fp16)x[c][1]}, h1 = {(__fp16)x[c][2], (__fp16)x[c][3]};
+        half2v h2 = {(__fp16)x[c][4], (__fp16)x[c][5]}, h3 = {(__fp16)x[c][6], (__fp16)x[c][7]};
+        o.x = __builtin_bit_cast(uint32_t, h0);
+        o.y = __builtin_bit_cast(uint32_t, h1);
+        o.z = __builtin_bit_cast(uint32_t, h2);
+        o.w = __builtin_bit_cast(uint32_t, h3);
+        *reinterpret_cast<uint4*>(dst + (32 * c + 8 * q) / 2) = o;
+    }
+}
+
+// int8 2p of this lane's 32 coordinates, packed 4 per dword in coordinate order.
+template <int D, int L>
+__device__ __forceinline__ void codes2p(const CodecArgs& a, uint32_t tensor, size_t row, int q,
+                                        uint32_t (&out)[D / 32][2]) {
+    float p[D / 32][8];
+    int coset[D / 32];
+    float scale;
+    unpack_points<D, L>(a, tensor, row, q, p, coset, scale);
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)(p[c][j] * 2.0f);
+            if (j < 4) lo |= b << (8 * j);
+            else hi |= b << (8 * (j - 4));
+        }
+        out[c][0] = lo;
+        out[c][1] = hi;
+    }
+}
+
+// Byte-wise wrapping subtraction of four int8 lanes.
+__device__ __forceinline__ uint32_t sub_bytes(uint32_t a, uint32_t b) {
+    return ((a | 0x80808080u) - (b & 0x7f7f7f7fu)) ^ ((a ^ ~b) & 0x80808080u);
+}
+
+template <int D, int L, bool DELTA>
+__global__ __launch_bounds__(256) void int8_codes_kernel(CodecArgs a) {
+    constexpr int C = D / 32;
+    const int q = threadIdx.x & 3;
+    const uint32_t w = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
+    if (w >= a.work) return;
+    const uint32_t tensor = w % a.n_tensors;
+    const uint32_t rest = w / a.n_tensors;
+    const uint32_t bh = rest % a.bh;
+    const uint32_t t = (rest / a.bh) * 64u + (threadIdx.x >> 2);
+    if (t >= a.seq) return;  // no cross-lane operations below
+    const size_t row = (size_t)bh * a.seq + t;
+    uint32_t cur[C][2];
+    codes2p<D, L>(a, tensor, row, q, cur);
+    if constexpr (DELTA) {
+        if (t > 0) {
+            uint32_t prev[C][2];
+            codes2p<D, L>(a, tensor, row - 1, q, prev);
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                cur[c][0] = sub_bytes(cur[c][0], prev[c][0]);
+                cur[c][1] = sub_bytes(cur[c][1], prev[c][1]);
+            }
+        }
+    }
+    int8_t* dst = reinterpret_cast<int8_t*>(a.out[tensor]) + row * D;
+#pragma unroll
+    for (int c = 0; c < C; ++c) *reinterpret_cast<uint2*>(dst + 32 * c + 8 * q) = make_uint2(cur[c][0], cur[c][1]);
+}
+
+// Prefix sum of int8 deltas along tokens (wrapping), four coordinates per thread.
+__global__ __launch_bounds__(256) void delta_decode_kernel(const uint64_t* deltas, const uint64_t* out, uint32_t bh,
+                                                           uint32_t seq, uint32_t words_per_row, uint32_t n_cols) {
+    const uint32_t col = blockIdx.x * 256u + threadIdx.x;  // (stream, word)
+    if (col >= n_cols) return;
+    const uint32_t tensor = blockIdx.y;
+    const uint32_t stream = col / words_per_row;
+    const uint32_t word = col - stream * words_per_row;
+    const uint32_t* in = reinterpret_cast<const uint32_t*>(deltas[tensor]) + (size_t)stream * seq * words_per_row + word;
+    uint32_t* o = reinterpret_cast<uint32_t*>(out[tensor]) + (size_t)stream * seq * words_per_row + word;
+    uint32_t acc = 0;
+    for (uint32_t t = 0; t < seq; ++t) {
+        const uint32_t d = in[(size_t)t * words_per_row];
+        acc = ((acc & 0x7f7f7f7fu) + (d & 0x7f7f7f7fu)) ^ ((acc ^ d) & 0x80808080u);
+        o[(size_t)t * words_per_row] = acc;
+    }
+}
+
+template <int D, int L>
+static hipError_t launch_codec(int kind, bool key, const CodecArgs& a, hipStream_t s) {
+    dim3 grid(a.per_xcd * 8u);
+    if (kind == 0) {
+        if (key) hipLaunchKernelGGL((dequant_kernel<D, L, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((dequant_kernel<D, L, false>), grid, dim3(256), 0, s, a);
+    } else if (kind == 1) {
+        hipLaunchKernelGGL((int8_codes_kernel<D, L, false>), grid, dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((int8_codes_kernel<D, L, true>), grid, dim3(256), 0, s, a);
+    }
+    return hipGetLastError();
+}
+
+template <int D>
+static hipError_t codec_levels(int L, int kind, bool key, const CodecArgs& a, hipStream_t s) {
+    switch (L) {
+        case 2: return launch_codec<D, 2>(kind, key, a, s);
+        case 4: return launch_codec<D, 4>(kind, key, a, s);
+        case 8: return launch_codec<D, 8>(kind, key, a, s);
+        default: return launch_codec<D, 16>(kind, key, a, s);
+    }
+}
+
+static int run_codec(const nq_codes_desc* d, int kind, void* stream) {
+    NQ_CHECK_ARG(d != nullptr, "nq codes: desc is NULL");
+    NQ_CHECK_ARG(d->n_tensors >= 0 && d->n_tensors <= 65535, "nq codes: n_tensors out of range");
+    if (d->n_tensors == 0 || d->seq == 0) return NQ_OK;
+    NQ_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128 || d->head_dim == 256,
+                 "nq codes: head_dim %d unsupported (64, 128, 256)", d->head_dim);
+    NQ_CHECK_ARG(d->levels == 2 || d->levels == 4 || d->levels == 8 || d->levels == 16,
+                 "nq codes: levels must be 2, 4, 8 or 16");
+    NQ_CHECK_ARG(d->batch > 0 && d->heads > 0 && d->seq > 0, "nq codes: bad geometry");
+    NQ_CHECK_ARG(d->syms && d->cosets && d->scales && d->out, "nq codes: NULL pointer array");
+    if (kind == 0 && d->is_key) {
+        NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos >= d->seq, "nq_dequantize: RoPE table too short");
+    }
+    const uint64_t rows = (uint64_t)d->batch * d->heads * d->seq;
+    NQ_CHECK_ARG(rows < (1ull << 31), "nq codes: too many rows");
+    CodecArgs a;
+    a.syms = d->syms;
+    a.cosets = d->cosets;
+    a.scales = d->scales;
+    a.out = d->out;
+    a.rope_cos = d->rope_cos;
+    a.rope_sin = d->rope_sin;
+    a.heads = (uint32_t)d->heads;
+    a.seq = (uint32_t)d->seq;
+    a.n_tensors = (uint32_t)d->n_tensors;
+    a.bh = (uint32_t)d->batch * (uint32_t)d->heads;
+    const uint64_t work = (uint64_t)((d->seq + 63) / 64) * a.bh * a.n_tensors;
+    NQ_CHECK_ARG(work < (1ull << 32) - 8, "nq codes: grid too large");
+    a.work = (uint32_t)work;
+    a.per_xcd = (uint32_t)((work + 7) / 8);
+    a.hscale = d->hadamard_scale;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e;
+    switch (d->head_dim) {
+        case 64: e = codec_levels<64>(d->levels, kind, d->is_key != 0, a, s); break;
+        case 128: e = codec_levels<128>(d->levels, kind, d->is_key != 0, a, s); break;
+        default: e = codec_levels<256>(d->levels, kind, d->is_key != 0, a, s); break;
+    }
+    NQ_CHECK_HIP(e);
+    return NQ_OK;
+}
+
+}  // namespace nq
+
+extern "C" int nq_dequantize(const nq_codes_desc* desc, void* stream) { return nq::run_codec(desc, 0, stream); }
+
+extern "C" int nq_codes_to_int8(const nq_codes_desc* desc, int32_t delta, void* stream) {
+    return nq::run_codec(desc, delta ? 2 : 1, stream);
+}
+
+extern "C" int nq_delta_decode(const uint64_t* deltas, const uint64_t* out, int32_t n_tensors, int32_t streams,
+                               int32_t seq, int32_t coords, void* stream) {
+    using namespace nq;
+    NQ_CHECK_ARG(deltas && out, "nq_delta_decode: NULL pointer array");
+    NQ_CHECK_ARG(n_tensors >= 0 && n_tensors <= 65535 && streams >= 0 && seq >= 0, "nq_delta_decode: bad shape");
+    NQ_CHECK_ARG(coords > 0 && coords % 4 == 0, "nq_delta_decode: coords must be a positive multiple of 4");
+    if (n_tensors == 0 || streams == 0 || seq == 0) return NQ_OK;
+    const uint64_t cols = (uint64_t)streams * (coords / 4);
+    NQ_CHECK_ARG(cols < (1ull << 31), "nq_delta_decode: too many streams");
+    dim3 grid((uint32_t)((cols + 255) / 256), (uint32_t)n_tensors);
+    hipLaunchKernelGGL(delta_decode_kernel, grid, dim3(256), 0, (hipStream_t)stream, deltas, out, (uint32_t)streams,
+                       (uint32_t)seq, (uint32_t)(coords / 4), (uint32_t)cols);
+    NQ_CHECK_HIP(hipGetLastError());
+    return NQ_OK;
+}

@@ -15,7 +15,7 @@
 // Arithmetic follows oracle/nq_spec.c step by step (no FMA contraction: the
 // file is compiled with -ffp-contract=off; the explicit fmaf calls below are
 // exact sign-folded butterflies or the correctly rounded division refinement).
-#include "nq_common.h"
+#include "nq_rowmath.h"
 
 namespace nq {
 
@@ -33,166 +33,6 @@ struct QuantArgs {
     uint32_t n_tensors, bh, work, per_xcd;  // work items = ceil(seq_out/64) * bh * n_tensors
     float hscale;
 };
-
-template <int L>
-struct SymBits {
-    static constexpr int value = L == 2 ? 2 : L == 4 ? 3 : L == 8 ? 4 : 5;
-};
-
-// ------------------------------------------------------------- loads ------
-
-template <int DT>
-__device__ __forceinline__ void load8(const void* base, int64_t elem_off, float* out) {
-    if constexpr (DT == NQ_F32) {
-        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem_off);
-        float4 a = p[0], b = p[1];
-        out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-        out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
-    } else {
-        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem_off);
-        uint4 w = *p;
-        uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if constexpr (DT == NQ_BF16) {
-                out[2 * k] = __builtin_bit_cast(float, ws[k] << 16);
-                out[2 * k + 1] = __builtin_bit_cast(float, ws[k] & 0xffff0000u);
-            } else {
-                out[2 * k] = f16_bits_to_f32(ws[k] & 0xffffu);
-                out[2 * k + 1] = f16_bits_to_f32(ws[k] >> 16);
-            }
-        }
-    }
-}
-
-__device__ __forceinline__ void load8f(const float* p, float* out) {
-    const float4* q = reinterpret_cast<const float4*>(p);
-    float4 a = q[0], b = q[1];
-    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
-}
-
-// ------------------------------------------------------------ Hadamard ----
-
-typedef __fp16 half2v __attribute__((ext_vector_type(2)));
-
-// Quad butterfly v <- v + c * partner(v) with the partner read through DPP in
-// the same v_fmac_f32 instruction.  The DPP read of a VGPR needs two wait
-// states after the VALU write that produced it; s_nop 1 provides them for the
-// first instruction, and the other seven read registers written before it.
-#define NQ_FMAC_DPP8(PERM, x, c)                                                       \
-    asm("s_nop 1\n\t"                                                                  \
-        "v_fmac_f32_dpp %0, %0, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-        "v_fmac_f32_dpp %1, %1, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-        "v_fmac_f32_dpp %2, %2, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-        "v_fmac_f32_dpp %3, %3, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-        "v_fmac_f32_dpp %4, %4, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-        "v_fmac_f32_dpp %5, %5, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-        "v_fmac_f32_dpp %6, %6, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-        "v_fmac_f32_dpp %7, %7, %8 " PERM " row_mask:0xf bank_mask:0xf bound_ctrl:1"     \
-        : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),       \
-          "+v"(x[6]), "+v"(x[7])                                                       \
-        : "v"(c))
-
-// Unnormalised Walsh-Hadamard over the quad's row.  Stage order follows
-// coordinate bits 0,1,2 (in chunk), 3,4 (across the quad), 5.. (across chunks).
-// The quad stages compute v + c * partner with c = +-1 per lane, the exact
-// butterfly up to a sign; every lane's values end multiplied by
-// sigma(q) = (-1)^popcount(q), which the caller folds into the next multiply.
-template <int C>
-__device__ __forceinline__ void fwht_row(float (&x)[C][8], int q) {
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-#pragma unroll
-        for (int len = 1; len < 8; len <<= 1) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                if (i & len) continue;
-                float a = x[c][i], b = x[c][i + len];
-                x[c][i] = a + b;
-                x[c][i + len] = a - b;
-            }
-        }
-    }
-    const float s3 = (q & 1) ? -1.0f : 1.0f;
-    const float s4 = (q & 2) ? -1.0f : 1.0f;
-#pragma unroll
-    for (int c = 0; c < C; ++c) NQ_FMAC_DPP8("quad_perm:[1,0,3,2]", x[c], s3);
-#pragma unroll
-    for (int c = 0; c < C; ++c) NQ_FMAC_DPP8("quad_perm:[2,3,0,1]", x[c], s4);
-#pragma unroll
-    for (int len = 1; len < C; len <<= 1) {
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            if (c & len) continue;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float a = x[c][i], b = x[c + len][i];
-                x[c][i] = a + b;
-                x[c + len][i] = a - b;
-            }
-        }
-    }
-}
-
-// The same transform on lattice points packed two per register as fp16
-// (coordinates 2k, 2k+1 of a chunk in register k).  Every value stays a
-// multiple of 1/2 of magnitude <= D*L/2 <= 1024, so fp16 holds it exactly and
-// the result equals the fp32 transform in any stage order.  Output carries the
-// same sigma(q) sign.
-template <int C>
-__device__ __forceinline__ void fwht_row_f16(half2v (&h)[C][4], int q) {
-    const half2v pm = {(__fp16)1.0f, (__fp16)-1.0f};
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) h[c][k] = __builtin_elementwise_fma(h[c][k], pm, h[c][k].yx);
-#pragma unroll
-        for (int len = 1; len < 4; len <<= 1) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (k & len) continue;
-                half2v a = h[c][k], b = h[c][k + len];
-                h[c][k] = a + b;
-                h[c][k + len] = a - b;
-            }
-        }
-    }
-    const __fp16 f3 = (q & 1) ? (__fp16)-1.0f : (__fp16)1.0f;
-    const __fp16 f4 = (q & 2) ? (__fp16)-1.0f : (__fp16)1.0f;
-    const half2v s3 = {f3, f3}, s4 = {f4, f4};
-#pragma unroll
-    for (int c = 0; c < C; ++c)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            half2v p = __builtin_bit_cast(half2v, dpp_u32<kQuadXor1>(__builtin_bit_cast(uint32_t, h[c][k])));
-            h[c][k] = __builtin_elementwise_fma(s3, p, h[c][k]);
-        }
-#pragma unroll
-    for (int c = 0; c < C; ++c)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            half2v p = __builtin_bit_cast(half2v, dpp_u32<kQuadXor2>(__builtin_bit_cast(uint32_t, h[c][k])));
-            h[c][k] = __builtin_elementwise_fma(s4, p, h[c][k]);
-        }
-#pragma unroll
-    for (int len = 1; len < C; len <<= 1) {
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            if (c & len) continue;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                half2v a = h[c][k], b = h[c + len][k];
-                h[c][k] = a + b;
-                h[c + len][k] = a - b;
-            }
-        }
-    }
-}
-
-__device__ __forceinline__ float quad_sign(int q) {
-    return ((q ^ (q >> 1)) & 1) ? -1.0f : 1.0f;
-}
 
 // ------------------------------------------------------------------ E8 ----
 

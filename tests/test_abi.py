@@ -8,6 +8,8 @@ import os
 import re
 import subprocess
 
+import pytest
+
 from nexusquant_amd import _lib
 from nexusquant_amd.build import LIB_PATH
 
@@ -34,20 +36,21 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert sorted(_lib.SIGNATURES) == names, "ctypes signature table out of sync with the header"
 
 
-def test_struct_layout_matches_the_c_compiler(tmp_path):
+@pytest.mark.parametrize("cname,pystruct", [("nq_quant_desc", _lib.QuantDesc), ("nq_codes_desc", _lib.CodesDesc)])
+def test_struct_layout_matches_the_c_compiler(tmp_path, cname, pystruct):
     """ctypes offsets of every descriptor field equal gcc's offsetof on the header."""
-    fields = [f[0] for f in _lib.QuantDesc._fields_]
+    fields = [f[0] for f in pystruct._fields_]
     prog = ["#include <stddef.h>", "#include <stdio.h>", f'#include "{HEADER}"', "int main(void){",
-            'printf("%zu\\n", sizeof(nq_quant_desc));']
-    prog += [f'printf("%zu\\n", offsetof(nq_quant_desc, {f}));' for f in fields]
+            f'printf("%zu\\n", sizeof({cname}));']
+    prog += [f'printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
     prog += ["return 0;}"]
     src = tmp_path / "layout.c"
     src.write_text("\n".join(prog))
     exe = tmp_path / "layout"
     subprocess.check_call(["gcc", "-o", str(exe), str(src)])
     out = [int(x) for x in subprocess.check_output([str(exe)]).split()]
-    assert out[0] == ctypes.sizeof(_lib.QuantDesc)
-    assert out[1:] == [getattr(_lib.QuantDesc, f).offset for f in fields]
+    assert out[0] == ctypes.sizeof(pystruct)
+    assert out[1:] == [getattr(pystruct, f).offset for f in fields]
 
 
 def test_abi_version_and_error_calls_need_no_gpu():

@@ -1,0 +1,81 @@
+"""GPU parity of the code kernels: dequantize, int8 2p codes, temporal deltas."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codes as C
+from oracle import spec as S
+from oracle import torch_ref as T
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _quant(D, L, key, dtype=torch.float16, shape=(2, 3, 150), seed=0):
+    from nexusquant_amd.ops import quantize_tensors
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, D, generator=g)
+    x[..., ::16] *= 6
+    x = x.to(dtype).to(DEV)
+    rec, cd = quantize_tensors([x], is_key=key, levels=L, rope_base=10000.0, codes=True)
+    return x, rec[0], cd[0]
+
+
+def _same_fp16(a, b):
+    a = a.cpu().numpy()
+    b = b.cpu().numpy()
+    diff = a.view(np.uint16) != b.view(np.uint16)
+    return bool(np.all(~diff | ((a == 0) & (b == 0))))
+
+
+@pytest.mark.parametrize("D,L,key", [(128, 8, True), (128, 4, False), (128, 2, True), (128, 16, False),
+                                     (64, 8, True), (256, 4, False), (256, 16, True)])
+def test_dequantize_reproduces_fused_reconstruction(D, L, key):
+    from nexusquant_amd.codec import dequantize
+    print(f"[gpu] dequant D={D} L={L} key={key}", flush=True)
+    _, rec, cd = _quant(D, L, key, seed=D + L)
+    out = dequantize([cd], rope_base=10000.0)[0]
+    torch.cuda.synchronize()
+    assert _same_fp16(out, rec)
+
+
+@pytest.mark.parametrize("D,L", [(128, 8), (128, 4), (128, 2), (256, 16), (64, 4)])
+def test_int8_codes_and_deltas_match_oracle(D, L):
+    from nexusquant_amd.codec import codes_int8, delta_decode
+    print(f"[gpu] int8 codes D={D} L={L}", flush=True)
+    x, rec, cd = _quant(D, L, False, seed=7 * D + L)
+    ref = S.quant_rows(x.float().cpu().numpy().reshape(-1, D), L)
+    two_p = C.codes_2p(ref["sym"], ref["coset"], L)
+    got = codes_int8([cd])[0].cpu().numpy().reshape(-1, D)
+    assert np.array_equal(got, two_p)
+    assert np.array_equal(got, T.lattice_codes_2p(torch.from_numpy(ref["p"])).numpy())
+    b, h, s = cd.scales.shape
+    d = codes_int8([cd], delta=True)[0]
+    want = C.delta_tokens(two_p.reshape(b * h, s, D))
+    assert np.array_equal(d.cpu().numpy().reshape(b * h, s, D), want)
+    back = delta_decode([d])[0].cpu().numpy().reshape(-1, D)
+    assert np.array_equal(back, two_p)
+    # vLLM dequant convention (code * 0.5) * scale equals the lattice point times the scale
+    sc = cd.scales.cpu().numpy().reshape(-1, 1)
+    assert np.array_equal((got.astype(np.float32) * 0.5) * sc, ref["p"] * sc)
+
+
+def test_nqc1_container_roundtrip_and_ratio():
+    from nexusquant_amd.codec import codes_int8, pack_nqc1, unpack_nqc1
+    print("[gpu] nqc1", flush=True)
+    layers = {}
+    for li in range(3):
+        _, _, ck = _quant(128, 8, True, shape=(1, 2, 300), seed=li)
+        _, _, cv = _quant(128, 4, False, shape=(1, 2, 300), seed=10 + li)
+        layers[li] = (ck, cv)
+    packed = pack_nqc1(layers, zstd_level=3)
+    assert packed["ratio"] > 3.0
+    out = unpack_nqc1(packed["blob"])
+    assert out["key_bits"] == 3 and out["value_bits"] == 2
+    for li in range(3):
+        for r in range(2):
+            want = codes_int8([layers[li][r]])[0]
+            assert torch.equal(out["codes"][2 * li + r].reshape(want.shape), want)
+            assert np.array_equal(out["scales"][2 * li + r].reshape(-1),
+                                  layers[li][r].scales.cpu().numpy().reshape(-1))
