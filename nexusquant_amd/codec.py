@@ -25,8 +25,10 @@ from .ops import PackedCodes, _addr, _ptr_arrays
 from .rope import device_table
 
 
-def _codes_desc(codes: Sequence[PackedCodes], outs: Sequence[torch.Tensor], rope=None) -> tuple:
+def _codes_desc(codes: Sequence[PackedCodes], outs: Sequence[torch.Tensor], rope=None,
+                head_dim=None) -> tuple:
     c0 = codes[0]
+    head_dim = c0.padded_dim if head_dim is None else head_dim
     b, h, s = c0.scales.shape
     for c in codes:
         if c.scales.shape != c0.scales.shape or c.levels != c0.levels or c.padded_dim != c0.padded_dim:
@@ -39,7 +41,7 @@ def _codes_desc(codes: Sequence[PackedCodes], outs: Sequence[torch.Tensor], rope
     if rope is not None:
         cos, sin = rope
         n_pos = cos.shape[0]
-    desc = _lib.CodesDesc(n_tensors=len(codes), batch=b, heads=h, seq=s, head_dim=c0.padded_dim,
+    desc = _lib.CodesDesc(n_tensors=len(codes), batch=b, heads=h, seq=s, head_dim=head_dim,
                           levels=c0.levels, is_key=int(rope is not None), syms=_addr(arrays[0]),
                           cosets=_addr(arrays[1]), scales=_addr(arrays[2]), out=_addr(arrays[3]),
                           rope_cos=_addr(cos), rope_sin=_addr(sin), rope_n_pos=n_pos,
@@ -55,13 +57,11 @@ def dequantize(codes: Sequence[PackedCodes], rope_base: float = 10000.0,
         return []
     c0 = codes[0]
     _lib.require_device(c0.scales, "codes")
-    if c0.head_dim != c0.padded_dim:
-        raise NotImplementedError("dequantize of padded head dims is not supported yet")
     b, h, s = c0.scales.shape
     dev = c0.scales.device
     outs = [torch.empty(b, h, s, c0.head_dim, dtype=torch.float16, device=dev) for _ in codes]
     rope = device_table(s, c0.head_dim, rope_base, rope_scaling, dev) if c0.is_key else None
-    desc, keep_alive = _codes_desc(codes, outs, rope)
+    desc, keep_alive = _codes_desc(codes, outs, rope, head_dim=c0.head_dim)
     with torch.cuda.device(dev):
         st = lib.nq_dequantize(ctypes.byref(desc), ctypes.c_void_p(_lib.current_stream_handle(dev)))
     _lib.check(st, "nq_dequantize")

@@ -74,10 +74,10 @@ __device__ __forceinline__ void unpack_points(const CodecArgs& a, uint32_t tenso
     }
 }
 
-template <int D, int L, bool IS_KEY>
+template <int D, int L, bool IS_KEY, int DR>
 __global__ __launch_bounds__(256) void dequant_kernel(CodecArgs a) {
     constexpr int C = D / 32;
-    constexpr int HALF = D / 2;
+    constexpr int RC = RopeChunks<D, DR>::value;
     const int q = threadIdx.x & 3;
     const uint32_t w = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
     if (w >= a.work) return;
@@ -118,29 +118,19 @@ __global__ __launch_bounds__(256) void dequant_kernel(CodecArgs a) {
             for (int i = 0; i < 8; ++i) x[c][i] = x[c][i] * g;
     }
     if constexpr (IS_KEY) {
-        const float* ct = a.rope_cos + (size_t)t * HALF;
-        const float* st = a.rope_sin + (size_t)t * HALF;
-#pragma unroll
-        for (int c = 0; c < C / 2; ++c) {
-            float cs[8], sn[8];
-            load8f(ct + 32 * c + 8 * q, cs);
-            load8f(st + 32 * c + 8 * q, sn);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float lo = x[c][i], hi = x[c + C / 2][i];
-                x[c][i] = __builtin_fmaf(lo, cs[i], -(hi * sn[i]));
-                x[c + C / 2][i] = __builtin_fmaf(lo, sn[i], hi * cs[i]);
-            }
-        }
+        float cs[RC][8], sn[RC][8];
+        load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t, q, cs, sn);
+        apply_rope<D, DR, RC, false>(x, q, cs, sn);
     }
 #pragma unroll
     for (int c = 0; c < C; ++c)
 #pragma unroll
         for (int i = 0; i < 8; ++i) asm("" : "+v"(x[c][i]));  // keep the fp32 rounding (see quantizer)
     if (!active) return;
-    half2v* dst = reinterpret_cast<half2v*>(reinterpret_cast<uint16_t*>(a.out[tensor]) + row * D);
+    half2v* dst = reinterpret_cast<half2v*>(reinterpret_cast<uint16_t*>(a.out[tensor]) + row * DR);
 #pragma unroll
     for (int c = 0; c < C; ++c) {
+        if (32 * c >= DR) continue;
         uint4 o;
         half2v h0 = {(__fp16)x[c][0], (__fp16)x[c][1]}, h1 = {(__fp16)x[c][2], (__fp16)x[c][3]};
         half2v h2 = {(__fp16)x[c][4], (__fp16)x[c][5]}, h3 = {(__fp16)x[c][6], (__fp16)x[c][7]};
@@ -227,12 +217,12 @@ __global__ __launch_bounds__(256) void delta_decode_kernel(const uint64_t* delta
     }
 }
 
-template <int D, int L>
+template <int D, int L, int DR>
 static hipError_t launch_codec(int kind, bool key, const CodecArgs& a, hipStream_t s) {
     dim3 grid(a.per_xcd * 8u);
     if (kind == 0) {
-        if (key) hipLaunchKernelGGL((dequant_kernel<D, L, true>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((dequant_kernel<D, L, false>), grid, dim3(256), 0, s, a);
+        if (key) hipLaunchKernelGGL((dequant_kernel<D, L, true, DR>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((dequant_kernel<D, L, false, DR>), grid, dim3(256), 0, s, a);
     } else if (kind == 1) {
         hipLaunchKernelGGL((int8_codes_kernel<D, L, false>), grid, dim3(256), 0, s, a);
     } else {
@@ -241,13 +231,13 @@ static hipError_t launch_codec(int kind, bool key, const CodecArgs& a, hipStream
     return hipGetLastError();
 }
 
-template <int D>
+template <int D, int DR = D>
 static hipError_t codec_levels(int L, int kind, bool key, const CodecArgs& a, hipStream_t s) {
     switch (L) {
-        case 2: return launch_codec<D, 2>(kind, key, a, s);
-        case 4: return launch_codec<D, 4>(kind, key, a, s);
-        case 8: return launch_codec<D, 8>(kind, key, a, s);
-        default: return launch_codec<D, 16>(kind, key, a, s);
+        case 2: return launch_codec<D, 2, DR>(kind, key, a, s);
+        case 4: return launch_codec<D, 4, DR>(kind, key, a, s);
+        case 8: return launch_codec<D, 8, DR>(kind, key, a, s);
+        default: return launch_codec<D, 16, DR>(kind, key, a, s);
     }
 }
 
@@ -255,8 +245,8 @@ static int run_codec(const nq_codes_desc* d, int kind, void* stream) {
     NQ_CHECK_ARG(d != nullptr, "nq codes: desc is NULL");
     NQ_CHECK_ARG(d->n_tensors >= 0 && d->n_tensors <= 65535, "nq codes: n_tensors out of range");
     if (d->n_tensors == 0 || d->seq == 0) return NQ_OK;
-    NQ_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128 || d->head_dim == 256,
-                 "nq codes: head_dim %d unsupported (64, 128, 256)", d->head_dim);
+    NQ_CHECK_ARG(d->head_dim == 64 || d->head_dim == 96 || d->head_dim == 128 || d->head_dim == 256,
+                 "nq codes: head_dim %d unsupported (64, 96, 128, 256)", d->head_dim);
     NQ_CHECK_ARG(d->levels == 2 || d->levels == 4 || d->levels == 8 || d->levels == 16,
                  "nq codes: levels must be 2, 4, 8 or 16");
     NQ_CHECK_ARG(d->batch > 0 && d->heads > 0 && d->seq > 0, "nq codes: bad geometry");
@@ -286,6 +276,7 @@ static int run_codec(const nq_codes_desc* d, int kind, void* stream) {
     hipError_t e;
     switch (d->head_dim) {
         case 64: e = codec_levels<64>(d->levels, kind, d->is_key != 0, a, s); break;
+        case 96: e = codec_levels<128, 96>(d->levels, kind, d->is_key != 0, a, s); break;
         case 128: e = codec_levels<128>(d->levels, kind, d->is_key != 0, a, s); break;
         default: e = codec_levels<256>(d->levels, kind, d->is_key != 0, a, s); break;
     }

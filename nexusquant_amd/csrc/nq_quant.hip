@@ -130,10 +130,10 @@ __device__ __forceinline__ void store_symbols(uint8_t* row_syms, int q, const fl
 
 // -------------------------------------------------------------- kernel ----
 
-template <int D, int L, bool IS_KEY, int DT>
+template <int D, int L, bool IS_KEY, int DT, int DR>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     constexpr int C = D / 32;
-    constexpr int HALF = D / 2;
+    constexpr int RC = RopeChunks<D, DR>::value;
     const int q = threadIdx.x & 3;
     // Block -> work item.  Consecutive block ids go round-robin to the 8 XCDs, so
     // block 8k + x takes work item x * per_xcd + k: each XCD walks a contiguous
@@ -161,9 +161,16 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
 
     float x[C][8];
     const void* src = reinterpret_cast<const void*>(a.src[tensor]);
-    const int64_t in_off = ((int64_t)bh * a.seq_in + t_in) * D;
+    const int64_t in_off = ((int64_t)bh * a.seq_in + t_in) * DR;
 #pragma unroll
-    for (int c = 0; c < C; ++c) load8<DT>(src, in_off + 32 * c + 8 * q, x[c]);
+    for (int c = 0; c < C; ++c) {
+        if (32 * c < DR) {
+            load8<DT>(src, in_off + 32 * c + 8 * q, x[c]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[c][i] = 0.0f;  // zero padding to D
+        }
+    }
     if (!keep) {
 #pragma unroll
         for (int c = 0; c < C; ++c)
@@ -171,24 +178,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
             for (int i = 0; i < 8; ++i) x[c][i] = 0.0f;
     }
 
-    float cs[C / 2][8], sn[C / 2][8];
+    float cs[RC][8], sn[RC][8];
     if constexpr (IS_KEY) {
-        const float* ct = a.rope_cos + (size_t)t_in * HALF;
-        const float* st = a.rope_sin + (size_t)t_in * HALF;
-#pragma unroll
-        for (int c = 0; c < C / 2; ++c) {
-            load8f(ct + 32 * c + 8 * q, cs[c]);
-            load8f(st + 32 * c + 8 * q, sn[c]);
-        }
-#pragma unroll
-        for (int c = 0; c < C / 2; ++c) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float lo = x[c][i], hi = x[c + C / 2][i];
-                x[c][i] = lo * cs[c][i] + hi * sn[c][i];
-                x[c + C / 2][i] = (-lo) * sn[c][i] + hi * cs[c][i];
-            }
-        }
+        load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t_in, q, cs, sn);
+        apply_rope<D, DR, RC, true>(x, q, cs, sn);
     }
 
     fwht_row<C>(x, q);
@@ -269,27 +262,11 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     }
 
     if constexpr (IS_KEY) {
-        if (a.gather && t_out != t_in) {
-            const float* ct = a.rope_cos + (size_t)t_out * HALF;
-            const float* st = a.rope_sin + (size_t)t_out * HALF;
-#pragma unroll
-            for (int c = 0; c < C / 2; ++c) {
-                load8f(ct + 32 * c + 8 * q, cs[c]);
-                load8f(st + 32 * c + 8 * q, sn[c]);
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < C / 2; ++c) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float lo = x[c][i], hi = x[c + C / 2][i];
-                x[c][i] = __builtin_fmaf(lo, cs[c][i], -(hi * sn[c][i]));
-                x[c + C / 2][i] = __builtin_fmaf(lo, sn[c][i], hi * cs[c][i]);
-            }
-        }
+        if (a.gather && t_out != t_in) load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t_out, q, cs, sn);
+        apply_rope<D, DR, RC, false>(x, q, cs, sn);
     }
     if (!active) return;
-    half2v* dst = reinterpret_cast<half2v*>(reinterpret_cast<uint16_t*>(a.recon[tensor]) + out_row * D);
+    half2v* dst = reinterpret_cast<half2v*>(reinterpret_cast<uint16_t*>(a.recon[tensor]) + out_row * DR);
     // The fp32 result is rounded to fp16 in a second step, as the reference does
     // (fp32 tensor, then .half()).  The empty asm pins the fp32 value: without it
     // the backend folds fma + convert into v_fma_mix{lo,hi}_f16, which rounds
@@ -300,6 +277,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
         for (int i = 0; i < 8; ++i) asm("" : "+v"(x[c][i]));
 #pragma unroll
     for (int c = 0; c < C; ++c) {
+        if (32 * c >= DR) continue;  // padding coordinates are not part of the output
         half2v o[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) o[k] = half2v{(__fp16)x[c][2 * k], (__fp16)x[c][2 * k + 1]};
@@ -314,35 +292,35 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
 
 // ---------------------------------------------------------------- host ----
 
-template <int D, int L, bool K, int DT>
+template <int D, int L, bool K, int DT, int DR>
 static hipError_t launch_quant(const QuantArgs& a, uint32_t n_tensors, hipStream_t s) {
     (void)n_tensors;
     dim3 grid(a.per_xcd * 8u);
-    hipLaunchKernelGGL((quant_rows_kernel<D, L, K, DT>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((quant_rows_kernel<D, L, K, DT, DR>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
-template <int D, int L, bool K>
+template <int D, int L, bool K, int DR>
 static hipError_t dispatch_dtype(int dt, const QuantArgs& a, uint32_t n, hipStream_t s) {
     switch (dt) {
-        case NQ_F16: return launch_quant<D, L, K, NQ_F16>(a, n, s);
-        case NQ_BF16: return launch_quant<D, L, K, NQ_BF16>(a, n, s);
-        default: return launch_quant<D, L, K, NQ_F32>(a, n, s);
+        case NQ_F16: return launch_quant<D, L, K, NQ_F16, DR>(a, n, s);
+        case NQ_BF16: return launch_quant<D, L, K, NQ_BF16, DR>(a, n, s);
+        default: return launch_quant<D, L, K, NQ_F32, DR>(a, n, s);
     }
 }
 
-template <int D, int L>
+template <int D, int L, int DR>
 static hipError_t dispatch_key(bool key, int dt, const QuantArgs& a, uint32_t n, hipStream_t s) {
-    return key ? dispatch_dtype<D, L, true>(dt, a, n, s) : dispatch_dtype<D, L, false>(dt, a, n, s);
+    return key ? dispatch_dtype<D, L, true, DR>(dt, a, n, s) : dispatch_dtype<D, L, false, DR>(dt, a, n, s);
 }
 
-template <int D>
+template <int D, int DR = D>
 static hipError_t dispatch_levels(int L, bool key, int dt, const QuantArgs& a, uint32_t n, hipStream_t s) {
     switch (L) {
-        case 2: return dispatch_key<D, 2>(key, dt, a, n, s);
-        case 4: return dispatch_key<D, 4>(key, dt, a, n, s);
-        case 8: return dispatch_key<D, 8>(key, dt, a, n, s);
-        default: return dispatch_key<D, 16>(key, dt, a, n, s);
+        case 2: return dispatch_key<D, 2, DR>(key, dt, a, n, s);
+        case 4: return dispatch_key<D, 4, DR>(key, dt, a, n, s);
+        case 8: return dispatch_key<D, 8, DR>(key, dt, a, n, s);
+        default: return dispatch_key<D, 16, DR>(key, dt, a, n, s);
     }
 }
 
@@ -353,8 +331,8 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     NQ_CHECK_ARG(d != nullptr, "nq_quantize: desc is NULL");
     NQ_CHECK_ARG(d->n_tensors >= 0 && d->n_tensors <= 65535, "nq_quantize: n_tensors %d out of range", d->n_tensors);
     if (d->n_tensors == 0) return NQ_OK;
-    NQ_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128 || d->head_dim == 256,
-                 "nq_quantize: head_dim %d unsupported by this entry point (64, 128, 256)", d->head_dim);
+    NQ_CHECK_ARG(d->head_dim == 64 || d->head_dim == 96 || d->head_dim == 128 || d->head_dim == 256,
+                 "nq_quantize: head_dim %d unsupported by this entry point (64, 96, 128, 256)", d->head_dim);
     NQ_CHECK_ARG(d->levels == 2 || d->levels == 4 || d->levels == 8 || d->levels == 16,
                  "nq_quantize: levels must be 2, 4, 8 or 16 (got %d)", d->levels);
     NQ_CHECK_ARG(d->dtype == NQ_F16 || d->dtype == NQ_BF16 || d->dtype == NQ_F32,
@@ -399,6 +377,7 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     hipError_t e;
     switch (d->head_dim) {
         case 64: e = dispatch_levels<64>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
+        case 96: e = dispatch_levels<128, 96>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
         case 128: e = dispatch_levels<128>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
         default: e = dispatch_levels<256>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
     }

@@ -167,4 +167,88 @@ __device__ __forceinline__ float quad_sign(int q) {
     return ((q ^ (q >> 1)) & 1) ? -1.0f : 1.0f;
 }
 
+// ------------------------------------------------------------------ RoPE ----
+//
+// Split-half RoPE pairs coordinate i with i + DR/2 (DR = real head dim).  With
+// DR == D the pair is chunk c and c + C/2 of the same lane.  With DR = 96
+// padded to D = 128 the partner of every live coordinate sits in quad lane
+// q ^ 2: for q < 2 chunks (0, 1, 2) pair with that lane's chunks (1, 2, 0), for
+// q >= 2 with (2, 0, 1); chunk 3 is padding.  rope_col gives the table column
+// of the pair's first coordinate for each of the lane's RoPE chunks.
+
+template <int D, int DR>
+struct RopeChunks {
+    static constexpr int value = DR == D ? D / 64 : 3;
+};
+
+template <int D, int DR>
+__device__ __forceinline__ int rope_col(int c, int q) {
+    if constexpr (DR == D) {
+        return 32 * c + 8 * q;
+    } else {
+        static_assert(D == 128 && DR == 96, "padded RoPE layout implemented for 96 -> 128");
+        const bool lowq = q < 2;
+        return c == 0 ? 8 * q : (c == 1 ? (lowq ? 32 + 8 * q : 8 * (q - 2)) : (lowq ? 16 + 8 * q : 32 + 8 * (q - 2)));
+    }
+}
+
+template <int D, int DR, int RC>
+__device__ __forceinline__ void load_rope(const float* cos_t, const float* sin_t, uint32_t pos, int q,
+                                          float (&cs)[RC][8], float (&sn)[RC][8]) {
+    const float* ct = cos_t + (size_t)pos * (DR / 2);
+    const float* st = sin_t + (size_t)pos * (DR / 2);
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+        load8f(ct + rope_col<D, DR>(c, q), cs[c]);
+        load8f(st + rope_col<D, DR>(c, q), sn[c]);
+    }
+}
+
+// INVERSE (input side, reference rounding): lo' = lo*c + hi*s, hi' = (-lo)*s + hi*c.
+// Forward (output side): lo' = fma(lo, c, -(hi*s)), hi' = fma(lo, s, hi*c).
+template <int D, int DR, int RC, bool INVERSE>
+__device__ __forceinline__ void apply_rope(float (&x)[D / 32][8], int q, const float (&cs)[RC][8],
+                                           const float (&sn)[RC][8]) {
+    constexpr int C = D / 32;
+    if constexpr (DR == D) {
+#pragma unroll
+        for (int c = 0; c < C / 2; ++c) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float lo = x[c][i], hi = x[c + C / 2][i];
+                if constexpr (INVERSE) {
+                    x[c][i] = lo * cs[c][i] + hi * sn[c][i];
+                    x[c + C / 2][i] = (-lo) * sn[c][i] + hi * cs[c][i];
+                } else {
+                    x[c][i] = __builtin_fmaf(lo, cs[c][i], -(hi * sn[c][i]));
+                    x[c + C / 2][i] = __builtin_fmaf(lo, sn[c][i], hi * cs[c][i]);
+                }
+            }
+        }
+    } else {
+        float P[3][8];
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) P[c][i] = dpp_f32<kQuadXor2>(x[c][i]);
+        const bool lowq = q < 2;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const bool is_lo = c == 0 || (c == 1 && lowq);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float p = c == 0 ? (lowq ? P[1][i] : P[2][i])
+                                       : (c == 1 ? (lowq ? P[2][i] : P[0][i]) : (lowq ? P[0][i] : P[1][i]));
+                const float v = x[c][i];
+                if constexpr (INVERSE) {
+                    x[c][i] = is_lo ? (v * cs[c][i] + p * sn[c][i]) : ((-p) * sn[c][i] + v * cs[c][i]);
+                } else {
+                    x[c][i] = is_lo ? __builtin_fmaf(v, cs[c][i], -(p * sn[c][i]))
+                                    : __builtin_fmaf(p, sn[c][i], v * cs[c][i]);
+                }
+            }
+        }
+    }
+}
+
 }  // namespace nq

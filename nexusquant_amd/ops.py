@@ -87,8 +87,8 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
     if levels not in SYM_BITS:
         raise ValueError(f"levels must be 2, 4, 8 or 16, got {levels}")
     D = next_power_of_2(d)
-    if D != d or d not in (64, 128, 256):
-        raise NotImplementedError(f"head_dim {d} is not supported by the fused kernel yet")
+    if d not in (64, 96, 128, 256):
+        raise NotImplementedError(f"head_dim {d} is not supported by the fused kernel (64, 96, 128, 256)")
     dev = t0.device
     # contiguous and 16-byte aligned (the kernel reads 16-byte vectors)
     src = [t.contiguous() for t in tensors]

@@ -30,7 +30,8 @@ def _same_fp16(a, b):
 
 
 @pytest.mark.parametrize("D,L,key", [(128, 8, True), (128, 4, False), (128, 2, True), (128, 16, False),
-                                     (64, 8, True), (256, 4, False), (256, 16, True)])
+                                     (64, 8, True), (256, 4, False), (256, 16, True), (96, 4, True),
+                                     (96, 8, False)])
 def test_dequantize_reproduces_fused_reconstruction(D, L, key):
     from nexusquant_amd.codec import dequantize
     print(f"[gpu] dequant D={D} L={L} key={key}", flush=True)

@@ -93,7 +93,10 @@ CASES = [(128, L, key, torch.float16) for L in (2, 4, 8, 16) for key in (True, F
 CASES += [(64, 8, True, torch.float16), (64, 4, False, torch.float16),
           (256, 8, True, torch.float16), (256, 4, False, torch.float16),
           (128, 8, True, torch.bfloat16), (128, 4, False, torch.bfloat16),
-          (128, 8, True, torch.float32)]
+          (128, 8, True, torch.float32),
+          # head_dim 96 zero-padded to 128 (Phi-3-mini shape; the reference raises here)
+          (96, 4, True, torch.float16), (96, 4, False, torch.float16), (96, 8, True, torch.bfloat16),
+          (96, 16, True, torch.float32)]
 
 
 @pytest.mark.parametrize("D,L,key,dtype", CASES)
@@ -127,16 +130,17 @@ def test_quantizer_far_positions_and_llama3_scaling():
                           ref["scale"])
 
 
-def test_gather_truncation_path_bitexact():
-    print("[gpu] gather", flush=True)
-    x = _inputs((1, 4, 300, 128), torch.float16, seed=9)
+@pytest.mark.parametrize("d", [128, 96])
+def test_gather_truncation_path_bitexact(d):
+    print(f"[gpu] gather d={d}", flush=True)
+    x = _inputs((1, 4, 300, d), torch.float16, seed=9)
     kept = np.sort(np.random.default_rng(1).choice(300, 173, replace=False)).astype(np.int32)
     kept[0] = 0
     g = torch.from_numpy(kept)[None, :]
     for key, L in ((True, 8), (False, 4)):
         rec, cd = gpu_quant(x.to(DEV), L, key, rope_base=10000.0, gather=g.to(DEV))
         ref = spec_tensor(x.float().numpy(), L, key, 10000.0, gather=kept[None, :])
-        assert rec.shape == (1, 4, 173, 128)
+        assert rec.shape == (1, 4, 173, d)
         assert_bitexact(rec, cd, ref, L)
 
 
