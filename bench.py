@@ -84,13 +84,133 @@ def cpu_baseline(keys, values, torch):
                       f"{t_total:.1f} s); Tier-A torch restatement of the reference, same inputs"}
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def _aux_cache(torch, gen, dev, layers, b, h, s, d, base, sink):
+    """Synthetic fp16 cache with the BASELINE distribution (keys post-RoPE)."""
+    from nexusquant_amd.rope import device_table
+    ks, vs = [], []
+    cos, sin = device_table(s, d, base, None, dev)
+    c, sn = cos[:s], sin[:s]
+    for _ in range(layers):
+        kp = torch.randn(b, h, s, d, device=dev, generator=gen)
+        idx = torch.argsort(torch.rand(h, d, device=dev, generator=gen), dim=1)[:, :4]
+        scale = torch.ones(h, d, device=dev)
+        scale.scatter_(1, idx, 8.0)
+        kp *= scale[None, :, None, :]
+        if sink:
+            kp[:, :, 0, :] *= 4
+        lo, hi = kp[..., :d // 2], kp[..., d // 2:]
+        ks.append(torch.cat([lo * c - hi * sn, lo * sn + hi * c], dim=-1).half())
+        vs.append((torch.randn(b, h, s, d, device=dev, generator=gen) * 0.5).half())
+    return ks, vs
+
+
+def _timed(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def aux_workload(name, steps, warmup):
+    """Secondary configs (BASELINE.json configs[2..4]); one JSON line each."""
+    import torch
+    import nexusquant_amd as nq
+    from nexusquant_amd.scoring import score_real_accumulate
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+
+    class Cache:
+        def __init__(self, ks, vs):
+            self.key_cache, self.value_cache = list(ks), list(vs)
+
+    out = {"metric": f"aux {name}", "unit": "ms", "higher_is_better": False, "n_gpus": 1,
+           "data": "synthetic", "steps": steps, "warmup": warmup}
+    if name == "copy":
+        # calibration for the HBM byte counters: a plain device copy of known size
+        n = 4 << 30
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        ms = _timed(torch, lambda: dst.copy_(src), steps, warmup) * 1e3
+        out.update(config={"workload": f"device copy of {n} bytes (read {n}, write {n})"},
+                   ms_per_step=round(ms, 3), value=round(ms, 3), bytes_read=n, bytes_written=n,
+                   copy_gbs=round(2 * n / (ms * 1e-3) / 1e9, 1))
+    elif name == "c3":
+        ks, vs = _aux_cache(torch, gen, dev, 32, 4, 8, 8192, 128, 10000.0, True)
+        comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.25, sliding_window=32,
+                                  obs_window=32, rope_base=10000.0)
+        score_ms = _timed(torch, lambda: comp._score_importance(ks[0]), steps, warmup) * 1e3
+        step_ms = _timed(torch, lambda: comp.compress(Cache(ks, vs)), steps, warmup) * 1e3
+        elems = 2 * 32 * 4 * 8 * 8192 * 128
+        out.update(config={"workload": "light eviction, key-key scorer: Mistral-7B shape, 32 layers x K,V fp16 "
+                           "[4, 8, 8192, 128], 25% eviction, BOS + last 32 kept, K3V2 on survivors"},
+                   ms_per_step=round(step_ms, 3), value=round(step_ms, 3),
+                   keykey_score_ms=round(score_ms, 4),
+                   keykey_score_gbs=round(4 * 8 * 8192 * 128 * 2 / (score_ms * 1e-3) / 1e9, 1),
+                   gbs_fp16_compressed=round(2 * elems / (step_ms * 1e-3) / 1e9, 1))
+    elif name == "c4":
+        s, hq, hkv, d, layers = 8192, 32, 8, 128, 32
+        qs = [torch.randn(1, hq, s, d, device=dev, generator=gen).half() for _ in range(layers)]
+        ks, vs = _aux_cache(torch, gen, dev, layers, 1, hkv, s, d, 10000.0, True)
+
+        def score():
+            imp = torch.zeros(1, s, device=dev)
+            for q, k in zip(qs, ks):
+                score_real_accumulate(q, k, imp, d ** -0.5)
+            return imp / layers
+        score_ms = _timed(torch, score, steps, warmup) * 1e3
+        imp = score()
+        comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.35, sliding_window=32,
+                                  rope_base=10000.0, scorer="real", protect_boundary=2)
+        comp._score_importance = lambda k, _imp=imp: _imp
+        step_ms = _timed(torch, lambda: comp.compress(Cache(ks, vs)), steps, warmup) * 1e3
+        flops = layers * 2 * (2 * hq * d * s * (s + 1) / 2)
+        tflops = flops / (score_ms * 1e-3) / 1e12
+        out.update(config={"workload": "real-attention scorer: Q fp16 [1, 32, 8192, 128], GQA 4 vs K,V "
+                           "[1, 8, 8192, 128], causal, 32 layers; 35% eviction, boundary 2, K3V2"},
+                   ms_per_step=round(score_ms + step_ms, 3), value=round(score_ms + step_ms, 3),
+                   real_score_ms=round(score_ms, 3), evict_quant_ms=round(step_ms, 3),
+                   roofline={"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                             "algorithmic_flops": flops,
+                             "note": "two causal QK^T passes per layer (the kernel runs three sweeps)"})
+    elif name in ("c5a", "c5b"):
+        if name == "c5a":
+            layers, h, d, rate, desc = 32, 32, 96, 0.60, "Phi-3-mini shape, 32 layers x K,V fp16 [1, 32, 16384, 96]"
+        else:
+            layers, h, d, rate, desc = 26, 4, 256, 0.80, "Gemma-2-2b shape, 26 layers x K,V fp16 [1, 4, 16384, 256]"
+        ks, vs = _aux_cache(torch, gen, dev, layers, 1, h, 16384, d, 10000.0, True)
+        comp = nq.NexusQuantEvict(bits=2, eviction_rate=rate, sliding_window=32, rope_base=10000.0)
+        step_ms = _timed(torch, lambda: comp.compress(Cache(ks, vs)), steps, warmup) * 1e3
+        elems = 2 * layers * h * 16384 * d
+        out.update(config={"workload": f"{desc}, K2V2, {int(rate * 100)}% key-key eviction"},
+                   ms_per_step=round(step_ms, 3), value=round(step_ms, 3),
+                   gbs_fp16_compressed=round(2 * elems / (step_ms * 1e-3) / 1e9, 1))
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="c2",
+                    help="c2 (headline, default), a secondary config: c3, c4, c5a, c5b, aux (all four), "
+                         "or copy (HBM counter calibration)")
     args = ap.parse_args()
+    if args.workload != "c2":
+        for w in (["c3", "c4", "c5a", "c5b"] if args.workload == "aux" else [args.workload]):
+            aux_workload(w, args.steps, args.warmup)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the compression path is data-parallel per layer "
               "and head, and this build runs on single-GPU boxes (see DESIGN.md, sharding).",
