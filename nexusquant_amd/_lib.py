@@ -13,6 +13,7 @@ import threading
 from .build import LIB_PATH
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
+ABI_VERSION = 1  # NQ_ABI_VERSION of the header these bindings mirror
 _P = ctypes.c_void_p
 
 
@@ -88,6 +89,10 @@ def load():
                 fn = getattr(lib, name)
                 fn.argtypes = args
                 fn.restype = res
+            if lib.nq_abi_version() != ABI_VERSION:
+                raise NexusQuantError(
+                    f"{LIB_PATH} has ABI version {lib.nq_abi_version()}, the bindings expect "
+                    f"{ABI_VERSION}; rebuild with `python -m nexusquant_amd.build`")
             _lib = lib
     return _lib
 
