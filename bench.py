@@ -18,6 +18,7 @@ the host, on layers {0, 40, 79} (a bounded sample), scaled to the same unit.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -241,12 +242,25 @@ def main():
                                       launch_events=ev)
         return rk, ck, rv, cv
 
+    # Setup: one untimed priming step builds the RoPE table, the address ring
+    # and the allocator pools, so the W warmup steps start from a running GPU.
+    out = step()
+    del out
+    # timing events: the runtime builds an event at its first record, so every
+    # event is recorded once here, outside the timed region
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for e4 in ev:
+        for e in e4:
+            e.record()
+    torch.cuda.synchronize()
+    # A full collection of the harness's heap (torch, the 160 input tensors)
+    # takes ~40 ms of host time; collect now and freeze the survivors so no
+    # generation-2 pass lands inside the timed steps and starves the GPU queue.
+    gc.collect()
+    gc.freeze()
     for _ in range(args.warmup):
         out = step()
         del out
-    torch.cuda.synchronize()
-
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):

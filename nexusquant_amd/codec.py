@@ -21,7 +21,7 @@ import torch
 
 from . import _lib
 from .hadamard import hadamard_constant
-from .ops import PackedCodes, _addr, _ptr_arrays
+from .ops import PackedCodes, _addr, _PtrArrays
 from .rope import device_table
 
 
@@ -34,8 +34,9 @@ def _codes_desc(codes: Sequence[PackedCodes], outs: Sequence[torch.Tensor], rope
         if c.scales.shape != c0.scales.shape or c.levels != c0.levels or c.padded_dim != c0.padded_dim:
             raise ValueError("all codes of one launch must share shape and levels")
     dev = c0.scales.device
-    arrays = _ptr_arrays([[c.syms for c in codes], [c.cosets for c in codes], [c.scales for c in codes],
-                          list(outs)], dev)
+    staged = _PtrArrays([[c.syms for c in codes], [c.cosets for c in codes], [c.scales for c in codes],
+                         list(outs)], dev)
+    arrays = staged.arrays
     cos = sin = None
     n_pos = 0
     if rope is not None:
@@ -46,7 +47,7 @@ def _codes_desc(codes: Sequence[PackedCodes], outs: Sequence[torch.Tensor], rope
                           cosets=_addr(arrays[1]), scales=_addr(arrays[2]), out=_addr(arrays[3]),
                           rope_cos=_addr(cos), rope_sin=_addr(sin), rope_n_pos=n_pos,
                           hadamard_scale=hadamard_constant(c0.padded_dim))
-    return desc, arrays
+    return desc, staged
 
 
 def dequantize(codes: Sequence[PackedCodes], rope_base: float = 10000.0,
@@ -61,9 +62,12 @@ def dequantize(codes: Sequence[PackedCodes], rope_base: float = 10000.0,
     dev = c0.scales.device
     outs = [torch.empty(b, h, s, c0.head_dim, dtype=torch.float16, device=dev) for _ in codes]
     rope = device_table(s, c0.head_dim, rope_base, rope_scaling, dev) if c0.is_key else None
-    desc, keep_alive = _codes_desc(codes, outs, rope, head_dim=c0.head_dim)
+    desc, staged = _codes_desc(codes, outs, rope, head_dim=c0.head_dim)
     with torch.cuda.device(dev):
-        st = lib.nq_dequantize(ctypes.byref(desc), ctypes.c_void_p(_lib.current_stream_handle(dev)))
+        try:
+            st = lib.nq_dequantize(ctypes.byref(desc), ctypes.c_void_p(_lib.current_stream_handle(dev)))
+        finally:
+            staged.release()
     _lib.check(st, "nq_dequantize")
     return outs
 
@@ -78,9 +82,13 @@ def codes_int8(codes: Sequence[PackedCodes], delta: bool = False) -> List[torch.
     b, h, s = c0.scales.shape
     dev = c0.scales.device
     outs = [torch.empty(b, h, s, c0.padded_dim, dtype=torch.int8, device=dev) for _ in codes]
-    desc, keep_alive = _codes_desc(codes, outs)
+    desc, staged = _codes_desc(codes, outs)
     with torch.cuda.device(dev):
-        st = lib.nq_codes_to_int8(ctypes.byref(desc), int(delta), ctypes.c_void_p(_lib.current_stream_handle(dev)))
+        try:
+            st = lib.nq_codes_to_int8(ctypes.byref(desc), int(delta),
+                                      ctypes.c_void_p(_lib.current_stream_handle(dev)))
+        finally:
+            staged.release()
     _lib.check(st, "nq_codes_to_int8")
     return outs
 
@@ -95,10 +103,14 @@ def delta_decode(deltas: Sequence[torch.Tensor]) -> List[torch.Tensor]:
     b, h, s, D = d0.shape
     src = [d.contiguous() for d in deltas]
     outs = [torch.empty_like(d) for d in src]
-    arrs = _ptr_arrays([src, outs], d0.device)
+    staged = _PtrArrays([src, outs], d0.device)
+    arrs = staged.arrays
     with torch.cuda.device(d0.device):
-        st = lib.nq_delta_decode(_addr(arrs[0]), _addr(arrs[1]), len(src), b * h, s, D,
-                                 ctypes.c_void_p(_lib.current_stream_handle(d0.device)))
+        try:
+            st = lib.nq_delta_decode(_addr(arrs[0]), _addr(arrs[1]), len(src), b * h, s, D,
+                                     ctypes.c_void_p(_lib.current_stream_handle(d0.device)))
+        finally:
+            staged.release()
     _lib.check(st, "nq_delta_decode")
     return outs
 

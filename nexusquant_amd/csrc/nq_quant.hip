@@ -36,39 +36,92 @@ struct QuantArgs {
 
 // ------------------------------------------------------------------ E8 ----
 
-// Relaxed E8 (oracle/nq_spec.c nqs_e8_group): returns the coset flag and
-// overwrites x with the clamped lattice point.  The odd-sum step goes to the
-// first coordinate whose |x - r| equals the group minimum, which is the
-// reference's first argmin.
-template <int L>
-__device__ __forceinline__ int e8_group(float (&x)[8]) {
-    constexpr float HL = (float)(L / 2);
-    float r[8], e[8], a[8];
-    int isum = 0;
+// min(|e0|, ..., |e7|) in four min3/min instructions.  Written in asm because
+// the compiler otherwise quiets every |e| (a max with itself) before the min.
+__device__ __forceinline__ float min8_abs(const float (&e)[8]) {
+    float m1, m2, m3, m;
+    asm("v_min3_f32 %0, |%1|, |%2|, |%3|" : "=v"(m1) : "v"(e[0]), "v"(e[1]), "v"(e[2]));
+    asm("v_min3_f32 %0, |%1|, |%2|, |%3|" : "=v"(m2) : "v"(e[3]), "v"(e[4]), "v"(e[5]));
+    asm("v_min3_f32 %0, |%1|, |%2|, %3" : "=v"(m3) : "v"(e[6]), "v"(e[7]), "v"(m1));
+    asm("v_min_f32 %0, %1, %2" : "=v"(m) : "v"(m2), "v"(m3));
+    return m;
+}
+
+// r += d in the lanes of `mask` only: one VALU instruction under a narrowed
+// EXEC, restored inside the same asm block.
+__device__ __forceinline__ void add_in_lanes(float& r, float d, uint64_t mask) {
+    uint64_t saved;
+    asm volatile("s_and_saveexec_b64 %1, %2\n\t"
+                 "v_add_f32 %0, %0, %3\n\t"
+                 "s_mov_b64 exec, %1"
+                 : "+v"(r), "=&s"(saved)
+                 : "s"(mask), "v"(d));
+}
+
+// r[j] = rint(x[j] - 0.5) in the lanes of `mask` only.
+__device__ __forceinline__ void half_candidates_in_lanes(float (&r)[8], const float (&x)[8], uint64_t mask) {
+    uint64_t saved;
+    asm volatile("s_and_saveexec_b64 %8, %9\n\t"
+                 "v_add_f32 %0, -0.5, %10\n\t"
+                 "v_add_f32 %1, -0.5, %11\n\t"
+                 "v_add_f32 %2, -0.5, %12\n\t"
+                 "v_add_f32 %3, -0.5, %13\n\t"
+                 "v_add_f32 %4, -0.5, %14\n\t"
+                 "v_add_f32 %5, -0.5, %15\n\t"
+                 "v_add_f32 %6, -0.5, %16\n\t"
+                 "v_add_f32 %7, -0.5, %17\n\t"
+                 "v_rndne_f32 %0, %0\n\t"
+                 "v_rndne_f32 %1, %1\n\t"
+                 "v_rndne_f32 %2, %2\n\t"
+                 "v_rndne_f32 %3, %3\n\t"
+                 "v_rndne_f32 %4, %4\n\t"
+                 "v_rndne_f32 %5, %5\n\t"
+                 "v_rndne_f32 %6, %6\n\t"
+                 "v_rndne_f32 %7, %7\n\t"
+                 "s_mov_b64 exec, %8"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]),
+                   "+v"(r[7]), "=&s"(saved)
+                 : "s"(mask), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]),
+                   "v"(x[6]), "v"(x[7]));
+}
+
+// Relaxed E8 decision for one group (oracle/nq_spec.c nqs_e8_group).  x holds
+// the normalised coordinates, already clamped to [-L/2, L/2].  On return x
+// holds the chosen candidate before the coset offset and the final clamp:
+// the integer point r (with the odd-sum step applied) when the integer coset
+// wins, rint(x - 0.5) when the half coset wins (the caller adds 1/2).  The
+// odd-sum step goes to the first coordinate whose |x - r| equals the group
+// minimum, which is the reference's first argmin, and moves toward x (+1 on a
+// zero gap: x - r is never -0).  Returns the half-coset flag.
+__device__ __forceinline__ bool e8_select(float (&x)[8]) {
+    float r[8], e[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         r[j] = __builtin_rintf(x[j]);
         e[j] = x[j] - r[j];
-        a[j] = __builtin_fabsf(e[j]);
-        isum += (int)r[j];
     }
-    const bool odd = (isum & 1) != 0;
-    const float amin = __builtin_fminf(__builtin_fminf(__builtin_fminf(a[0], a[1]), __builtin_fminf(a[2], a[3])),
-                                       __builtin_fminf(__builtin_fminf(a[4], a[5]), __builtin_fminf(a[6], a[7])));
-    const float asum = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
-    const float thr = odd ? (1.0f + 2.0f * amin) : 2.0f;
+    const float rsum = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));  // exact
+    const bool odd = ((int)rsum & 1) != 0;
+    const float amin = min8_abs(e);
+    const float asum = ((__builtin_fabsf(e[0]) + __builtin_fabsf(e[1])) +
+                        (__builtin_fabsf(e[2]) + __builtin_fabsf(e[3]))) +
+                       ((__builtin_fabsf(e[4]) + __builtin_fabsf(e[5])) +
+                        (__builtin_fabsf(e[6]) + __builtin_fabsf(e[7])));
+    const float thr = odd ? __builtin_fmaf(2.0f, amin, 1.0f) : 2.0f;  // 1 + 2*amin, one rounding
     const bool use_half = asum > thr;
-    bool pending = odd && !use_half;
+    const uint64_t half_lanes = __builtin_amdgcn_ballot_w64(use_half);
+    const uint64_t pending = __builtin_amdgcn_ballot_w64(odd) & ~half_lanes;
+    uint64_t seen = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const float h = __builtin_rintf(x[j] - 0.5f) + 0.5f;
-        const bool hit = pending && (a[j] == amin);
-        pending = pending && !hit;
-        const float rs = r[j] + __builtin_copysignf(1.0f, e[j]);  // e is never -0
-        float v = use_half ? h : (hit ? rs : r[j]);
-        x[j] = __builtin_fminf(__builtin_fmaxf(v, -HL), HL);
+        const uint64_t eq = __builtin_amdgcn_ballot_w64(__builtin_fabsf(e[j]) == amin);
+        add_in_lanes(r[j], __builtin_copysignf(1.0f, e[j]), eq & pending & ~seen);
+        seen |= eq;
     }
-    return use_half ? 1 : 0;
+    half_candidates_in_lanes(r, x, half_lanes);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = r[j];
+    return use_half;
 }
 
 // --------------------------------------------------------------- codes ----
@@ -123,6 +176,106 @@ __device__ __forceinline__ void store_symbols(uint8_t* row_syms, int q, const fl
             for (int k = 0; k < NB; k += 2) {
                 uint16_t w = (uint16_t)(bytes[k] | (bytes[k + 1] << 8));
                 *reinterpret_cast<uint16_t*>(dst + k) = w;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------- packed lattice points ----
+//
+// For D * L <= 1024 and levels <= 8 the chosen candidates are carried as
+// packed fp16 pairs (coordinate k, k + 4 of a group in register k) of
+//   U = clamp01((p + L/2) / L),
+// computed in one v_pk_fma_f16 with the clamp bit: p is the candidate plus the
+// coset offset, so the clamp is the reference's clamp to [-L/2, L/2].  Every
+// value is a multiple of 1/(2L) in [0, 1], exact in fp16.
+
+__device__ __forceinline__ uint32_t pk_fma_clamp(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t d;
+    asm("v_pk_fma_f16 %0, %1, %2, %3 clamp" : "=v"(d) : "v"(a), "s"(b), "v"(c));
+    return d;
+}
+
+__device__ __forceinline__ uint32_t pk_f16_bits(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
+__device__ __forceinline__ uint32_t splat_f16(float v) {
+    const uint32_t h = __builtin_bit_cast(uint16_t, (__fp16)v);
+    return h | (h << 16);
+}
+
+// Symbols of one group from its four U registers.  sym = p + L/2 (integer
+// coset), floor(p) + L/2 (half coset, L/2 even) or ceil(p) + L/2 (L/2 odd).
+// S = U * (L * 2^-23) + c * 2^-24 is an exact fp16 subnormal whose bit pattern
+// is the integer 2(p + L/2) + c (c = 1 only for L = 2), so sym = bits >> 1 in
+// every case (the shift is the floor of half-coset points).  Returns the
+// group's 8 symbols, symbol j at bit j * bits.
+template <int L>
+__device__ __forceinline__ uint32_t group_symbols(const uint32_t (&u)[4]) {
+    constexpr int B = SymBits<L>::value;
+    const half2v scl = {(__fp16)(L * 0x1p-23f), (__fp16)(L * 0x1p-23f)};
+    const half2v off = L == 2 ? half2v{(__fp16)0x1p-24f, (__fp16)0x1p-24f} : half2v{(__fp16)0.0f, (__fp16)0.0f};
+    uint32_t d[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        d[k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2v, u[k]), scl, off));
+    if constexpr (B == 4 || B == 3) {
+        // fields 2(p + L/2) at bits 0 and 16 of each register; the low bit (set
+        // for half-coset points) is dropped so it cannot reach the neighbour
+        uint32_t m[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) m[k] = d[k] & 0xfffefffeu;
+        if constexpr (B == 4) {
+            return (m[0] >> 1) | (m[1] << 3) | (m[2] << 7) | (m[3] << 11);
+        } else {
+            const uint32_t t = (m[0] >> 1) | (m[1] << 2) | (m[2] << 5) | (m[3] << 8);  // s0..3 @0, s4..7 @16
+            return (t & 0xfffu) | ((t >> 4) & 0xfff000u);
+        }
+    } else {
+        static_assert(B == 2, "packed symbols implemented for 2, 3 and 4 bits");
+        uint32_t m[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) m[k] = d[k] & 0x00060006u;  // drop the +1 bit
+        const uint32_t t = (m[0] >> 1) | (m[1] << 1) | (m[2] << 3) | (m[3] << 5);  // s0..3 @0, s4..7 @16
+        return (t & 0xffu) | ((t >> 8) & 0xff00u);
+    }
+}
+
+// Store the lane's C group words (B bytes each, slot order) at dst.
+template <int B, int C>
+__device__ __forceinline__ void store_group_words(uint8_t* dst, const uint32_t (&w)[C]) {
+    if constexpr (B == 4) {
+        if constexpr (C == 2) {
+            *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+        } else {
+#pragma unroll
+            for (int c = 0; c < C; c += 4)
+                *reinterpret_cast<uint4*>(dst + 4 * c) = make_uint4(w[c], w[c + 1], w[c + 2], w[c + 3]);
+        }
+    } else if constexpr (B == 2) {
+        if constexpr (C == 2) {
+            *reinterpret_cast<uint32_t*>(dst) = w[0] | (w[1] << 16);
+        } else {
+#pragma unroll
+            for (int c = 0; c < C; c += 4)
+                *reinterpret_cast<uint2*>(dst + 2 * c) = make_uint2(w[c] | (w[c + 1] << 16), w[c + 2] | (w[c + 3] << 16));
+        }
+    } else {
+        static_assert(B == 3, "3-byte groups");
+        if constexpr (C == 2) {
+            // 6 bytes at a 2-byte aligned address
+            uint16_t* d16 = reinterpret_cast<uint16_t*>(dst);
+            d16[0] = (uint16_t)w[0];
+            d16[1] = (uint16_t)((w[0] >> 16) | (w[1] << 8));
+            d16[2] = (uint16_t)(w[1] >> 8);
+        } else {
+#pragma unroll
+            for (int c = 0; c < C; c += 4) {
+                const uint32_t a = w[c] | (w[c + 1] << 24);
+                const uint32_t b = (w[c + 1] >> 8) | (w[c + 2] << 16);
+                const uint32_t e = (w[c + 2] >> 16) | (w[c + 3] << 8);
+                *reinterpret_cast<uint3*>(dst + 3 * c) = make_uint3(a, b, e);
             }
         }
     }
@@ -184,42 +337,39 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
         apply_rope<D, DR, RC, true>(x, q, cs, sn);
     }
 
-    fwht_row<C>(x, q);
+    fwht_row<C>(x, q);  // x = sigma(q) * S x
+    constexpr float HL = (float)(L / 2);
     const float sigma = quad_sign(q);
-    const float hs = sigma * a.hscale;
-    float amax = 0.0f;
+    float umax = 0.0f;
 #pragma unroll
     for (int c = 0; c < C; ++c)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            x[c][i] = x[c][i] * hs;
-            amax = __builtin_fmaxf(amax, __builtin_fabsf(x[c][i]));
-        }
-    amax = __builtin_fmaxf(amax, dpp_f32<kQuadXor1>(amax));
-    amax = __builtin_fmaxf(amax, dpp_f32<kQuadXor2>(amax));
-    amax = __builtin_fmaxf(amax, 1e-8f);
+        for (int i = 0; i < 8; ++i) umax = __builtin_fmaxf(umax, __builtin_fabsf(x[c][i]));
+    umax = __builtin_fmaxf(umax, dpp_f32<kQuadXor1>(umax));
+    umax = __builtin_fmaxf(umax, dpp_f32<kQuadXor2>(umax));
+    // Row scale as the reference: amax of the normalised rotation, clamped at
+    // 1e-8 (rounding is monotone, so fl(max|u| h) is the max of fl(|u| h)).
+    const float amax_raw = umax * a.hscale;
+    const bool tiny = !(amax_raw >= 1e-8f);
+    const float amax = tiny ? 1e-8f : amax_raw;
     const float scale = amax * (2.0f / (float)L);
-    const float rcp = 1.0f / scale;  // correctly rounded reciprocal
+    // Normalisation factor: the smallest f >= fl((L/2) / umax) with
+    // fl(umax * f) >= L/2, so the row maximum lands on +-L/2 after the clamp;
+    // fl(h / scale) for rows whose amax was clamped.  One correctly rounded
+    // division per row.
+    float f = (tiny ? a.hscale : HL) / (tiny ? scale : umax);
+    if (!tiny && umax * f < HL) f = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, f) + 1u);
+    const float fs = sigma * f;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[c][i] = __builtin_amdgcn_fmed3f(x[c][i] * fs, -HL, HL);
 
-    int coset[C];
+    bool coset[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            // correctly rounded x / scale by one refinement of the reciprocal
-            float q0 = x[c][i] * rcp;
-            float rem = __builtin_fmaf(-q0, scale, x[c][i]);
-            x[c][i] = __builtin_fmaf(rem, rcp, q0);
-        }
-        coset[c] = e8_group<L>(x[c]);
-    }
+    for (int c = 0; c < C; ++c) coset[c] = e8_select(x[c]);
 
     const size_t out_row = (size_t)bh * a.seq_out + t_out;
-    if (a.syms && active) {
-        constexpr int ROW_BYTES = D / 8 * SymBits<L>::value;
-        uint8_t* dst = reinterpret_cast<uint8_t*>(a.syms[tensor]) + out_row * ROW_BYTES;
-        store_symbols<L, C>(dst, q, x, coset);
-    }
     uint32_t cbits = 0;
 #pragma unroll
     for (int c = 0; c < C; ++c) cbits |= (uint32_t)coset[c] << (4 * c + q);
@@ -234,31 +384,94 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
         }
         if (a.scales) reinterpret_cast<float*>(a.scales[tensor])[out_row] = scale;
     }
+    constexpr int B = SymBits<L>::value;
+    constexpr int ROW_BYTES = D / 8 * B;
+    const float g = sigma * (a.hscale * scale);  // reconstruction multiplier, sign folded
 
-    if (!a.recon) return;
-    const float g = sigma * (a.hscale * scale);
-    constexpr bool EXACT_F16 = D * (L / 2) <= 1024;
-    if constexpr (EXACT_F16) {
+    constexpr bool PACKED = D * L <= 1024 && B <= 4;
+    if constexpr (PACKED) {
+        // U = clamp01((candidate + offset + L/2) / L); offset 1/2 for the half coset
+        const uint32_t inv_l = splat_f16(1.0f / (float)L);
+        const uint32_t off_int = splat_f16(HL / (float)L);
+        const uint32_t off_half = splat_f16((HL + 0.5f) / (float)L);
+        uint32_t u[C][4];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const uint32_t off = coset[c] ? off_half : off_int;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) u[c][k] = pk_fma_clamp(pk_f16_bits(x[c][k], x[c][k + 4]), inv_l, off);
+        }
+        if (a.syms && active) {
+            uint32_t wds[C];
+#pragma unroll
+            for (int c = 0; c < C; ++c) wds[c] = group_symbols<L>(u[c]);
+            uint8_t* dst = reinterpret_cast<uint8_t*>(a.syms[tensor]) + out_row * ROW_BYTES + q * (C * B);
+            store_group_words<B, C>(dst, wds);
+        }
+        if (!a.recon) return;
+        // Walsh-Hadamard of U in fp16 (exact: multiples of 1/(2L), |.| <= D).
+        // S U = (S p)/L + (D/2) e_0, so every output but coordinate 0 (lane 0,
+        // chunk 0, register 0 low half) is (S p)/L; that one is corrected by
+        // subtracting (L/2) D after the exact multiply by L.
         half2v hp[C][4];
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                hp[c][k] = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(x[c][2 * k], x[c][2 * k + 1]));
+            for (int k = 0; k < 4; ++k) hp[c][k] = __builtin_bit_cast(half2v, u[c][k]);
         fwht_row_f16<C>(hp, q);
+        const float gl = g * (float)L;  // exact
+        const float dc = q == 0 ? HL * (float)D : 0.0f;
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                x[c][2 * k] = __builtin_fmaf((float)hp[c][k].x, g, 0.0f);
-                x[c][2 * k + 1] = __builtin_fmaf((float)hp[c][k].y, g, 0.0f);
+                if (c == 0 && k == 0) {
+                    const float t = __builtin_fmaf((float)hp[0][0].x, (float)L, -dc);  // exact
+                    x[0][0] = t * g;
+                } else {
+                    x[c][k] = __builtin_fmaf((float)hp[c][k].x, gl, 0.0f);
+                }
+                x[c][k + 4] = __builtin_fmaf((float)hp[c][k].y, gl, 0.0f);
             }
     } else {
-        fwht_row<C>(x, q);  // exact on half-integer lattice points
+        // candidate + coset offset, clamped, as fp32 lattice points
 #pragma unroll
-        for (int c = 0; c < C; ++c)
+        for (int c = 0; c < C; ++c) {
+            const float off = coset[c] ? 0.5f : 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) x[c][i] = x[c][i] * g;
+            for (int i = 0; i < 8; ++i) x[c][i] = __builtin_amdgcn_fmed3f(x[c][i] + off, -HL, HL);
+        }
+        if (a.syms && active) {
+            int cs[C];
+#pragma unroll
+            for (int c = 0; c < C; ++c) cs[c] = coset[c] ? 1 : 0;
+            uint8_t* dst = reinterpret_cast<uint8_t*>(a.syms[tensor]) + out_row * ROW_BYTES;
+            store_symbols<L, C>(dst, q, x, cs);
+        }
+        if (!a.recon) return;
+        constexpr bool EXACT_F16 = D * (L / 2) <= 1024;
+        if constexpr (EXACT_F16) {
+            half2v hp[C][4];
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    hp[c][k] = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(x[c][2 * k], x[c][2 * k + 1]));
+            fwht_row_f16<C>(hp, q);
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    x[c][2 * k] = __builtin_fmaf((float)hp[c][k].x, g, 0.0f);
+                    x[c][2 * k + 1] = __builtin_fmaf((float)hp[c][k].y, g, 0.0f);
+                }
+        } else {
+            fwht_row<C>(x, q);  // exact on half-integer lattice points
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[c][i] = x[c][i] * g;
+        }
     }
 
     if constexpr (IS_KEY) {

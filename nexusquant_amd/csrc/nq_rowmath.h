@@ -204,7 +204,7 @@ __device__ __forceinline__ void load_rope(const float* cos_t, const float* sin_t
     }
 }
 
-// INVERSE (input side, reference rounding): lo' = lo*c + hi*s, hi' = (-lo)*s + hi*c.
+// INVERSE (input side): lo' = fma(lo, c, hi*s), hi' = fma(hi, c, -(lo*s)).
 // Forward (output side): lo' = fma(lo, c, -(hi*s)), hi' = fma(lo, s, hi*c).
 template <int D, int DR, int RC, bool INVERSE>
 __device__ __forceinline__ void apply_rope(float (&x)[D / 32][8], int q, const float (&cs)[RC][8],
@@ -217,8 +217,8 @@ __device__ __forceinline__ void apply_rope(float (&x)[D / 32][8], int q, const f
             for (int i = 0; i < 8; ++i) {
                 const float lo = x[c][i], hi = x[c + C / 2][i];
                 if constexpr (INVERSE) {
-                    x[c][i] = lo * cs[c][i] + hi * sn[c][i];
-                    x[c + C / 2][i] = (-lo) * sn[c][i] + hi * cs[c][i];
+                    x[c][i] = __builtin_fmaf(lo, cs[c][i], hi * sn[c][i]);
+                    x[c + C / 2][i] = __builtin_fmaf(hi, cs[c][i], -(lo * sn[c][i]));
                 } else {
                     x[c][i] = __builtin_fmaf(lo, cs[c][i], -(hi * sn[c][i]));
                     x[c + C / 2][i] = __builtin_fmaf(lo, sn[c][i], hi * cs[c][i]);
@@ -241,7 +241,8 @@ __device__ __forceinline__ void apply_rope(float (&x)[D / 32][8], int q, const f
                                        : (c == 1 ? (lowq ? P[2][i] : P[0][i]) : (lowq ? P[0][i] : P[1][i]));
                 const float v = x[c][i];
                 if constexpr (INVERSE) {
-                    x[c][i] = is_lo ? (v * cs[c][i] + p * sn[c][i]) : ((-p) * sn[c][i] + v * cs[c][i]);
+                    const float ps = p * sn[c][i];
+                    x[c][i] = __builtin_fmaf(v, cs[c][i], is_lo ? ps : -ps);
                 } else {
                     x[c][i] = is_lo ? __builtin_fmaf(v, cs[c][i], -(p * sn[c][i]))
                                     : __builtin_fmaf(p, sn[c][i], v * cs[c][i]);

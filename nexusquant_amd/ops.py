@@ -3,8 +3,9 @@
 from __future__ import annotations
 
 import ctypes
+import threading
 from dataclasses import dataclass
-from typing import List, Optional, Sequence, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 
@@ -37,23 +38,117 @@ class PackedCodes:
         return sum(t.numel() * t.element_size() for t in (self.syms, self.cosets, self.scales))
 
 
-def _ptr_arrays(groups: Sequence[Optional[Sequence[torch.Tensor]]], device) -> List[Optional[torch.Tensor]]:
-    """Device int64 arrays of base addresses, staged through one pinned buffer and
-    one asynchronous copy (a pageable copy would block the host behind the
-    previous kernel on the stream)."""
-    flat = []
-    spans = []
-    for g in groups:
-        if g is None:
-            spans.append(None)
-            continue
-        spans.append((len(flat), len(g)))
-        flat.extend(t.data_ptr() for t in g)
-    if not flat:
-        return [None for _ in groups]
-    host = torch.tensor(flat, dtype=torch.int64).pin_memory()
-    dev = host.to(device, non_blocking=True)
-    return [None if sp is None else dev[sp[0]:sp[0] + sp[1]] for sp in spans]
+class _AddressRing:
+    """Per-device ring of pinned host and device int64 slots for the address
+    arrays a launch descriptor points at.
+
+    Each launch writes its addresses into a free span of the pinned buffer and
+    copies the span to the same span of the device buffer with one asynchronous
+    copy on the launch stream.  An event recorded after the launch marks the
+    span busy; a span is rewritten only after its event has completed, which
+    the host checks (and in practice never waits for: the ring holds 64K
+    addresses).  Allocating pinned memory per launch instead would let the
+    runtime synchronise the device, and a pageable copy would block the host
+    behind the previous kernel.
+    """
+
+    ENTRIES = 1 << 16
+    EVENTS = 16  # events created (and recorded once) up front
+
+    def __init__(self, device):
+        self.device = device
+        self.host = torch.empty(self.ENTRIES, dtype=torch.int64, pin_memory=True)
+        self.host_np = self.host.numpy()
+        self.dev = torch.empty(self.ENTRIES, dtype=torch.int64, device=device)
+        self.head = 0
+        self.busy: List[Tuple[int, int, torch.cuda.Event]] = []  # oldest first
+        # The runtime creates an event's resources at its first record, which can
+        # block the host; recording a pool once here keeps that out of launches.
+        stream = torch.cuda.current_stream(device)
+        self.free_events: List[torch.cuda.Event] = []
+        for _ in range(self.EVENTS):
+            ev = torch.cuda.Event()
+            ev.record(stream)
+            self.free_events.append(ev)
+        self.lock = threading.Lock()
+
+    def _wait_for(self, start: int, end: int) -> None:
+        # recycle completed reservations, oldest first
+        while self.busy and self.busy[0][2].query():
+            self.free_events.append(self.busy.pop(0)[2])
+        keep = []
+        for (s0, e0, ev) in self.busy:
+            if s0 < end and start < e0:
+                ev.synchronize()
+                self.free_events.append(ev)
+            else:
+                keep.append((s0, e0, ev))
+        self.busy = keep
+
+    def stage(self, flat: List[int]) -> Tuple[torch.Tensor, Tuple[int, int]]:
+        n = len(flat)
+        if n > self.ENTRIES:
+            raise ValueError(f"{n} tensors in one launch exceed the address ring ({self.ENTRIES})")
+        with self.lock:
+            start = self.head if self.head + n <= self.ENTRIES else 0
+            end = start + n
+            self._wait_for(start, end)
+            self.host_np[start:end] = flat
+            self.dev[start:end].copy_(self.host[start:end], non_blocking=True)
+            self.head = end
+        return self.dev[start:end], (start, end)
+
+    def release(self, span: Tuple[int, int]) -> None:
+        with self.lock:
+            ev = self.free_events.pop() if self.free_events else torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))
+            self.busy.append((span[0], span[1], ev))
+
+
+_rings: Dict[int, _AddressRing] = {}
+_rings_lock = threading.Lock()
+
+
+def _ring(device) -> _AddressRing:
+    idx = torch.device(device).index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    r = _rings.get(idx)
+    if r is None:
+        with _rings_lock:
+            r = _rings.get(idx)
+            if r is None:
+                r = _rings[idx] = _AddressRing(torch.device("cuda", idx))
+    return r
+
+
+class _PtrArrays:
+    """Device int64 arrays of the base addresses of each tensor group, staged
+    through the device's address ring.  Call release() right after the launch
+    that reads them."""
+
+    def __init__(self, groups: Sequence[Optional[Sequence[torch.Tensor]]], device):
+        flat: List[int] = []
+        spans = []
+        for g in groups:
+            if g is None:
+                spans.append(None)
+                continue
+            spans.append((len(flat), len(g)))
+            flat.extend(t.data_ptr() for t in g)
+        self._ring = None
+        self._span = None
+        if not flat:
+            self.arrays = [None for _ in groups]
+            return
+        self._ring = _ring(device)
+        dev, self._span = self._ring.stage(flat)
+        self.arrays = [None if sp is None else dev[sp[0]:sp[0] + sp[1]] for sp in spans]
+
+    def release(self) -> None:
+        if self._ring is not None and self._span is not None:
+            self._ring.release(self._span)
+            self._span = None
 
 
 def _addr(t: Optional[torch.Tensor]):
@@ -111,14 +206,17 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
             raise ValueError(f"keep must be [batch, seq] = {(b, s)}, got {tuple(k.shape)}")
 
     n = len(src)
-    recon_t = [torch.empty(b, h, seq_out, d, dtype=torch.float16, device=dev) for _ in range(n)] if recon else None
+    # one allocation per output kind; every tensor gets a contiguous slice
+    recon_t = None
+    if recon:
+        recon_t = list(torch.empty(n, b, h, seq_out, d, dtype=torch.float16, device=dev).unbind(0))
     codes_t = None
     if codes:
-        codes_t = [PackedCodes(
-            syms=torch.empty(b, h, seq_out, D // 8 * SYM_BITS[levels], dtype=torch.uint8, device=dev),
-            cosets=torch.empty(b, h, seq_out, D // 64, dtype=torch.uint8, device=dev),
-            scales=torch.empty(b, h, seq_out, dtype=torch.float32, device=dev),
-            levels=levels, head_dim=d, padded_dim=D, is_key=is_key) for _ in range(n)]
+        syms = torch.empty(n, b, h, seq_out, D // 8 * SYM_BITS[levels], dtype=torch.uint8, device=dev).unbind(0)
+        cosets = torch.empty(n, b, h, seq_out, D // 64, dtype=torch.uint8, device=dev).unbind(0)
+        scales = torch.empty(n, b, h, seq_out, dtype=torch.float32, device=dev).unbind(0)
+        codes_t = [PackedCodes(syms=syms[i], cosets=cosets[i], scales=scales[i], levels=levels, head_dim=d,
+                               padded_dim=D, is_key=is_key) for i in range(n)]
 
     cos = sin = None
     n_pos = 0
@@ -131,7 +229,8 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
               [c.syms for c in codes_t] if codes_t else None,
               [c.cosets for c in codes_t] if codes_t else None,
               [c.scales for c in codes_t] if codes_t else None]
-    arrays = dict(zip(names, _ptr_arrays(groups, dev)))
+    staged = _PtrArrays(groups, dev)
+    arrays = dict(zip(names, staged.arrays))
     desc = _lib.QuantDesc(
         n_tensors=n, batch=b, heads=h, seq_in=s, seq_out=seq_out, head_dim=d,
         dtype=_lib.dtype_code(t0.dtype), levels=levels, is_key=int(is_key),
@@ -140,17 +239,15 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
         gather=_addr(g), keep=_addr(k), rope_cos=_addr(cos), rope_sin=_addr(sin),
         rope_n_pos=n_pos, hadamard_scale=hadamard_constant(D))
     with torch.cuda.device(dev):
-        if launch_events is not None:
-            launch_events[0].record()
-        status = lib.nq_quantize(ctypes.byref(desc), ctypes.c_void_p(_lib.current_stream_handle(dev)))
-        if launch_events is not None:
-            launch_events[1].record()
+        try:
+            if launch_events is not None:
+                launch_events[0].record()
+            status = lib.nq_quantize(ctypes.byref(desc), ctypes.c_void_p(_lib.current_stream_handle(dev)))
+            if launch_events is not None:
+                launch_events[1].record()
+        finally:
+            staged.release()
     _lib.check(status, "nq_quantize")
-    # keep the pointer arrays and inputs alive until the kernel has consumed them
-    stream = torch.cuda.current_stream(dev)
-    for t in list(arrays.values()) + src + [g, k]:
-        if t is not None:
-            t.record_stream(stream)
     return recon_t, codes_t
 
 
@@ -245,10 +342,15 @@ def gather_rows(tensors: Sequence[torch.Tensor], *, gather: Optional[torch.Tenso
         k = keep.to(device=dev, dtype=torch.uint8).contiguous()
         if tuple(k.shape) != (b, s):
             raise ValueError(f"keep must be [batch, seq] = {(b, s)}")
-    out = [torch.empty(b, h, seq_out, d, dtype=torch.float16, device=dev) for _ in src]
-    arr_src, arr_dst = _ptr_arrays([src, out], dev)
+    out = list(torch.empty(len(src), b, h, seq_out, d, dtype=torch.float16, device=dev).unbind(0))
+    staged = _PtrArrays([src, out], dev)
+    arr_src, arr_dst = staged.arrays
     with torch.cuda.device(dev):
-        st = lib.nq_gather_rows(_addr(arr_src), _addr(arr_dst), len(src), _lib.dtype_code(t0.dtype), b, h, s,
-                                seq_out, d, _addr(g), _addr(k), ctypes.c_void_p(_lib.current_stream_handle(dev)))
+        try:
+            st = lib.nq_gather_rows(_addr(arr_src), _addr(arr_dst), len(src), _lib.dtype_code(t0.dtype), b, h, s,
+                                    seq_out, d, _addr(g), _addr(k),
+                                    ctypes.c_void_p(_lib.current_stream_handle(dev)))
+        finally:
+            staged.release()
     _lib.check(st, "nq_gather_rows")
     return out

@@ -9,17 +9,27 @@
  *  rope_utils.py:75-249, hadamard.py:23-43) and fixes every rounding step so
  * that the HIP kernel can be compared with it bit for bit:
  *
- *  1. Inverse RoPE exactly as the reference (separate fp32 products and sums,
- *     no FMA contraction): lo' = lo*c + hi*s ; hi' = (-lo)*s + hi*c.
+ *  1. Inverse RoPE with one fused multiply-add per coordinate:
+ *     lo' = fma(lo, c, fl(hi*s)) ; hi' = fma(hi, c, -fl(lo*s)).  The reference
+ *     rounds both products (rope_utils.py:75-112); the difference is one ulp of
+ *     the rotated value, far below what moves a code except at a near tie.
  *  2. Zero-pad to D = next power of two (the reference raises for d = 96,
  *     hadamard.py:35-36; padding is this build's definition).
- *  3. Unnormalised Walsh-Hadamard butterflies, stages on index bit 0,1,...,
- *     log2(D)-1 in that order, each (a, b) -> (a + b, a - b) in fp32, then one
- *     multiply by the reference's normalisation constant h_D.  The reference
- *     uses a dense fp32 GEMM here, so the two differ in the last ulp; the
- *     resulting code disagreement is measured in tests (about 1e-6 of groups).
- *  4. amax over all D rotated values, clamped at fp32(1e-8); scale = amax/(L/2)
- *     (exact); xn = z / scale, correctly rounded (e8_lattice.py:114-116).
+ *  3. Unnormalised Walsh-Hadamard butterflies u = S x, stages on index bit
+ *     0,1,..., log2(D)-1 in that order, each (a, b) -> (a + b, a - b) in fp32.
+ *     The reference uses a dense fp32 GEMM with the normalised matrix h_D * S
+ *     here, so the two differ in the last ulp; the resulting code disagreement
+ *     is measured in tests (about 1e-6 of groups).
+ *  4. Row scale exactly as the reference's amax of the normalised rotation:
+ *     amax = fl(max|u| * h_D) (rounding is monotone, so this equals the max of
+ *     the rounded products), clamped at fp32(1e-8); scale = amax/(L/2) (exact)
+ *     (e8_lattice.py:114-116).  Normalised coordinates xn = clamp(fl(u * f),
+ *     -L/2, L/2): one multiply per coordinate in place of the reference's
+ *     multiply by h_D and division by scale, within a few ulp of it.  f is the
+ *     smallest float >= fl((L/2) / max|u|) with fl(max|u| * f) >= L/2, so the
+ *     row's largest coordinate lands exactly on +-L/2 after the clamp, as it
+ *     does in the reference (amax / scale == L/2 exactly).  Rows whose amax is
+ *     clamped to 1e-8 use f = fl(h_D / scale) and never reach L/2.
  *  5. Relaxed E8 per 8-group (e8_lattice.py:36-69): r = rint(x); on odd sum
  *     the first smallest |x - r| coordinate steps toward x (zero gap: +1);
  *     h = rint(x - 0.5) + 0.5.  The choice d_half < d_int is evaluated in the
@@ -169,6 +179,14 @@ void nqs_e8_group(const float* x, float half_levels, float* p, int* coset, float
 
 static int coset_of(const uint8_t* flags, int i) { return flags[i >> 3]; }
 
+static float next_up(float f) { /* f > 0, finite */
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    ++b;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
 static void fwht_inplace(float* v, int D) {
     for (int len = 1; len < D; len <<= 1) {
         for (int i = 0; i < D; ++i) {
@@ -215,26 +233,34 @@ void nqs_quant_rows(int64_t n, int d, int D, int L, float hD,
             const float* s = sin_in + row * half;
             for (int i = 0; i < half; ++i) {
                 float lo = xr[i], hi = xr[i + half];
-                float t1 = lo * c[i];
-                float t2 = hi * s[i];
-                float t3 = (-lo) * s[i];
-                float t4 = hi * c[i];
-                v[i] = t1 + t2;
-                v[i + half] = t3 + t4;
+                v[i] = fmaf(lo, c[i], hi * s[i]);
+                v[i + half] = fmaf(hi, c[i], -(lo * s[i]));
             }
         } else {
             for (int i = 0; i < d; ++i) v[i] = xr[i];
         }
         fwht_inplace(v, D);
-        float amax = 0.0f;
+        float umax = 0.0f;
         for (int i = 0; i < D; ++i) {
-            v[i] = v[i] * hD;
             float av = fabsf(v[i]);
-            if (av > amax) amax = av;
+            if (av > umax) umax = av;
         }
-        if (!(amax >= 1e-8f)) amax = 1e-8f;
+        float amax = umax * hD;
+        float f;
+        if (amax >= 1e-8f) {
+            /* smallest f >= fl(L/2 / umax) with fl(umax * f) >= L/2: the quotient
+             * is within half an ulp, so one step up always suffices */
+            f = half_levels / umax;
+            if (umax * f < half_levels) f = next_up(f);
+        } else {
+            amax = 1e-8f;
+            f = hD / (amax / half_levels);
+        }
         float scale = amax / half_levels;
-        for (int i = 0; i < D; ++i) xn[i] = v[i] / scale;
+        for (int i = 0; i < D; ++i) {
+            float t = v[i] * f;
+            xn[i] = t > half_levels ? half_levels : (t < -half_levels ? -half_levels : t);
+        }
         uint8_t coset_flags[NQS_MAXD / 8];
         for (int g = 0; g < G; ++g) {
             int cs;
@@ -242,6 +268,11 @@ void nqs_quant_rows(int64_t n, int d, int D, int L, float hD,
             nqs_e8_group(xn + 8 * g, half_levels, p + 8 * g, &cs, &mg);
             coset_flags[g] = (uint8_t)cs;
             if (coset_out) coset_out[row * G + g] = (uint8_t)cs;
+            /* a coordinate the clamp moved onto +-L/2 that is not the row maximum
+             * sits one ulp from where the reference puts it: a tie for the
+             * direction of the odd-sum step */
+            for (int j = 0; j < 8 && mg > 0.0f; ++j)
+                if (fabsf(xn[8 * g + j]) == half_levels && fabsf(v[8 * g + j]) != umax) mg = 0.0f;
             if (margin_out) margin_out[row * G + g] = mg;
         }
         if (xn_out) memcpy(xn_out + row * D, xn, sizeof(float) * D);
@@ -282,21 +313,3 @@ void nqs_quant_rows(int64_t n, int d, int D, int L, float hD,
     }
 }
 
-/* Correctly rounded division check helper: q = fl(z / s) via the reciprocal
- * refinement the HIP kernel uses (y = fl(1/s); q0 = z*y; r = fma(-q0, s, z);
- * q = fma(r, y, q0)).  Returns the count of inputs where it differs from z/s. */
-int64_t nqs_check_markstein(int64_t n, const float* z, const float* s) {
-    int64_t bad = 0;
-    for (int64_t i = 0; i < n; ++i) {
-        float y = 1.0f / s[i];
-        float q0 = z[i] * y;
-        float r = fmaf(-q0, s[i], z[i]);
-        float q = fmaf(r, y, q0);
-        float ref = z[i] / s[i];
-        uint32_t a, b;
-        memcpy(&a, &q, 4);
-        memcpy(&b, &ref, 4);
-        if (a != b) ++bad;
-    }
-    return bad;
-}

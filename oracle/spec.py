@@ -33,8 +33,6 @@ def lib():
         L.nqs_quant_rows.restype = None
         L.nqs_e8_group.argtypes = [P, ctypes.c_float, P, P, P]
         L.nqs_e8_group.restype = None
-        L.nqs_check_markstein.argtypes = [ctypes.c_int64, P, P]
-        L.nqs_check_markstein.restype = ctypes.c_int64
         L.nqs_f32_to_f16.argtypes = [ctypes.c_float]
         L.nqs_f32_to_f16.restype = ctypes.c_uint16
         _lib = L
@@ -99,9 +97,3 @@ def e8_groups(x: np.ndarray, L: int):
         f(_ptr(x[i]), float(L // 2), _ptr(p[i]), ctypes.c_void_p(cs[i:].ctypes.data),
           ctypes.c_void_p(mg[i:].ctypes.data))
     return p, cs, mg
-
-
-def markstein_mismatches(z: np.ndarray, s: np.ndarray) -> int:
-    z = np.ascontiguousarray(z, np.float32)
-    s = np.ascontiguousarray(s, np.float32)
-    return int(lib().nqs_check_markstein(z.size, _ptr(z), _ptr(s)))

@@ -110,14 +110,28 @@ def test_quantizer_invariants():
         assert o["sym"].max() <= L
 
 
-def test_markstein_division_is_correctly_rounded():
+def test_normalisation_within_two_ulp_of_reference_division():
+    # The spec multiplies by f = fl(h_D * fl(1/scale)) where the reference
+    # multiplies by h_D and divides by the row scale (e8_lattice.py:114-116).
+    # Compare the normalised coordinates with the reference formula computed
+    # from the same unnormalised transform: a dropped or doubled h_D, a wrong
+    # level count or a scale taken before the clamp fails by orders of magnitude.
     rng = np.random.default_rng(5)
-    s = np.exp(rng.uniform(-30, 30, 500000)).astype(np.float32)
-    z = (rng.uniform(-1, 1, 500000) * s * 4).astype(np.float32)
-    assert S.markstein_mismatches(z, s) == 0
-    s2 = (np.float32(1e-8) / 4) * np.ones(1000, np.float32)
-    z2 = rng.standard_normal(1000).astype(np.float32) * np.float32(1e-8)
-    assert S.markstein_mismatches(z2, s2) == 0
+    x = rng.standard_normal((2048, 128)).astype(np.float32)
+    x[3] *= np.float32(1e-12)            # row whose amax falls under the 1e-8 clamp
+    H = T.hadamard_matrix(128).numpy()
+    hD = np.float32(S.hadamard_constant(128))
+    for L in (2, 4, 8, 16):
+        o = S.quant_rows(x, L)
+        u = (x.astype(np.float64) @ np.sign(H).astype(np.float64)).astype(np.float32)
+        y = u * hD
+        amax = np.maximum(np.abs(y).max(1), np.float32(1e-8))
+        scale = (amax / np.float32(L / 2)).astype(np.float32)
+        assert np.allclose(o["scale"], scale, rtol=1e-5, atol=0)
+        ref = (y / scale[:, None]).astype(np.float32)
+        ulp = np.spacing(np.abs(ref)).astype(np.float32)
+        assert np.all(np.abs(o["xn"] - ref) <= 2 * ulp + 1e-5 * np.abs(ref).max(1, keepdims=True))
+        assert np.abs(o["xn"]).max() == L / 2
 
 
 def test_fp16_rounding_matches_numpy():
