@@ -222,7 +222,15 @@ struct RealArgs {
     float* importance; // [batch, seq] accumulated
     int32_t seq, hq, hkv, batch;
     float scaling;
+    int32_t n_items, per_xcd;  // 128-row blocks x batch*hq; blocks per XCD range
 };
+
+// Block -> work item: consecutive block ids go round-robin to the 8 XCDs, so
+// block 8k + x takes item x * per_xcd + k and each XCD walks one contiguous
+// range of the item order (which keeps one operand set in its L2).
+__device__ __forceinline__ int xcd_item(const RealArgs& a) {
+    return (int)(blockIdx.x & 7u) * a.per_xcd + (int)(blockIdx.x >> 3);
+}
 
 __device__ __forceinline__ float round_bf16(float x) {
     uint32_t u = __builtin_bit_cast(uint32_t, x);
@@ -308,6 +316,372 @@ __global__ __launch_bounds__(64) void real_sweep(RealArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Real scorer, fp16 / bf16 models: workgroups of 4 waves on the gfx950
+// 32x32x16 MFMA, one operand resident in registers and the other streamed
+// through LDS tiles of 32 rows x D (rows padded by 16 bytes, so the 16-byte
+// operand reads of 16 consecutive lanes hit 64 distinct banks).
+//
+// real_rowstats: a workgroup owns 128 query rows (wave w: rows 32w..32w+31 of
+// the block) of one query head; its queries are the MFMA A operand.  It streams
+// the key tiles 0..(last row)/32 twice: first the row maximum of the raw
+// logits (the rounding chain round_T(round_T(.) * scaling) is monotone, so it
+// is applied once to the maximum), then the row sums of exp(x - max).  Writes
+// -max * log2(e) and 1 / sum per row.
+// real_colsum: a workgroup owns 128 keys (wave w: keys 32w..32w+31) as the B
+// operand and streams the query tiles from its first key on; it accumulates
+// round_T(exp(x - max) / sum) per key column in registers (fixed order, so the
+// result does not depend on scheduling) and writes the column sums.
+// exp is v_exp_f32 on x * log2(e) - max * log2(e) and the division a multiply
+// by the row's reciprocal sum: within a few ulp of the eager fp32 softmax.
+// ---------------------------------------------------------------------------
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int D>
+struct RealTile {
+    static constexpr int ROWB = 2 * D + 16;          // padded LDS row bytes
+    static constexpr int ROWS = 64;                  // rows per LDS stage (two 32-row MFMA blocks)
+    static constexpr int UNITS = ROWS * D / 8;       // 16-byte units per stage
+    static constexpr int PER_THREAD = (UNITS + 255) / 256;
+    static constexpr int KS = D / 16;                // MFMA K steps
+    static constexpr int BUF = ROWS * ROWB;
+};
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma16(uint4 a, uint4 b, f32x16 acc) {
+    if constexpr (DT == NQ_F16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
+                                                      acc, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       acc, 0, 0, 0);
+}
+
+// 16-byte units of rows [row0, row0 + 64) of a [seq, D] matrix (rows clamped to seq - 1).
+// Every thread loads PER_THREAD units unconditionally (UNITS is a multiple of
+// 256 for every supported D), so the loads issue back to back and only the
+// LDS store waits for them.
+template <int D>
+__device__ __forceinline__ void tile_load(const uint16_t* base, int row0, int seq, uint4 (&r)[RealTile<D>::PER_THREAD]) {
+    static_assert(RealTile<D>::UNITS % 256 == 0, "64-row stages of 16-byte units fill 256 threads evenly");
+#pragma unroll
+    for (int k = 0; k < RealTile<D>::PER_THREAD; ++k) {
+        const int u = threadIdx.x + 256 * k;
+        int row = row0 + u / (D / 8);
+        row = row < seq ? row : seq - 1;
+        r[k] = *reinterpret_cast<const uint4*>(base + (size_t)row * D + (u % (D / 8)) * 8);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void tile_store(char* lds, const uint4 (&r)[RealTile<D>::PER_THREAD]) {
+#pragma unroll
+    for (int k = 0; k < RealTile<D>::PER_THREAD; ++k) {
+        const int u = threadIdx.x + 256 * k;
+        *reinterpret_cast<uint4*>(lds + (u / (D / 8)) * RealTile<D>::ROWB + (u % (D / 8)) * 16) = r[k];
+    }
+}
+
+// 32x32 logits: A from registers (this lane's row, K chunks), B from 32 LDS rows.
+template <int DT, int D>
+__device__ __forceinline__ f32x16 logits_regs_lds(const uint4 (&a)[RealTile<D>::KS], const char* lds, int c, int g) {
+    f32x16 acc = {};
+    const char* row = lds + c * RealTile<D>::ROWB + 16 * g;
+#pragma unroll
+    for (int s = 0; s < RealTile<D>::KS; ++s)
+        acc = mfma16<DT>(a[s], *reinterpret_cast<const uint4*>(row + 32 * s), acc);
+    return acc;
+}
+
+// 32x32 logits: A (queries) from 32 LDS rows, B (keys) from registers.
+template <int DT, int D>
+__device__ __forceinline__ f32x16 logits_lds_regs(const char* lds, const uint4 (&b)[RealTile<D>::KS], int c, int g) {
+    f32x16 acc = {};
+    const char* row = lds + c * RealTile<D>::ROWB + 16 * g;
+#pragma unroll
+    for (int s = 0; s < RealTile<D>::KS; ++s)
+        acc = mfma16<DT>(*reinterpret_cast<const uint4*>(row + 32 * s), b[s], acc);
+    return acc;
+}
+
+// this lane's K chunks of one row of a [seq, D] matrix (row clamped)
+template <int D>
+__device__ __forceinline__ void row_operand(const uint16_t* base, int row, int seq, int g, uint4 (&r)[RealTile<D>::KS]) {
+    row = row < seq ? row : seq - 1;
+    const uint16_t* p = base + (size_t)row * D + 8 * g;
+#pragma unroll
+    for (int s = 0; s < RealTile<D>::KS; ++s) r[s] = *reinterpret_cast<const uint4*>(p + 16 * s);
+}
+
+// x = round_T(round_T(logit) * scaling), both roundings kept (the empty asm
+// stops the fp32 product and the second rounding from fusing into one
+// mixed-precision instruction that would round once).
+template <int DT>
+__device__ __forceinline__ float eager_logit(float acc, float scaling) {
+    float t = round_model<DT>(acc) * scaling;
+    asm("" : "+v"(t));
+    return round_model<DT>(t);
+}
+
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef __fp16 f16x2v __attribute__((ext_vector_type(2)));
+
+// two fp32 -> packed fp16, round to nearest even (one v_cvt_pk_f16_f32)
+__device__ __forceinline__ f16x2v cvt_pk_f16(float lo, float hi) {
+    uint32_t r;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return __builtin_bit_cast(f16x2v, r);
+}
+
+// exp2 arguments of two logits: round_T(round_T(acc) * scaling) * log2(e) + nm,
+// the roundings done on packed pairs.
+template <int DT>
+__device__ __forceinline__ void exp_args2(float a0, float a1, float scaling, float nm0, float nm1, float& o0,
+                                          float& o1) {
+    if constexpr (DT == NQ_F16) {
+        const f16x2v h = cvt_pk_f16(a0, a1);
+        float t0 = __builtin_fmaf((float)h.x, scaling, 0.0f), t1 = __builtin_fmaf((float)h.y, scaling, 0.0f);
+        asm("" : "+v"(t0), "+v"(t1));
+        const f16x2v x = cvt_pk_f16(t0, t1);
+        o0 = __builtin_fmaf((float)x.x, kLog2e, nm0);
+        o1 = __builtin_fmaf((float)x.y, kLog2e, nm1);
+    } else {
+        const bf16x2v h = {(__bf16)a0, (__bf16)a1};
+        float t0 = (float)h.x * scaling, t1 = (float)h.y * scaling;
+        asm("" : "+v"(t0), "+v"(t1));
+        const bf16x2v x = {(__bf16)t0, (__bf16)t1};
+        o0 = __builtin_fmaf((float)x.x, kLog2e, nm0);
+        o1 = __builtin_fmaf((float)x.y, kLog2e, nm1);
+    }
+}
+
+// round_T of two fp32 values, added to acc in fp32
+template <int DT>
+__device__ __forceinline__ float add_rounded2(float acc, float p0, float p1, bool v0, bool v1) {
+    if constexpr (DT == NQ_F16) {
+        const f16x2v h = cvt_pk_f16(p0, p1);
+        acc = v0 ? acc + (float)h.x : acc;
+        return v1 ? acc + (float)h.y : acc;
+    } else {
+        const bf16x2v h = {(__bf16)p0, (__bf16)p1};
+        acc = v0 ? acc + (float)h.x : acc;
+        return v1 ? acc + (float)h.y : acc;
+    }
+}
+
+// One pass over the 64-key LDS stages of a query block: two LDS buffers, the
+// next stage's global loads issued before the current stage is computed and
+// stored to the other buffer after it (one barrier per stage).
+template <int DT, int D, int PASS>
+__device__ __forceinline__ void rowstats_sweep(const RealArgs& a, const uint16_t* kbase, char* lds,
+                                               const uint4 (&qa)[RealTile<D>::KS], int n_it, bool live,
+                                               int q0, int lane, float (&m)[16], float (&z)[16]) {
+    const int g = lane >> 5, c = lane & 31;
+    const int my_diag = q0 / 32;  // this wave's diagonal 32-key block
+    uint4 stage[RealTile<D>::PER_THREAD];
+    tile_load<D>(kbase, 0, a.seq, stage);
+    tile_store<D>(lds, stage);
+    __syncthreads();
+#pragma unroll 1
+    for (int it = 0; it < n_it; ++it) {
+        const char* cur = lds + (it & 1) * RealTile<D>::BUF;
+        if (it + 1 < n_it) tile_load<D>(kbase, (it + 1) * 64, a.seq, stage);
+        if (live) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int kt = 2 * it + h;
+                if (kt > my_diag) continue;
+                const f32x16 acc = logits_regs_lds<DT, D>(qa, cur + h * 32 * RealTile<D>::ROWB, c, g);
+                if (kt < my_diag) {  // every key of the block precedes every row of the wave
+#pragma unroll
+                    for (int j = 0; j < 16; j += 2) {
+                        if constexpr (PASS == 0) {
+                            m[j] = __builtin_fmaxf(m[j], acc[j]);
+                            m[j + 1] = __builtin_fmaxf(m[j + 1], acc[j + 1]);
+                        } else {
+                            float x0, x1;
+                            exp_args2<DT>(acc[j], acc[j + 1], a.scaling, m[j], m[j + 1], x0, x1);
+                            z[j] += __builtin_amdgcn_exp2f(x0);
+                            z[j + 1] += __builtin_amdgcn_exp2f(x1);
+                        }
+                    }
+                } else {
+                    const int key = kt * 32 + c;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const int i = q0 + acc_row(j, lane);
+                        const bool valid = key <= i && i < a.seq;
+                        if constexpr (PASS == 0) {
+                            m[j] = valid ? __builtin_fmaxf(m[j], acc[j]) : m[j];
+                        } else {
+                            const float e = __builtin_amdgcn_exp2f(
+                                __builtin_fmaf(eager_logit<DT>(acc[j], a.scaling), kLog2e, m[j]));
+                            z[j] += valid ? e : 0.0f;
+                        }
+                    }
+                }
+            }
+        }
+        if (it + 1 < n_it) tile_store<D>(lds + ((it + 1) & 1) * RealTile<D>::BUF, stage);
+        __syncthreads();
+    }
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void real_rowstats(RealArgs a) {
+    __shared__ __align__(16) char lds[2 * RealTile<D>::BUF];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 5, c = lane & 31;
+    // items ordered (batch x kv head, query block from the last, query head of
+    // the group): an XCD range covers whole KV groups, whose keys stay in its L2
+    const int item = xcd_item(a);
+    if (item >= a.n_items) return;
+    const int n_blocks = (a.seq + 127) / 128;
+    const int grp = a.hq / a.hkv;
+    const int hh = item % grp;
+    const int rest = item / grp;
+    const int qb = n_blocks - 1 - rest % n_blocks;   // longest rows first
+    const int bg = rest / n_blocks;                  // batch * hkv + kv head
+    const int b = bg / a.hkv, hk = bg - b * a.hkv;
+    const int hq = hk * grp + hh;
+    const int bhq = b * a.hq + hq;
+    const uint16_t* qbase = static_cast<const uint16_t*>(a.q) + (size_t)bhq * a.seq * D;
+    const uint16_t* kbase = static_cast<const uint16_t*>(a.k) + ((size_t)b * a.hkv + hk) * a.seq * D;
+    const int q0 = qb * 128 + wave * 32;             // this wave's first query row
+    const bool live = q0 < a.seq;                    // wave-uniform
+    const int last_key = min(qb * 128 + 127, a.seq - 1);
+    const int n_it = last_key / 64 + 1;              // 64-key stages
+    uint4 qa[RealTile<D>::KS];
+    row_operand<D>(qbase, q0 + c, a.seq, g, qa);
+
+    float m[16], z[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        m[j] = -__builtin_inff();
+        z[j] = 0.0f;
+    }
+    rowstats_sweep<DT, D, 0>(a, kbase, lds, qa, n_it, live, q0, lane, m, z);
+    // row max of the raw logits -> max of the eager logits -> -max * log2(e)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) m[j] = -(eager_logit<DT>(reduce32_max(m[j]), a.scaling) * kLog2e);
+    rowstats_sweep<DT, D, 1>(a, kbase, lds, qa, n_it, live, q0, lane, m, z);
+    if (!live) return;
+    const size_t stat = (size_t)bhq * a.seq;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const float zs = reduce32_sum(z[j]);
+        const int i = q0 + acc_row(j, lane);
+        if (c == 0 && i < a.seq) {
+            a.row_max[stat + i] = m[j];
+            a.row_sum[stat + i] = 1.0f / zs;
+        }
+    }
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
+    __shared__ __align__(16) char lds[2 * RealTile<D>::BUF];
+    __shared__ __align__(16) float st_nm[2][64];
+    __shared__ __align__(16) float st_rz[2][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 5, c = lane & 31;
+    // items ordered (batch x query head, key block): an XCD range walks its
+    // query heads one after the other, so the streamed queries stay in its L2
+    const int item = xcd_item(a);
+    if (item >= a.n_items) return;
+    const int n_blocks = (a.seq + 127) / 128;
+    const int kb = item % n_blocks;                  // first key blocks see the most queries
+    const int bhq = item / n_blocks;
+    const int b = bhq / a.hq, hq = bhq - b * a.hq;
+    const int hk = hq / (a.hq / a.hkv);
+    const uint16_t* qbase = static_cast<const uint16_t*>(a.q) + (size_t)bhq * a.seq * D;
+    const uint16_t* kbase = static_cast<const uint16_t*>(a.k) + ((size_t)b * a.hkv + hk) * a.seq * D;
+    const size_t stat = (size_t)bhq * a.seq;
+    const int k0 = kb * 128 + wave * 32;            // this wave's first key
+    const int key = k0 + c;
+    const int my_first = k0 / 32;                    // first 32-row query block that sees these keys
+    const int it0 = kb * 2;                          // first 64-row query stage of the block
+    const int n_it = (a.seq + 63) / 64;
+    const bool live = k0 < a.seq;
+    uint4 kr[RealTile<D>::KS];
+    row_operand<D>(kbase, key, a.seq, g, kr);
+    float col = 0.0f;
+    const int t = threadIdx.x;
+    uint4 stage[RealTile<D>::PER_THREAD];
+    float snm = 0.0f, srz = 0.0f;  // threads 0..63 carry the row statistics of one row
+    tile_load<D>(qbase, it0 * 64, a.seq, stage);
+    if (t < 64) {
+        const int i = min(it0 * 64 + t, a.seq - 1);
+        snm = a.row_max[stat + i];
+        srz = a.row_sum[stat + i];
+    }
+    tile_store<D>(lds, stage);
+    if (t < 64) {
+        st_nm[0][t] = snm;
+        st_rz[0][t] = srz;
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int it = it0; it < n_it; ++it) {
+        const int cb = (it - it0) & 1;
+        const char* cur = lds + cb * RealTile<D>::BUF;
+        if (it + 1 < n_it) {
+            tile_load<D>(qbase, (it + 1) * 64, a.seq, stage);
+            if (t < 64) {
+                const int i = min((it + 1) * 64 + t, a.seq - 1);
+                snm = a.row_max[stat + i];
+                srz = a.row_sum[stat + i];
+            }
+        }
+        if (live) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int qt = 2 * it + h;
+                if (qt < my_first) continue;
+                const f32x16 acc = logits_lds_regs<DT, D>(cur + h * 32 * RealTile<D>::ROWB, kr, c, g);
+                // interior blocks (all rows after all keys, all rows < seq) skip the masks
+                const bool interior = qt > my_first && qt * 32 + 32 <= a.seq;
+#pragma unroll
+                for (int jq = 0; jq < 4; ++jq) {
+                    const int r0 = 8 * jq + 4 * g;  // rows r0 .. r0 + 3 of the 32-row block
+                    const float4 nm4 = *reinterpret_cast<const float4*>(&st_nm[cb][32 * h + r0]);
+                    const float4 rz4 = *reinterpret_cast<const float4*>(&st_rz[cb][32 * h + r0]);
+                    const float nm[4] = {nm4.x, nm4.y, nm4.z, nm4.w};
+                    const float rz[4] = {rz4.x, rz4.y, rz4.z, rz4.w};
+#pragma unroll
+                    for (int u = 0; u < 4; u += 2) {
+                        const int j = 4 * jq + u;
+                        const int i = qt * 32 + r0 + u;
+                        float x0, x1;
+                        exp_args2<DT>(acc[j], acc[j + 1], a.scaling, nm[u], nm[u + 1], x0, x1);
+                        const float p0 = __builtin_amdgcn_exp2f(x0) * rz[u];
+                        const float p1 = __builtin_amdgcn_exp2f(x1) * rz[u + 1];
+                        if (interior) {
+                            col = add_rounded2<DT>(col, p0, p1, true, true);
+                        } else {
+                            const bool v0 = (qt > my_first || key <= i) && i < a.seq;
+                            const bool v1 = (qt > my_first || key <= i + 1) && i + 1 < a.seq;
+                            col = add_rounded2<DT>(col, p0, p1, v0, v1);
+                        }
+                    }
+                }
+            }
+        }
+        if (it + 1 < n_it) {
+            tile_store<D>(lds + (cb ^ 1) * RealTile<D>::BUF, stage);
+            if (t < 64) {
+                st_nm[cb ^ 1][t] = snm;
+                st_rz[cb ^ 1][t] = srz;
+            }
+        }
+        __syncthreads();
+    }
+    col += __shfl_xor(col, 32, 64);
+    if (g == 0 && key < a.seq) a.colsum[stat + key] = col;
+}
+
 __global__ __launch_bounds__(256) void head_mean_accumulate(const float* colsum, float* importance, int hq,
                                                             int seq) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -320,11 +694,21 @@ __global__ __launch_bounds__(256) void head_mean_accumulate(const float* colsum,
 
 template <int DT, int D>
 static hipError_t launch_real(const RealArgs& a, hipStream_t st) {
-    const int n_tiles = (a.seq + 31) / 32;
-    dim3 grid(n_tiles, a.batch * a.hq);
-    hipLaunchKernelGGL((real_sweep<DT, D, 0>), grid, dim3(64), 0, st, a);
-    hipLaunchKernelGGL((real_sweep<DT, D, 1>), grid, dim3(64), 0, st, a);
-    hipLaunchKernelGGL((real_sweep<DT, D, 2>), grid, dim3(64), 0, st, a);
+    if constexpr (DT == NQ_F32) {
+        const int n_tiles = (a.seq + 31) / 32;
+        dim3 grid(n_tiles, a.batch * a.hq);
+        hipLaunchKernelGGL((real_sweep<DT, D, 0>), grid, dim3(64), 0, st, a);
+        hipLaunchKernelGGL((real_sweep<DT, D, 1>), grid, dim3(64), 0, st, a);
+        hipLaunchKernelGGL((real_sweep<DT, D, 2>), grid, dim3(64), 0, st, a);
+    } else {
+        RealArgs w = a;
+        const int n_blocks = (a.seq + 127) / 128;
+        w.n_items = n_blocks * a.batch * a.hq;
+        w.per_xcd = (w.n_items + 7) / 8;
+        dim3 grid(8 * w.per_xcd);
+        hipLaunchKernelGGL((real_rowstats<DT, D>), grid, dim3(256), 0, st, w);
+        hipLaunchKernelGGL((real_colsum<DT, D>), grid, dim3(256), 0, st, w);
+    }
     hipLaunchKernelGGL(head_mean_accumulate, dim3((a.seq + 255) / 256, a.batch), dim3(256), 0, st, a.colsum,
                        a.importance, a.hq, a.seq);
     return hipGetLastError();

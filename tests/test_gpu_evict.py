@@ -183,14 +183,17 @@ def test_truncation_with_protected_layers_gathers_fp16_exactly():
         assert torch.equal(c.value_cache[li].cpu(), ref.value_cache[li])
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_real_scorer_kernel_matches_eager_oracle(dtype):
+@pytest.mark.parametrize("dtype,s,d,hq,hkv", [
+    (torch.float16, 300, 64, 8, 2), (torch.bfloat16, 300, 64, 8, 2), (torch.float32, 300, 64, 8, 2),
+    # several 128-row blocks, partial last tile, GQA group 4, every head dim
+    (torch.float16, 700, 128, 8, 2), (torch.bfloat16, 515, 128, 4, 1), (torch.float16, 260, 96, 4, 4),
+    (torch.bfloat16, 200, 256, 2, 1), (torch.float16, 33, 128, 4, 2)])
+def test_real_scorer_kernel_matches_eager_oracle(dtype, s, d, hq, hkv):
     from nexusquant_amd.scoring import score_real_accumulate
-    print(f"[gpu] real scorer {dtype}", flush=True)
-    g = torch.Generator().manual_seed(3)
-    s, d = 300, 64
-    q = [(torch.randn(1, 8, s, d, generator=g) * 0.7).to(dtype) for _ in range(2)]
-    k = [(torch.randn(1, 2, s, d, generator=g) * 0.7).to(dtype) for _ in range(2)]
+    print(f"[gpu] real scorer {dtype} s={s} d={d} hq={hq} hkv={hkv}", flush=True)
+    g = torch.Generator().manual_seed(3 + s + d)
+    q = [(torch.randn(1, hq, s, d, generator=g) * 0.7).to(dtype) for _ in range(2)]
+    k = [(torch.randn(1, hkv, s, d, generator=g) * 0.7).to(dtype) for _ in range(2)]
     imp = torch.zeros(1, s, device=DEV)
     for ql, kl in zip(q, k):
         score_real_accumulate(ql.to(DEV), kl.to(DEV), imp, d ** -0.5)
