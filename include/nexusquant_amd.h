@@ -26,6 +26,11 @@ extern "C" {
 #define NQ_EUNSUPPORTED -2 /* valid request this build does not implement */
 #define NQ_EHIP -3        /* HIP runtime error (launch, device) */
 
+/* what nq_quantize does with rows whose keep entry is 0 */
+#define NQ_KEEP_ZERO 0
+#define NQ_KEEP_WRITE_KEPT 1
+#define NQ_KEEP_WRITE_EVICTED 2
+
 /* element types of input tensors */
 #define NQ_F16 0
 #define NQ_BF16 1
@@ -46,10 +51,17 @@ extern "C" {
  *   cosets [batch, heads, seq_out, D/64] coset bitmaps;
  *   scales [batch, heads, seq_out] fp32 row scales.
  * Row selection: output row t of batch b reads source token gather[b*seq_out+t]
- * (truncation) or token t (gather == NULL, then seq_out == seq_in); rows whose
- * keep[b*seq_in + src] == 0 are zeroed before quantization (mask eviction).
+ * (truncation) or token t (gather == NULL, then seq_out == seq_in).  With a
+ * keep list, keep_mode says what happens to rows whose keep[b*seq_in + src]
+ * is 0: NQ_KEEP_ZERO zeroes them before quantization (mask eviction);
+ * NQ_KEEP_WRITE_KEPT writes only the rows with keep != 0 and
+ * NQ_KEEP_WRITE_EVICTED only the rows with keep == 0, leaving the other rows
+ * of every output untouched (soft eviction: two launches, kept rows at the
+ * layer's levels and evicted rows at levels 2, into the same outputs).
  * RoPE tables are fp32 [rope_n_pos, head_dim/2]; keys use row position
  * src (inverse) and t (forward).
+ *
+ * Replaces (keep_mode 1 + 2): the soft-eviction loop   pipeline.py:1129-1183
  *
  * Replaces: NexusQuantQuantOnly.compress            pipeline.py:232-265
  *           NexusQuantEvict.compress (hard path)     pipeline.py:1190-1242
@@ -65,7 +77,7 @@ typedef struct nq_quant_desc {
     int32_t dtype;          /* NQ_F16 / NQ_BF16 / NQ_F32 */
     int32_t levels;         /* 2, 4, 8 or 16 */
     int32_t is_key;         /* 1: inverse/forward RoPE around the quantizer */
-    int32_t reserved;
+    int32_t keep_mode;      /* NQ_KEEP_ZERO / NQ_KEEP_WRITE_KEPT / NQ_KEEP_WRITE_EVICTED */
     /* device arrays of n_tensors base addresses (uint64); recon/syms/cosets/
      * scales arrays may be NULL to skip that output */
     const uint64_t* src;

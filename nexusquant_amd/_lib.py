@@ -13,6 +13,7 @@ import threading
 from .build import LIB_PATH
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
+NQ_KEEP_ZERO, NQ_KEEP_WRITE_KEPT, NQ_KEEP_WRITE_EVICTED = 0, 1, 2
 ABI_VERSION = 1  # NQ_ABI_VERSION of the header these bindings mirror
 _P = ctypes.c_void_p
 
@@ -24,7 +25,7 @@ class QuantDesc(ctypes.Structure):
         ("batch", ctypes.c_int32), ("heads", ctypes.c_int32), ("seq_in", ctypes.c_int32),
         ("seq_out", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("dtype", ctypes.c_int32), ("levels", ctypes.c_int32), ("is_key", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("keep_mode", ctypes.c_int32),
         ("src", _P), ("recon", _P), ("syms", _P), ("cosets", _P), ("scales", _P),
         ("gather", _P), ("keep", _P), ("rope_cos", _P), ("rope_sin", _P),
         ("rope_n_pos", ctypes.c_int64),

@@ -32,6 +32,7 @@ struct QuantArgs {
     uint32_t heads, seq_in, seq_out, rows;
     uint32_t n_tensors, bh, work, per_xcd;  // work items = ceil(seq_out/64) * bh * n_tensors
     float hscale;
+    int32_t keep_mode;                      // NQ_KEEP_*
 };
 
 // ------------------------------------------------------------------ E8 ----
@@ -300,8 +301,8 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     const uint32_t bh = rest % a.bh;
     const uint32_t tile = rest / a.bh;
     const uint32_t t_raw = tile * 64u + (threadIdx.x >> 2);
-    const bool active = t_raw < a.seq_out;
-    const uint32_t t_out = active ? t_raw : a.seq_out - 1u;  // idle quads recompute a valid row
+    const bool in_range = t_raw < a.seq_out;
+    const uint32_t t_out = in_range ? t_raw : a.seq_out - 1u;  // idle quads recompute a valid row
     const uint32_t b = bh / a.heads;
     uint32_t t_in = t_out;
     if (a.gather) {
@@ -311,6 +312,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     }
     bool keep = true;
     if (a.keep) keep = a.keep[(size_t)b * a.seq_in + t_in] != 0;
+    // rows this launch writes: all, or (soft eviction) only the kept / only the evicted ones
+    const bool active = in_range && (a.keep_mode == NQ_KEEP_ZERO || keep == (a.keep_mode == NQ_KEEP_WRITE_KEPT));
+    if (a.keep_mode != NQ_KEEP_ZERO) keep = true;  // selected rows are quantized as they are
 
     float x[C][8];
     const void* src = reinterpret_cast<const void*>(a.src[tensor]);
@@ -555,6 +559,11 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     NQ_CHECK_ARG(d->gather != nullptr || d->seq_out == d->seq_in,
                  "nq_quantize: seq_out must equal seq_in without a gather list");
     NQ_CHECK_ARG(d->src != nullptr, "nq_quantize: src is NULL");
+    NQ_CHECK_ARG(d->keep_mode == NQ_KEEP_ZERO || d->keep_mode == NQ_KEEP_WRITE_KEPT ||
+                     d->keep_mode == NQ_KEEP_WRITE_EVICTED,
+                 "nq_quantize: keep_mode %d unknown", d->keep_mode);
+    NQ_CHECK_ARG(d->keep_mode == NQ_KEEP_ZERO || d->keep != nullptr,
+                 "nq_quantize: keep_mode %d needs a keep list", d->keep_mode);
     const uint64_t rows = (uint64_t)d->batch * d->heads * d->seq_out;
     NQ_CHECK_ARG(rows < (1ull << 31), "nq_quantize: %llu rows per tensor exceeds 2^31", (unsigned long long)rows);
     if (rows == 0) return NQ_OK;
@@ -579,6 +588,7 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     a.seq_out = (uint32_t)d->seq_out;
     a.rows = (uint32_t)rows;
     a.hscale = d->hadamard_scale;
+    a.keep_mode = d->keep_mode;
     a.n_tensors = (uint32_t)d->n_tensors;
     a.bh = (uint32_t)d->batch * (uint32_t)d->heads;
     const uint64_t work = (uint64_t)((d->seq_out + 63) / 64) * a.bh * a.n_tensors;

@@ -158,12 +158,17 @@ def _addr(t: Optional[torch.Tensor]):
 def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: int,
                      rope_base: float = 10000.0, rope_scaling: Optional[dict] = None,
                      gather: Optional[torch.Tensor] = None, keep: Optional[torch.Tensor] = None,
+                     keep_mode: int = _lib.NQ_KEEP_ZERO, recon_out: Optional[Sequence[torch.Tensor]] = None,
                      recon: bool = True, codes: bool = False, launch_events=None,
                      ) -> Tuple[Optional[List[torch.Tensor]], Optional[List[PackedCodes]]]:
     """Run the fused quantizer over same-shaped [b, h, s, d] tensors in one launch.
 
     gather: int32/int64 [b, seq_out] source token per output row (truncation).
-    keep:   bool/uint8 [b, seq_in]; rows with keep == 0 are zeroed (mask eviction).
+    keep:   bool/uint8 [b, seq_in]; with keep_mode NQ_KEEP_ZERO rows with keep == 0
+            are zeroed (mask eviction); NQ_KEEP_WRITE_KEPT / NQ_KEEP_WRITE_EVICTED
+            write only the kept / only the evicted rows (soft eviction).
+    recon_out: fp16 [b, h, seq_out, d] tensors to write the reconstructions into
+            (rows this launch does not write keep their contents).
     launch_events: optional (start, end) torch.cuda.Event pair recorded on the
     launch stream immediately around the kernel launch.
     Returns (fp16 reconstructions or None, PackedCodes or None), one per tensor.
@@ -205,10 +210,23 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
         if tuple(k.shape) != (b, s):
             raise ValueError(f"keep must be [batch, seq] = {(b, s)}, got {tuple(k.shape)}")
 
+    if keep_mode not in (_lib.NQ_KEEP_ZERO, _lib.NQ_KEEP_WRITE_KEPT, _lib.NQ_KEEP_WRITE_EVICTED):
+        raise ValueError(f"unknown keep_mode {keep_mode}")
+    if keep_mode != _lib.NQ_KEEP_ZERO and k is None:
+        raise ValueError("keep_mode other than NQ_KEEP_ZERO needs a keep mask")
     n = len(src)
     # one allocation per output kind; every tensor gets a contiguous slice
     recon_t = None
-    if recon:
+    if recon_out is not None:
+        recon_t = list(recon_out)
+        if len(recon_t) != n:
+            raise ValueError("recon_out must hold one tensor per input tensor")
+        for r in recon_t:
+            _lib.require_device(r, "recon_out tensor")
+            if (tuple(r.shape) != (b, h, seq_out, d) or r.dtype != torch.float16 or not r.is_contiguous()
+                    or r.data_ptr() % 16):
+                raise ValueError(f"recon_out tensors must be contiguous 16-byte aligned fp16 {(b, h, seq_out, d)}")
+    elif recon:
         recon_t = list(torch.empty(n, b, h, seq_out, d, dtype=torch.float16, device=dev).unbind(0))
     codes_t = None
     if codes:
@@ -233,7 +251,7 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
     arrays = dict(zip(names, staged.arrays))
     desc = _lib.QuantDesc(
         n_tensors=n, batch=b, heads=h, seq_in=s, seq_out=seq_out, head_dim=d,
-        dtype=_lib.dtype_code(t0.dtype), levels=levels, is_key=int(is_key),
+        dtype=_lib.dtype_code(t0.dtype), levels=levels, is_key=int(is_key), keep_mode=keep_mode,
         src=_addr(arrays["src"]), recon=_addr(arrays["recon"]), syms=_addr(arrays["syms"]),
         cosets=_addr(arrays["cosets"]), scales=_addr(arrays["scales"]),
         gather=_addr(g), keep=_addr(k), rope_cos=_addr(cos), rope_sin=_addr(sin),

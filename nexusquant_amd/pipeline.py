@@ -153,7 +153,8 @@ class NexusQuantEvict:
     Constructor arguments, validation errors and the (cache, mask) return
     convention follow NexusQuantEvict (pipeline.py:535-668, 1050-1244).  Evicted
     rows are zeroed inside the fused quantizer (mask eviction).  soft_eviction
-    and merge_eviction are not part of this build's hot path and raise.
+    quantizes evicted rows at levels 2 instead (two launches into the same
+    outputs); merge_eviction is not part of this build's hot path and raises.
     """
 
     def __init__(self, head_dim: int = 128, bits: int = 2, key_bits: int = None, value_bits: int = None,
@@ -310,8 +311,11 @@ class NexusQuantEvict:
             return self._score_importance_real(model, input_ids), k_score
         return self._score_importance(k_score), k_score
 
-    def _apply(self, past_key_values, n_layers: int, skip: set, *, keep=None, gather=None):
-        """Quantize (or pass through at fp16) every layer with one mask / gather list."""
+    def _apply(self, past_key_values, n_layers: int, skip: set, *, keep=None, gather=None, soft=False):
+        """Quantize (or pass through at fp16) every layer with one mask / gather list.
+
+        soft: kept rows at the layer's levels and evicted rows at levels 2, no row
+        zeroed (pipeline.py:1129-1183); protected layers pass through unmasked."""
         todo: Dict[tuple, List[int]] = {}
         passthrough: Dict[tuple, List[int]] = {}
         for li in range(n_layers):
@@ -334,6 +338,8 @@ class NexusQuantEvict:
 
         for key, layers in passthrough.items():
             kp, gp = layer_args(key[0])
+            if soft:
+                kp = None
             ks = [get_layer_kv(past_key_values, li)[0] for li in layers]
             vs = [get_layer_kv(past_key_values, li)[1] for li in layers]
             k_out = gather_rows(ks, gather=gp, keep=kp)
@@ -345,16 +351,25 @@ class NexusQuantEvict:
             kp, gp = layer_args(key[0])
             ks = [get_layer_kv(past_key_values, li)[0] for li in layers]
             vs = [get_layer_kv(past_key_values, li)[1] for li in layers]
-            k_out, _ = quantize_tensors(ks, is_key=True, levels=kl, rope_base=self.rope_base,
-                                        rope_scaling=self.rope_scaling, gather=gp, keep=kp)
-            v_out, _ = quantize_tensors(vs, is_key=False, levels=vl, gather=gp, keep=kp)
+            if soft:
+                from ._lib import NQ_KEEP_WRITE_EVICTED, NQ_KEEP_WRITE_KEPT
+                k_out, _ = quantize_tensors(ks, is_key=True, levels=kl, rope_base=self.rope_base,
+                                            rope_scaling=self.rope_scaling, keep=kp, keep_mode=NQ_KEEP_WRITE_KEPT)
+                quantize_tensors(ks, is_key=True, levels=2, rope_base=self.rope_base,
+                                 rope_scaling=self.rope_scaling, keep=kp, keep_mode=NQ_KEEP_WRITE_EVICTED,
+                                 recon_out=k_out)
+                v_out, _ = quantize_tensors(vs, is_key=False, levels=vl, keep=kp, keep_mode=NQ_KEEP_WRITE_KEPT)
+                quantize_tensors(vs, is_key=False, levels=2, keep=kp, keep_mode=NQ_KEEP_WRITE_EVICTED,
+                                 recon_out=v_out)
+            else:
+                k_out, _ = quantize_tensors(ks, is_key=True, levels=kl, rope_base=self.rope_base,
+                                            rope_scaling=self.rope_scaling, gather=gp, keep=kp)
+                v_out, _ = quantize_tensors(vs, is_key=False, levels=vl, gather=gp, keep=kp)
             for i, li in enumerate(layers):
                 set_layer_kv(past_key_values, li, k_out[i], v_out[i])
 
     def compress(self, past_key_values, model=None, input_ids=None):
         """Evict + quantize in place; returns (cache, prefix_attention_mask [b, s] float)."""
-        if self.soft_eviction:
-            raise NotImplementedError("soft_eviction is not part of the gfx950 hot path")
         if self.merge_eviction:
             raise NotImplementedError("merge_eviction is not part of the gfx950 hot path")
         n = num_layers(past_key_values)
@@ -367,6 +382,10 @@ class NexusQuantEvict:
         skip = self._skip_layers(past_key_values, n)
         if self.min_context_for_compression > 0 and seq < self.min_context_for_compression:
             return past_key_values, torch.ones(b, seq, device=device)
+        if self.soft_eviction:
+            # every position stays visible; evicted rows are only coarser (pipeline.py:1129-1183)
+            self._apply(past_key_values, n, skip, keep=keep, soft=True)
+            return past_key_values, torch.ones(b, seq, dtype=torch.float32, device=device)
         self._apply(past_key_values, n, skip, keep=keep)
         return past_key_values, prefix_attention_mask
 

@@ -485,6 +485,54 @@ def evict_mask_compress(cache, key_levels: int, value_levels: int, rate: float,
     return cache, mask_out
 
 
+def evict_soft_compress(cache, key_levels: int, value_levels: int, rate: float,
+                        sliding_window: int = 32, obs_window: int = 32, rope_base: float = 10000.0,
+                        rope_scaling: Optional[dict] = None, skip_layers: Sequence[int] = (),
+                        protected_positions=None, layer_bit_profile: str = "uniform"):
+    """Soft-eviction path of NexusQuantEvict.compress (pipeline.py:1129-1183).
+
+    Kept rows are quantized at the layer's levels, evicted rows at levels 2 (the
+    reference computes both on every row and selects with the 0/1 mask);
+    protected layers are cast to fp16 unmasked.  Returns (cache, all-ones mask).
+    """
+    n = num_layers(cache)
+    k0, _ = get_layer_kv(cache, 0)
+    b, _, seq, _ = k0.shape
+    importance = score_keykey(k0.float(), obs_window)
+    keep = build_keep_mask(importance, seq, rate, sliding_window, protected_positions)
+    ones = torch.ones(b, seq, dtype=torch.float32)
+    for li in range(n):
+        k, v = get_layer_kv(cache, li)
+        k = k.float()
+        v = v.float()
+        if li in skip_layers:
+            set_layer_kv(cache, li, k.half(), v.half())
+            continue
+        _, h, s_l, d = k.shape
+        H = hadamard_matrix(d).to(k.device).float()
+        kl, vl = resolve_layer_levels(li, n, key_levels, value_levels, layer_bit_profile)
+        m4 = keep[:, :s_l].unsqueeze(1).unsqueeze(-1).float()
+        k_out = []
+        for bi in range(b):
+            k_nr = inverse_rope(k[bi], base=rope_base, rope_scaling=rope_scaling)
+            k_flat = torch.einsum('hsd,de->hse', k_nr, H).reshape(-1, d)
+            full = e8_quantize_perhead(k_flat, levels=kl)
+            one_bit = e8_quantize_perhead(k_flat, levels=2)
+            kf = m4[bi].expand(h, s_l, 1).reshape(h * s_l, 1)
+            k_q = full * kf + one_bit * (1.0 - kf)
+            k_back = torch.einsum('hsd,ed->hse', k_q.reshape(h, s_l, d), H)
+            k_out.append(forward_rope(k_back, base=rope_base, rope_scaling=rope_scaling))
+        k_out = torch.stack(k_out, dim=0).to(torch.float16)
+        v_flat = torch.einsum('bhsd,de->bhse', v, H).reshape(-1, d)
+        full = e8_quantize_perhead(v_flat, levels=vl)
+        one_bit = e8_quantize_perhead(v_flat, levels=2)
+        vf = m4.expand(b, h, s_l, 1).reshape(b * h * s_l, 1)
+        v_q = full * vf + one_bit * (1.0 - vf)
+        v_out = torch.einsum('bhsd,ed->bhse', v_q.reshape(b, h, s_l, d), H).to(torch.float16)
+        set_layer_kv(cache, li, k_out, v_out)
+    return cache, ones
+
+
 def evict_truncate_compress(cache, key_levels: int, value_levels: int, rate: float,
                             sliding_window: int = 32, obs_window: int = 32,
                             rope_base: float = 10000.0, rope_scaling: Optional[dict] = None,

@@ -176,5 +176,22 @@ def real_scorer_fixture():
     save("real_scorer", q=qs, k=kss, scaling=captured[0][2], importance=imp)
 
 
+def make_soft():
+    """8. Soft eviction (pipeline.py:1129-1183): b = 2, K3V2 at rate 0.5, evicted
+    rows at levels 2, first and last layer protected (cast to fp16 unmasked)."""
+    ks, vs = synth_kv(81, 4, 2, 2, 128, 128, 10000.0, sink=True)
+    nq = NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.5, sliding_window=16,
+                         rope_base=10000.0, soft_eviction=True, protect_boundary=1)
+    imp = nq._score_importance(ks[0].float())
+    c = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+    _, mask = nq.compress(c)
+    save("evict_soft", k_in=torch.stack(ks), v_in=torch.stack(vs), importance=imp, mask=mask,
+         k_out=torch.stack(c.key_cache), v_out=torch.stack(c.value_cache))
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[2:] == ["evict_soft"]:
+        make_soft()
+    else:
+        main()
+        make_soft()

@@ -152,6 +152,49 @@ def test_boundary_protection_matches_reference_fixture(golden):
             _assert_close_rows(c.value_cache[li], g["v_out"][li])
 
 
+def test_soft_eviction_matches_reference_fixture(golden):
+    import nexusquant_amd as nq
+    print("[gpu] soft eviction fixture", flush=True)
+    g = golden("evict_soft")
+    c = Cache([torch.from_numpy(k).to(DEV) for k in g["k_in"]], [torch.from_numpy(v).to(DEV) for v in g["v_in"]])
+    comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.5, sliding_window=16,
+                              rope_base=10000.0, soft_eviction=True, protect_boundary=1)
+    _, mask = comp.compress(c)
+    assert np.array_equal(mask.cpu().numpy(), g["mask"])
+    n = len(c.key_cache)
+    for li in range(n):
+        assert c.key_cache[li].dtype == torch.float16
+        if li in (0, n - 1):                    # protected: fp16 cast, nothing evicted
+            assert np.array_equal(c.key_cache[li].cpu().numpy(), g["k_out"][li])
+            assert np.array_equal(c.value_cache[li].cpu().numpy(), g["v_out"][li])
+        else:
+            _assert_close_rows(c.key_cache[li], g["k_out"][li])
+            _assert_close_rows(c.value_cache[li], g["v_out"][li])
+
+
+def test_soft_eviction_rows_bitexact_vs_spec():
+    # kept rows at levels 8 and evicted rows at levels 2, each bit-exact against the C spec
+    from nexusquant_amd import _lib
+    from nexusquant_amd.ops import quantize_tensors
+    print("[gpu] soft eviction rows vs spec", flush=True)
+    x = _keys(2, 3, 150, 128, torch.float16, seed=5)
+    g = torch.Generator().manual_seed(6)
+    keep = (torch.rand(2, 150, generator=g) > 0.4).to(torch.uint8)
+    xd, kd = x.to(DEV), keep.to(DEV)
+    for is_key, lv in ((True, 8), (False, 4)):
+        out, _ = quantize_tensors([xd], is_key=is_key, levels=lv, keep=kd, keep_mode=_lib.NQ_KEEP_WRITE_KEPT)
+        quantize_tensors([xd], is_key=is_key, levels=2, keep=kd, keep_mode=_lib.NQ_KEEP_WRITE_EVICTED,
+                         recon_out=out)
+        torch.cuda.synchronize()
+        got = out[0].cpu().numpy().reshape(-1, 128)
+        from gpu_helpers import assert_same_fp16, spec_tensor
+        ref_keep = spec_tensor(x.float().numpy(), lv, is_key)["recon"]
+        ref_evict = spec_tensor(x.float().numpy(), 2, is_key)["recon"]
+        sel = np.repeat(keep.numpy()[:, None, :], 3, axis=1).reshape(-1).astype(bool)
+        want = np.where(sel[:, None], ref_keep, ref_evict)
+        assert_same_fp16(got, want)
+
+
 @pytest.mark.parametrize("rate", [25, 60])
 def test_truncation_matches_reference_fixture(golden, rate):
     import nexusquant_amd as nq

@@ -105,6 +105,19 @@ def test_boundary_protected_eviction_matches_reference(golden):
     assert np.array_equal(_stack(c, "value_cache"), g["v_out"])
 
 
+def test_soft_eviction_matches_reference(golden):
+    g = golden("evict_soft")
+    imp = T.score_keykey(_t(g["k_in"][0]).float(), 32)
+    assert np.array_equal(imp.numpy(), g["importance"])
+    c = _cache(g)
+    skip = T.boundary_skip_layers(len(c.key_cache), 1)
+    _, mask = T.evict_soft_compress(c, 8, 4, 0.5, sliding_window=16, rope_base=10000.0,
+                                    skip_layers=skip)
+    assert np.array_equal(mask.numpy(), g["mask"])
+    assert np.array_equal(_stack(c, "key_cache"), g["k_out"])
+    assert np.array_equal(_stack(c, "value_cache"), g["v_out"])
+
+
 @pytest.mark.parametrize("rate", [25, 60])
 def test_truncation_matches_reference(golden, rate):
     g = golden(f"evict_truncate_r{rate}")

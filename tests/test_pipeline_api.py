@@ -71,12 +71,10 @@ def test_truncate_batch_gt1_error_message_matches_reference():
         nq.NexusQuantEvictTruncate().compress(Cache())
 
 
-def test_soft_and_merge_eviction_are_refused():
+def test_merge_eviction_is_refused():
     class Cache:
         key_cache = [torch.zeros(1, 1, 4, 128)]
         value_cache = [torch.zeros(1, 1, 4, 128)]
-    with pytest.raises(NotImplementedError):
-        nq.NexusQuantEvict(soft_eviction=True).compress(Cache())
     with pytest.raises(NotImplementedError):
         nq.NexusQuantEvict(merge_eviction=True).compress(Cache())
 
