@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define NQ_ABI_VERSION 1
+#define NQ_ABI_VERSION 2
 
 /* status codes */
 #define NQ_OK 0
@@ -59,7 +59,12 @@ extern "C" {
  * of every output untouched (soft eviction: two launches, kept rows at the
  * layer's levels and evicted rows at levels 2, into the same outputs).
  * RoPE tables are fp32 [rope_n_pos, head_dim/2]; keys use row position
- * src (inverse) and t (forward).
+ * src (inverse) and t (forward).  For power-of-two head dims the kernel
+ * folds the rotation into the top Hadamard stage, whose pairs (i, i + d/2)
+ * are the RoPE pairs; it then needs fl(cos - sin) and fl(cos + sin), which it
+ * reads from rope_cos_minus_sin / rope_cos_plus_sin when given (same layout)
+ * and otherwise forms from rope_cos / rope_sin.  Either way the results are
+ * identical; the precomputed tables save two operations per pair.
  *
  * Replaces (keep_mode 1 + 2): the soft-eviction loop   pipeline.py:1129-1183
  *
@@ -92,6 +97,8 @@ typedef struct nq_quant_desc {
     int64_t rope_n_pos;
     float hadamard_scale;   /* h_D of the reference's Sylvester matrix */
     float reserved_f;
+    const float* rope_cos_minus_sin;  /* optional, [rope_n_pos, head_dim/2]; NULL: formed in-kernel */
+    const float* rope_cos_plus_sin;
 } nq_quant_desc;
 
 int nq_quantize(const nq_quant_desc* desc, void* stream);
@@ -176,6 +183,8 @@ typedef struct nq_codes_desc {
     int64_t rope_n_pos;
     float hadamard_scale;
     float reserved_f;
+    const float* rope_cos_minus_sin;  /* optional, as in nq_quant_desc */
+    const float* rope_cos_plus_sin;
 } nq_codes_desc;
 
 /*

@@ -14,7 +14,7 @@ from .build import LIB_PATH
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
 NQ_KEEP_ZERO, NQ_KEEP_WRITE_KEPT, NQ_KEEP_WRITE_EVICTED = 0, 1, 2
-ABI_VERSION = 1  # NQ_ABI_VERSION of the header these bindings mirror
+ABI_VERSION = 2  # NQ_ABI_VERSION of the header these bindings mirror
 _P = ctypes.c_void_p
 
 
@@ -30,6 +30,7 @@ class QuantDesc(ctypes.Structure):
         ("gather", _P), ("keep", _P), ("rope_cos", _P), ("rope_sin", _P),
         ("rope_n_pos", ctypes.c_int64),
         ("hadamard_scale", ctypes.c_float), ("reserved_f", ctypes.c_float),
+        ("rope_cos_minus_sin", _P), ("rope_cos_plus_sin", _P),
     ]
 
 
@@ -43,6 +44,7 @@ class CodesDesc(ctypes.Structure):
         ("syms", _P), ("cosets", _P), ("scales", _P), ("out", _P),
         ("rope_cos", _P), ("rope_sin", _P), ("rope_n_pos", ctypes.c_int64),
         ("hadamard_scale", ctypes.c_float), ("reserved_f", ctypes.c_float),
+        ("rope_cos_minus_sin", _P), ("rope_cos_plus_sin", _P),
     ]
 
 

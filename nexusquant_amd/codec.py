@@ -22,7 +22,7 @@ import torch
 from . import _lib
 from .hadamard import hadamard_constant
 from .ops import PackedCodes, _addr, _PtrArrays
-from .rope import device_table
+from .rope import device_merged_table, device_table
 
 
 def _codes_desc(codes: Sequence[PackedCodes], outs: Sequence[torch.Tensor], rope=None,
@@ -37,15 +37,18 @@ def _codes_desc(codes: Sequence[PackedCodes], outs: Sequence[torch.Tensor], rope
     staged = _PtrArrays([[c.syms for c in codes], [c.cosets for c in codes], [c.scales for c in codes],
                          list(outs)], dev)
     arrays = staged.arrays
-    cos = sin = None
+    cos = sin = dm = dp = None
     n_pos = 0
     if rope is not None:
-        cos, sin = rope
+        cos, sin = rope[0], rope[1]
+        if len(rope) == 4:
+            dm, dp = rope[2], rope[3]
         n_pos = cos.shape[0]
     desc = _lib.CodesDesc(n_tensors=len(codes), batch=b, heads=h, seq=s, head_dim=head_dim,
                           levels=c0.levels, is_key=int(rope is not None), syms=_addr(arrays[0]),
                           cosets=_addr(arrays[1]), scales=_addr(arrays[2]), out=_addr(arrays[3]),
                           rope_cos=_addr(cos), rope_sin=_addr(sin), rope_n_pos=n_pos,
+                          rope_cos_minus_sin=_addr(dm), rope_cos_plus_sin=_addr(dp),
                           hadamard_scale=hadamard_constant(c0.padded_dim))
     return desc, staged
 
@@ -61,7 +64,11 @@ def dequantize(codes: Sequence[PackedCodes], rope_base: float = 10000.0,
     b, h, s = c0.scales.shape
     dev = c0.scales.device
     outs = [torch.empty(b, h, s, c0.head_dim, dtype=torch.float16, device=dev) for _ in codes]
-    rope = device_table(s, c0.head_dim, rope_base, rope_scaling, dev) if c0.is_key else None
+    rope = None
+    if c0.is_key:
+        rope = device_table(s, c0.head_dim, rope_base, rope_scaling, dev)
+        if c0.head_dim != 96:
+            rope = rope + device_merged_table(rope[0].shape[0], c0.head_dim, rope_base, rope_scaling, dev)
     desc, staged = _codes_desc(codes, outs, rope, head_dim=c0.head_dim)
     with torch.cuda.device(dev):
         try:

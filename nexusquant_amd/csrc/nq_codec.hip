@@ -17,6 +17,8 @@ struct CodecArgs {
     const uint64_t* out;
     const float* rope_cos;
     const float* rope_sin;
+    const float* rope_dm;
+    const float* rope_dp;
     uint32_t heads, seq, n_tensors, bh, work, per_xcd;
     float hscale;
 };
@@ -94,6 +96,9 @@ __global__ __launch_bounds__(256) void dequant_kernel(CodecArgs a) {
     float scale;
     unpack_points<D, L>(a, tensor, row, q, x, coset, scale);
     const float g = quad_sign(q) * (a.hscale * scale);
+    // keys with DR == D: the top Hadamard stage merges with forward RoPE, as in
+    // the quantizer (the sum of exact partial transforms is the same number)
+    constexpr bool MERGED = IS_KEY && DR == D;
     constexpr bool EXACT_F16 = D * (L / 2) <= 1024;
     if constexpr (EXACT_F16) {
         half2v hp[C][4];
@@ -102,7 +107,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(CodecArgs a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k)
                 hp[c][k] = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(x[c][2 * k], x[c][2 * k + 1]));
-        fwht_row_f16<C>(hp, q);
+        fwht_row_f16<C, !MERGED>(hp, q);
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
@@ -111,13 +116,17 @@ __global__ __launch_bounds__(256) void dequant_kernel(CodecArgs a) {
                 x[c][2 * k + 1] = __builtin_fmaf((float)hp[c][k].y, g, 0.0f);
             }
     } else {
-        fwht_row<C>(x, q);
+        fwht_row<C, !MERGED>(x, q);
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
             for (int i = 0; i < 8; ++i) x[c][i] = x[c][i] * g;
     }
-    if constexpr (IS_KEY) {
+    if constexpr (MERGED) {
+        float dm[RC][8], dp[RC][8];
+        load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, t, q, dm, dp);
+        rope_stage_merged<C>(x, dm, dp);
+    } else if constexpr (IS_KEY) {
         float cs[RC][8], sn[RC][8];
         load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t, q, cs, sn);
         apply_rope<D, DR, RC, false>(x, q, cs, sn);
@@ -253,6 +262,10 @@ static int run_codec(const nq_codes_desc* d, int kind, void* stream) {
     NQ_CHECK_ARG(d->syms && d->cosets && d->scales && d->out, "nq codes: NULL pointer array");
     if (kind == 0 && d->is_key) {
         NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos >= d->seq, "nq_dequantize: RoPE table too short");
+        NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                     "nq_dequantize: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
+        NQ_CHECK_ARG(d->rope_cos_minus_sin == nullptr || d->head_dim != 96,
+                     "nq_dequantize: head_dim 96 keys take cos / sin tables only");
     }
     const uint64_t rows = (uint64_t)d->batch * d->heads * d->seq;
     NQ_CHECK_ARG(rows < (1ull << 31), "nq codes: too many rows");
@@ -263,6 +276,8 @@ static int run_codec(const nq_codes_desc* d, int kind, void* stream) {
     a.out = d->out;
     a.rope_cos = d->rope_cos;
     a.rope_sin = d->rope_sin;
+    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dp = d->rope_cos_plus_sin;
     a.heads = (uint32_t)d->heads;
     a.seq = (uint32_t)d->seq;
     a.n_tensors = (uint32_t)d->n_tensors;

@@ -29,6 +29,8 @@ struct QuantArgs {
     const uint8_t* keep;
     const float* rope_cos;
     const float* rope_sin;
+    const float* rope_dm;   // optional fl(cos - sin) / fl(cos + sin) tables
+    const float* rope_dp;
     uint32_t heads, seq_in, seq_out, rows;
     uint32_t n_tensors, bh, work, per_xcd;  // work items = ceil(seq_out/64) * bh * n_tensors
     float hscale;
@@ -335,13 +337,19 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
             for (int i = 0; i < 8; ++i) x[c][i] = 0.0f;
     }
 
-    float cs[RC][8], sn[RC][8];
-    if constexpr (IS_KEY) {
+    // Keys with DR == D: inverse RoPE and the top Hadamard stage in one step
+    // (their pairs coincide); the other stages follow in fwht_row.
+    constexpr bool MERGED = IS_KEY && DR == D;
+    float cs[RC][8], sn[RC][8];  // cos / sin, or fl(cos - sin) / fl(cos + sin) when MERGED
+    if constexpr (MERGED) {
+        load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, t_in, q, cs, sn);
+        rope_stage_merged<C>(x, cs, sn);
+    } else if constexpr (IS_KEY) {
         load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t_in, q, cs, sn);
         apply_rope<D, DR, RC, true>(x, q, cs, sn);
     }
 
-    fwht_row<C>(x, q);  // x = sigma(q) * S x
+    fwht_row<C, !MERGED>(x, q);  // x = sigma(q) * S x
     constexpr float HL = (float)(L / 2);
     const float sigma = quad_sign(q);
     float umax = 0.0f;
@@ -416,22 +424,24 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
         // Walsh-Hadamard of U in fp16 (exact: multiples of 1/(2L), |.| <= D).
         // S U = (S p)/L + (D/2) e_0, so every output but coordinate 0 (lane 0,
         // chunk 0, register 0 low half) is (S p)/L; that one is corrected by
-        // subtracting (L/2) D after the exact multiply by L.
+        // subtracting (L/2) D after the exact multiply by L.  Without the top
+        // stage (MERGED) the constant lands as (L/2)(D/2) on coordinates 0 and
+        // D/2 (lane 0, chunks 0 and C/2).
         half2v hp[C][4];
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
             for (int k = 0; k < 4; ++k) hp[c][k] = __builtin_bit_cast(half2v, u[c][k]);
-        fwht_row_f16<C>(hp, q);
+        fwht_row_f16<C, !MERGED>(hp, q);
         const float gl = g * (float)L;  // exact
-        const float dc = q == 0 ? HL * (float)D : 0.0f;
+        const float dc = q == 0 ? HL * (float)(MERGED ? D / 2 : D) : 0.0f;
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                if (c == 0 && k == 0) {
-                    const float t = __builtin_fmaf((float)hp[0][0].x, (float)L, -dc);  // exact
-                    x[0][0] = t * g;
+                if (k == 0 && (c == 0 || (MERGED && c == C / 2))) {
+                    const float t = __builtin_fmaf((float)hp[c][0].x, (float)L, -dc);  // exact
+                    x[c][0] = t * g;
                 } else {
                     x[c][k] = __builtin_fmaf((float)hp[c][k].x, gl, 0.0f);
                 }
@@ -461,7 +471,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                     hp[c][k] = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(x[c][2 * k], x[c][2 * k + 1]));
-            fwht_row_f16<C>(hp, q);
+            fwht_row_f16<C, !MERGED>(hp, q);
 #pragma unroll
             for (int c = 0; c < C; ++c)
 #pragma unroll
@@ -470,7 +480,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
                     x[c][2 * k + 1] = __builtin_fmaf((float)hp[c][k].y, g, 0.0f);
                 }
         } else {
-            fwht_row<C>(x, q);  // exact on half-integer lattice points
+            fwht_row<C, !MERGED>(x, q);  // exact on half-integer lattice points
 #pragma unroll
             for (int c = 0; c < C; ++c)
 #pragma unroll
@@ -478,7 +488,12 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
         }
     }
 
-    if constexpr (IS_KEY) {
+    if constexpr (MERGED) {
+        // the top inverse Hadamard stage and forward RoPE in one step
+        if (a.gather && t_out != t_in)
+            load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, t_out, q, cs, sn);
+        rope_stage_merged<C>(x, cs, sn);
+    } else if constexpr (IS_KEY) {
         if (a.gather && t_out != t_in) load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t_out, q, cs, sn);
         apply_rope<D, DR, RC, false>(x, q, cs, sn);
     }
@@ -567,6 +582,10 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     const uint64_t rows = (uint64_t)d->batch * d->heads * d->seq_out;
     NQ_CHECK_ARG(rows < (1ull << 31), "nq_quantize: %llu rows per tensor exceeds 2^31", (unsigned long long)rows);
     if (rows == 0) return NQ_OK;
+    NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                 "nq_quantize: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
+    NQ_CHECK_ARG(d->rope_cos_minus_sin == nullptr || d->head_dim != 96,
+                 "nq_quantize: head_dim 96 keys take cos / sin tables only");
     if (d->is_key) {
         NQ_CHECK_ARG(d->rope_cos && d->rope_sin, "nq_quantize: keys need RoPE tables");
         NQ_CHECK_ARG(d->rope_n_pos >= d->seq_in && d->rope_n_pos >= d->seq_out,
@@ -583,6 +602,8 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     a.keep = d->keep;
     a.rope_cos = d->rope_cos;
     a.rope_sin = d->rope_sin;
+    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dp = d->rope_cos_plus_sin;
     a.heads = (uint32_t)d->heads;
     a.seq_in = (uint32_t)d->seq_in;
     a.seq_out = (uint32_t)d->seq_out;

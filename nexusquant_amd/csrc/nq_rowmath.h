@@ -68,11 +68,13 @@ typedef __fp16 half2v __attribute__((ext_vector_type(2)));
         : "v"(c))
 
 // Unnormalised Walsh-Hadamard over the quad's row.  Stage order follows
-// coordinate bits 0,1,2 (in chunk), 3,4 (across the quad), 5.. (across chunks).
+// coordinate bits 0,1,2 (in chunk), 3,4 (across the quad), 5.. (across chunks);
+// TOP = false leaves out the stage on the top bit (pairs i, i + D/2), which
+// the merged RoPE step below performs.
 // The quad stages compute v + c * partner with c = +-1 per lane, the exact
 // butterfly up to a sign; every lane's values end multiplied by
 // sigma(q) = (-1)^popcount(q), which the caller folds into the next multiply.
-template <int C>
+template <int C, bool TOP = true>
 __device__ __forceinline__ void fwht_row(float (&x)[C][8], int q) {
 #pragma unroll
     for (int c = 0; c < C; ++c) {
@@ -94,7 +96,7 @@ __device__ __forceinline__ void fwht_row(float (&x)[C][8], int q) {
 #pragma unroll
     for (int c = 0; c < C; ++c) NQ_FMAC_DPP8("quad_perm:[2,3,0,1]", x[c], s4);
 #pragma unroll
-    for (int len = 1; len < C; len <<= 1) {
+    for (int len = 1; len < (TOP ? C : C / 2); len <<= 1) {
 #pragma unroll
         for (int c = 0; c < C; ++c) {
             if (c & len) continue;
@@ -113,7 +115,7 @@ __device__ __forceinline__ void fwht_row(float (&x)[C][8], int q) {
 // multiple of 1/2 of magnitude <= D*L/2 <= 1024, so fp16 holds it exactly and
 // the result equals the fp32 transform in any stage order.  Output carries the
 // same sigma(q) sign.
-template <int C>
+template <int C, bool TOP = true>
 __device__ __forceinline__ void fwht_row_f16(half2v (&h)[C][4], int q) {
     const half2v pm = {(__fp16)1.0f, (__fp16)-1.0f};
 #pragma unroll
@@ -149,7 +151,7 @@ __device__ __forceinline__ void fwht_row_f16(half2v (&h)[C][4], int q) {
             h[c][k] = __builtin_elementwise_fma(s4, p, h[c][k]);
         }
 #pragma unroll
-    for (int len = 1; len < C; len <<= 1) {
+    for (int len = 1; len < (TOP ? C : C / 2); len <<= 1) {
 #pragma unroll
         for (int c = 0; c < C; ++c) {
             if (c & len) continue;
@@ -248,6 +250,56 @@ __device__ __forceinline__ void apply_rope(float (&x)[D / 32][8], int q, const f
                                     : __builtin_fmaf(p, sn[c][i], v * cs[c][i]);
                 }
             }
+        }
+    }
+}
+
+// --------------------------------------------------- merged RoPE + top stage ----
+//
+// With DR == D the RoPE pair (i, i + D/2) is also the pair of the top
+// Walsh-Hadamard stage, and rotation followed by that butterfly is
+//   (lo, hi) -> (lo (c - s) + hi (c + s), lo (c + s) - hi (c - s))
+// on the input side (inverse RoPE, then the stage), and the same map on the
+// output side (the inverse stage, then forward RoPE).  With dm = fl(c - s)
+// and dp = fl(c + s):  lo' = fma(lo, dm, fl(hi dp)), hi' = fma(lo, dp, -fl(hi dm)).
+
+template <int D>
+__device__ __forceinline__ void load_rope_merged(const float* cos_t, const float* sin_t, const float* dm_t,
+                                                 const float* dp_t, uint32_t pos, int q, float (&dm)[D / 64][8],
+                                                 float (&dp)[D / 64][8]) {
+    constexpr int RC = D / 64;
+    const size_t base = (size_t)pos * (D / 2);
+    if (dm_t) {
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+            load8f(dm_t + base + 32 * c + 8 * q, dm[c]);
+            load8f(dp_t + base + 32 * c + 8 * q, dp[c]);
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+            float cs[8], sn[8];
+            load8f(cos_t + base + 32 * c + 8 * q, cs);
+            load8f(sin_t + base + 32 * c + 8 * q, sn);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                dm[c][i] = cs[i] - sn[i];
+                dp[c][i] = cs[i] + sn[i];
+            }
+        }
+    }
+}
+
+template <int C>
+__device__ __forceinline__ void rope_stage_merged(float (&x)[C][8], const float (&dm)[C / 2][8],
+                                                  const float (&dp)[C / 2][8]) {
+#pragma unroll
+    for (int c = 0; c < C / 2; ++c) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float lo = x[c][i], hi = x[c + C / 2][i];
+            x[c][i] = __builtin_fmaf(lo, dm[c][i], hi * dp[c][i]);
+            x[c + C / 2][i] = __builtin_fmaf(lo, dp[c][i], -(hi * dm[c][i]));
         }
     }
 }

@@ -11,7 +11,7 @@ import torch
 
 from . import _lib
 from .hadamard import hadamard_constant, next_power_of_2
-from .rope import device_table
+from .rope import device_merged_table, device_table
 
 SYM_BITS = {2: 2, 4: 3, 8: 4, 16: 5}
 
@@ -159,7 +159,7 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
                      rope_base: float = 10000.0, rope_scaling: Optional[dict] = None,
                      gather: Optional[torch.Tensor] = None, keep: Optional[torch.Tensor] = None,
                      keep_mode: int = _lib.NQ_KEEP_ZERO, recon_out: Optional[Sequence[torch.Tensor]] = None,
-                     recon: bool = True, codes: bool = False, launch_events=None,
+                     recon: bool = True, codes: bool = False, launch_events=None, merged_tables: bool = True,
                      ) -> Tuple[Optional[List[torch.Tensor]], Optional[List[PackedCodes]]]:
     """Run the fused quantizer over same-shaped [b, h, s, d] tensors in one launch.
 
@@ -171,6 +171,8 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
             (rows this launch does not write keep their contents).
     launch_events: optional (start, end) torch.cuda.Event pair recorded on the
     launch stream immediately around the kernel launch.
+    merged_tables: pass the precomputed fl(cos - sin) / fl(cos + sin) tables for
+            keys (False: the kernel forms them from cos / sin; same results).
     Returns (fp16 reconstructions or None, PackedCodes or None), one per tensor.
     """
     lib = _lib.load()
@@ -236,11 +238,13 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
         codes_t = [PackedCodes(syms=syms[i], cosets=cosets[i], scales=scales[i], levels=levels, head_dim=d,
                                padded_dim=D, is_key=is_key) for i in range(n)]
 
-    cos = sin = None
+    cos = sin = dm = dp = None
     n_pos = 0
     if is_key:
         cos, sin = device_table(max(s, seq_out), d, rope_base, rope_scaling, dev)
         n_pos = cos.shape[0]
+        if d != 96 and merged_tables:  # power-of-two head dims fold RoPE into the top Hadamard stage
+            dm, dp = device_merged_table(n_pos, d, rope_base, rope_scaling, dev)
 
     names = ("src", "recon", "syms", "cosets", "scales")
     groups = [src, recon_t,
@@ -255,7 +259,8 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
         src=_addr(arrays["src"]), recon=_addr(arrays["recon"]), syms=_addr(arrays["syms"]),
         cosets=_addr(arrays["cosets"]), scales=_addr(arrays["scales"]),
         gather=_addr(g), keep=_addr(k), rope_cos=_addr(cos), rope_sin=_addr(sin),
-        rope_n_pos=n_pos, hadamard_scale=hadamard_constant(D))
+        rope_n_pos=n_pos, hadamard_scale=hadamard_constant(D),
+        rope_cos_minus_sin=_addr(dm), rope_cos_plus_sin=_addr(dp))
     with torch.cuda.device(dev):
         try:
             if launch_events is not None:

@@ -81,6 +81,24 @@ def device_table(n_pos: int, head_dim: int, base: float, rope_scaling: Optional[
         return tab
 
 
+def device_merged_table(n_pos: int, head_dim: int, base: float, rope_scaling: Optional[dict],
+                        device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Cached device fl(cos - sin), fl(cos + sin) [>= n_pos, head_dim/2] (fp32, built on the
+    host from host_table).  The fused kernels fold RoPE into the top Hadamard stage
+    with these; they are the same numbers the kernels would form from cos and sin."""
+    device = torch.device(device)
+    key = ("merged", head_dim, float(base), json.dumps(rope_scaling, sort_keys=True, default=str), device)
+    with _lock:
+        hit = _cache.get(key)
+        if hit is not None and hit[0].shape[0] >= n_pos:
+            return hit
+        n = max(_ROUND, -(-n_pos // _ROUND) * _ROUND)
+        c, s = host_table(n, head_dim, base, rope_scaling)
+        tab = ((c - s).to(device), (c + s).to(device))
+        _cache[key] = tab
+        return tab
+
+
 def clear_cache() -> None:
     with _lock:
         _cache.clear()

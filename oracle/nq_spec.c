@@ -9,14 +9,20 @@
  *  rope_utils.py:75-249, hadamard.py:23-43) and fixes every rounding step so
  * that the HIP kernel can be compared with it bit for bit:
  *
- *  1. Inverse RoPE with one fused multiply-add per coordinate:
- *     lo' = fma(lo, c, fl(hi*s)) ; hi' = fma(hi, c, -fl(lo*s)).  The reference
- *     rounds both products (rope_utils.py:75-112); the difference is one ulp of
- *     the rotated value, far below what moves a code except at a near tie.
+ *  1. Inverse RoPE with one fused multiply-add per coordinate.  For d = D
+ *     (power-of-two head dims) the RoPE pair (i, i + D/2) is also the pair of
+ *     the top Hadamard stage, and the two are done as one step with dm =
+ *     fl(c - s), dp = fl(c + s):  lo' = fma(lo, dm, fl(hi*dp)),
+ *     hi' = fma(lo, dp, -fl(hi*dm)), after which stage 3 leaves out that top
+ *     stage.  For d = 96 (padded): lo' = fma(lo, c, fl(hi*s)),
+ *     hi' = fma(hi, c, -fl(lo*s)).  The reference rounds every product and sum
+ *     separately (rope_utils.py:75-112, dense GEMM); the differences are a few
+ *     ulp of the rotated value, below what moves a code except at a near tie.
  *  2. Zero-pad to D = next power of two (the reference raises for d = 96,
  *     hadamard.py:35-36; padding is this build's definition).
  *  3. Unnormalised Walsh-Hadamard butterflies u = S x, stages on index bit
- *     0,1,..., log2(D)-1 in that order, each (a, b) -> (a + b, a - b) in fp32.
+ *     0,1,..., log2(D)-1 in that order (the top one already done for d = D
+ *     keys), each (a, b) -> (a + b, a - b) in fp32.
  *     The reference uses a dense fp32 GEMM with the normalised matrix h_D * S
  *     here, so the two differ in the last ulp; the resulting code disagreement
  *     is measured in tests (about 1e-6 of groups).
@@ -40,10 +46,13 @@
  *     distances are within about 1e-6 of each other (a near tie).
  *  6. Clamp to [-L/2, L/2] after the choice (e8_lattice.py:120).
  *  7. Reconstruction: w = S * p is exact in fp32 for every order (p is a
- *     half-integer of magnitude <= 8), then recon = w * fl(h_D * scale),
- *     forward RoPE lo' = fma(lo, c, -fl(hi*s)), hi' = fma(lo, s, fl(hi*c)) (the
- *     reference rounds lo*c separately; the difference is below fp16
- *     resolution except at fp16 rounding ties), keep the first d outputs,
+ *     half-integer of magnitude <= 8), then recon = w * fl(h_D * scale).  Keys
+ *     with d = D stop w before the top stage and finish with the merged step
+ *     of 1. on the output-position tables (the top inverse stage followed by
+ *     forward RoPE is the same map); d = 96 keys apply forward RoPE
+ *     lo' = fma(lo, c, -fl(hi*s)), hi' = fma(lo, s, fl(hi*c)).  The reference
+ *     rounds every product separately; the difference is below fp16
+ *     resolution except at fp16 rounding ties.  Keep the first d outputs,
  *     round to fp16 (round to nearest even).
  *
  * Code symbols: the group's coset bit is 1 when the half-integer candidate was
@@ -187,8 +196,9 @@ static float next_up(float f) { /* f > 0, finite */
     return f;
 }
 
-static void fwht_inplace(float* v, int D) {
-    for (int len = 1; len < D; len <<= 1) {
+/* butterfly stages on index bits 0, 1, ... up to (not including) the bit of `top` */
+static void fwht_stages(float* v, int D, int top) {
+    for (int len = 1; len < top; len <<= 1) {
         for (int i = 0; i < D; ++i) {
             if (i & len) continue;
             float a = v[i], b = v[i + len];
@@ -228,7 +238,17 @@ void nqs_quant_rows(int64_t n, int d, int D, int L, float hD,
         float v[NQS_MAXD], xn[NQS_MAXD], p[NQS_MAXD];
         const float* xr = x + row * d;
         for (int i = 0; i < D; ++i) v[i] = 0.0f;
-        if (cos_in) {
+        const int merged = cos_in && d == D;  /* RoPE pairs are the top Hadamard pairs */
+        if (merged) {
+            const float* c = cos_in + row * half;
+            const float* s = sin_in + row * half;
+            for (int i = 0; i < half; ++i) {
+                float lo = xr[i], hi = xr[i + half];
+                float dm = c[i] - s[i], dp = c[i] + s[i];
+                v[i] = fmaf(lo, dm, hi * dp);
+                v[i + half] = fmaf(lo, dp, -(hi * dm));
+            }
+        } else if (cos_in) {
             const float* c = cos_in + row * half;
             const float* s = sin_in + row * half;
             for (int i = 0; i < half; ++i) {
@@ -239,7 +259,7 @@ void nqs_quant_rows(int64_t n, int d, int D, int L, float hD,
         } else {
             for (int i = 0; i < d; ++i) v[i] = xr[i];
         }
-        fwht_inplace(v, D);
+        fwht_stages(v, D, merged ? D / 2 : D);
         float umax = 0.0f;
         for (int i = 0; i < D; ++i) {
             float av = fabsf(v[i]);
@@ -289,11 +309,21 @@ void nqs_quant_rows(int64_t n, int d, int D, int L, float hD,
         if (recon_out) {
             float w[NQS_MAXD];
             memcpy(w, p, sizeof(float) * D);
-            fwht_inplace(w, D);
+            fwht_stages(w, D, merged ? D / 2 : D);  /* exact on half-integer points */
             float g = hD * scale;
             for (int i = 0; i < D; ++i) w[i] = w[i] * g;
             uint16_t* out = recon_out + row * d;
-            if (cos_out) {
+            if (merged) {
+                /* top inverse stage and forward RoPE in one step (same map as the input side) */
+                const float* c = cos_out + row * half;
+                const float* s = sin_out + row * half;
+                for (int i = 0; i < half; ++i) {
+                    float lo = w[i], hi = w[i + half];
+                    float dm = c[i] - s[i], dp = c[i] + s[i];
+                    out[i] = nqs_f32_to_f16(fmaf(lo, dm, hi * dp));
+                    out[i + half] = nqs_f32_to_f16(fmaf(lo, dp, -(hi * dm)));
+                }
+            } else if (cos_out) {
                 const float* c = cos_out + row * half;
                 const float* s = sin_out + row * half;
                 for (int i = 0; i < half; ++i) {

@@ -77,6 +77,20 @@ def _subsample_rows(x_np, heads, toks):
     return x_np[0][heads, toks]
 
 
+@pytest.mark.parametrize("D,L", [(128, 8), (64, 4), (256, 2), (128, 16)])
+def test_merged_rope_tables_match_in_kernel_tables(D, L):
+    # precomputed fl(cos - sin) / fl(cos + sin) tables and the ones the kernel
+    # forms from cos / sin give identical outputs
+    print(f"[gpu] merged tables D={D} L={L}", flush=True)
+    x = _inputs((1, 2, 130, D), torch.bfloat16, seed=D + L).to(DEV)
+    ops = _ops()
+    r1, c1 = ops.quantize_tensors([x], is_key=True, levels=L, rope_base=5e5, codes=True)
+    r2, c2 = ops.quantize_tensors([x], is_key=True, levels=L, rope_base=5e5, codes=True, merged_tables=False)
+    torch.cuda.synchronize()
+    assert torch.equal(r1[0], r2[0])
+    assert torch.equal(c1[0].syms, c2[0].syms) and torch.equal(c1[0].scales, c2[0].scales)
+
+
 def test_quantizer_far_positions_and_llama3_scaling():
     print("[gpu] far positions", flush=True)
     sc = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
