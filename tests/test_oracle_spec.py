@@ -111,8 +111,10 @@ def test_quantizer_invariants():
 
 
 def test_normalisation_within_two_ulp_of_reference_division():
-    # The spec multiplies by f = fl(h_D * fl(1/scale)) where the reference
-    # multiplies by h_D and divides by the row scale (e8_lattice.py:114-116).
+    # The spec multiplies the unnormalised transform by one factor f (the
+    # smallest float with fl(max|u| * f) >= L/2), then clamps, where the
+    # reference multiplies by h_D and divides by the row scale
+    # (e8_lattice.py:114-116).
     # Compare the normalised coordinates with the reference formula computed
     # from the same unnormalised transform: a dropped or doubled h_D, a wrong
     # level count or a scale taken before the clamp fails by orders of magnitude.
