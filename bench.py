@@ -193,9 +193,81 @@ def aux_workload(name, steps, warmup):
         out.update(config={"workload": f"{desc}, K2V2, {int(rate * 100)}% key-key eviction"},
                    ms_per_step=round(step_ms, 3), value=round(step_ms, 3),
                    gbs_fp16_compressed=round(2 * elems / (step_ms * 1e-3) / 1e9, 1))
+    elif name in ("decode70b", "decode7b"):
+        out.update(decode_workload(name, steps, warmup))
     else:
         raise SystemExit(f"unknown workload {name}")
     print(json.dumps(out), flush=True)
+
+
+def decode_workload(name, steps, warmup):
+    """Decode attention straight from compressed vLLM pages (nq_paged_attention).
+
+    decode70b: Llama-3-70B shape, one decode token, batch 1, 64 query heads over
+    8 kv heads (GQA 8), head_dim 128, 131072-token context in 16-token pages,
+    bits 2 (the compressor's default); 8 distinct layers' page pools are visited
+    in turn so no layer's pages sit in the 256 MB last-level cache.
+    decode7b: Llama-2-7B shape (MHA, the reference's own layout): batch 8,
+    32 heads, 8192-token contexts.
+    Reported per layer call; bytes are the pages' codes, scales and positions."""
+    import torch
+    from nexusquant_amd.vllm_backend import NexusQuantKVCompressor, NexusQuantPagedAttention
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(11)
+    if name == "decode70b":
+        batch, hq, hkv, ctx, pools = 1, 64, 8, 131072, 8
+    else:
+        batch, hq, hkv, ctx, pools = 8, 32, 32, 8192, 4
+    d, block, bits = 128, 16, 2
+    comp = NexusQuantKVCompressor(head_dim=d, bits=bits, rope_base=500000.0)
+    attn = NexusQuantPagedAttention(comp)
+    n_pages = batch * ctx // block
+    plans = []
+    for layer in range(pools):
+        cache = {}
+        for start in range(0, n_pages, 8192):
+            m = min(8192, n_pages - start)
+            k = torch.randn(m, hkv, block, d, device=dev, generator=gen).half()
+            v = (torch.randn(m, hkv, block, d, device=dev, generator=gen) * 0.5).half()
+            pos = [torch.arange(block, dtype=torch.int32) + block * ((start + i) % (ctx // block))
+                   for i in range(m)]
+            pages = comp.compress_pages([(k[i], v[i], pos[i]) for i in range(m)])
+            for i, pg in enumerate(pages):
+                cache[start + i] = pg
+            del k, v
+        per_row = ctx // block
+        tables = [list(range(r * per_row, (r + 1) * per_row)) for r in range(batch)]
+        plans.append(attn.plan(cache, tables, [ctx] * batch))
+    q = torch.randn(batch, hq, d, device=dev, generator=gen).half()
+    outs = [torch.empty_like(q) for _ in plans]
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in plans]
+
+    def step(events=False):
+        for i, pl in enumerate(plans):
+            if events:
+                evs[i][0].record(stream)
+            attn.run(pl, q, out=outs[i], workspace=ws)
+            if events:
+                evs[i][1].record(stream)
+
+    ms = _timed(torch, step, steps, warmup) * 1e3 / len(plans)
+    step(events=True)
+    torch.cuda.synchronize()
+    ev_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    tokens = batch * ctx
+    page_bytes = tokens * hkv * (2 * d + 2 * 2) + tokens * 4
+    fp16_bytes = tokens * hkv * d * 2 * 2
+    gbs = page_bytes / (ev_ms * 1e-3) / 1e9
+    shape = (f"batch {batch}, {hq} query heads over {hkv} kv heads, head_dim {d}, {ctx}-token context in "
+             f"{block}-token pages, bits {bits}")
+    return dict(config={"workload": f"paged decode attention from compressed pages: {shape}"},
+                ms_per_step=round(ms, 4), value=round(ms, 4), ms_per_layer_events=round(ev_ms, 4),
+                page_bytes_per_layer=page_bytes, fp16_kv_bytes_per_layer=fp16_bytes,
+                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                fp16_equivalent_gbs=round(fp16_bytes / (ev_ms * 1e-3) / 1e9, 1))
 
 
 def main():
@@ -206,6 +278,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="c2",
                     help="c2 (headline, default), a secondary config: c3, c4, c5a, c5b, aux (all four), "
+                         "decode70b / decode7b (paged decode attention from compressed pages), "
                          "or copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.workload != "c2":

@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define NQ_ABI_VERSION 2
+#define NQ_ABI_VERSION 3
 
 /* status codes */
 #define NQ_OK 0
@@ -216,6 +216,138 @@ int nq_codes_to_int8(const nq_codes_desc* desc, int32_t delta, void* stream);
  */
 int nq_delta_decode(const uint64_t* deltas, const uint64_t* out, int32_t n_tensors, int32_t streams, int32_t seq,
                     int32_t coords, void* stream);
+
+/*
+ * Pages of the vLLM compressor: n_pages pages of identical geometry
+ * [heads, tokens, head_dim] (head_dim 64, 128 or 256), keys or values, at
+ * `levels` 4, 8 or 16 (bits 2, 3, 4).  The format is the reference's
+ * CompressedPage: codes int8 [heads, tokens, head_dim] holding 2p for the
+ * clamped relaxed-E8 point p of the Hadamard-rotated row, scales fp16
+ * [heads, tokens] (the row scale amax / (levels/2) rounded to fp16), and
+ * int32 absolute positions [tokens] at which keys carry RoPE.  Arrays are
+ * device arrays of n_pages base addresses (uint64).
+ */
+typedef struct nq_page_desc {
+    int32_t n_pages;
+    int32_t heads, tokens, head_dim;
+    int32_t dtype;           /* nq_page_encode input: NQ_F16 / NQ_BF16 / NQ_F32 */
+    int32_t levels;
+    int32_t is_key;
+    int32_t reserved;
+    const uint64_t* src;       /* encode: K or V pages */
+    const uint64_t* positions; /* int32 [tokens] per page (keys) */
+    const uint64_t* codes;     /* int8 [heads, tokens, head_dim] per page */
+    const uint64_t* scales;    /* fp16 [heads, tokens] per page */
+    const uint64_t* out;       /* decode: fp16 [heads, tokens, head_dim] per page */
+    const float* rope_cos;     /* fp32 [rope_n_pos, head_dim/2], keys */
+    const float* rope_sin;
+    const float* rope_cos_minus_sin;  /* optional fl(cos - sin) / fl(cos + sin) */
+    const float* rope_cos_plus_sin;
+    int64_t rope_n_pos;        /* positions must lie in [0, rope_n_pos) */
+    float hadamard_scale;
+    float reserved_f;
+} nq_page_desc;
+
+/*
+ * Encode pages: inverse RoPE at each token's absolute position (keys),
+ * Walsh-Hadamard, per-row scale, relaxed E8 at `levels`, clamp; writes codes
+ * and scales.  Row arithmetic is nq_quantize's.
+ *
+ * Replaces: NexusQuantKVCompressor.compress_page        vllm_backend.py:344-392
+ *           _rope_remove_page / _quantize_perhead_with_scales  :187-224, 267-314
+ */
+int nq_page_encode(const nq_page_desc* desc, void* stream);
+
+/*
+ * Decode pages to fp16 [heads, tokens, head_dim]: x = (code / 2) * scale,
+ * inverse Walsh-Hadamard (exact on the integer codes), forward RoPE at the
+ * stored positions (keys), rounding to fp16.
+ *
+ * Replaces: NexusQuantKVCompressor.decompress_page      vllm_backend.py:394-429
+ *           _rope_apply_page / _dequantize_perhead       :226-265, 316-338
+ */
+int nq_page_decode(const nq_page_desc* desc, void* stream);
+
+/*
+ * Logits of queries against one page (n_pages == 1): query [heads, q_len,
+ * head_dim] of type q_dtype, logits fp32 [heads, q_len, tokens] =
+ * (q . k) / scale_divisor with k the page's decoded keys in fp32 (before the
+ * fp16 rounding of nq_page_decode).
+ *
+ * Replaces: NexusQuantKVCompressor.decompress_for_attention  vllm_backend.py:431-467
+ */
+int nq_page_logits(const nq_page_desc* desc, const void* query, int32_t q_dtype, int32_t q_len,
+                   float scale_divisor, float* logits, void* stream);
+
+/*
+ * Nibble packing of int8 codes [rows, d]: out[r, j] = n(2j) | n(2j+1) << 4 with
+ * n(k) = clamp(code[r, k] + 8, 0, 15) and n(d) = 0 for odd d; packed is
+ * [rows, (d + 1) / 2] bytes.  Unpacking reads [rows, packed_cols] bytes and
+ * writes the first d <= 2 * packed_cols nibbles of each row minus 8.
+ *
+ * Replaces: pack_codes_nibble / unpack_codes_nibble   vllm_backend.py:475-536
+ */
+int nq_nibble_pack(const int8_t* codes, int64_t rows, int32_t d, uint8_t* packed, void* stream);
+int nq_nibble_unpack(const uint8_t* packed, int64_t rows, int32_t packed_cols, int32_t d, int8_t* codes,
+                     void* stream);
+
+/*
+ * Decode attention read straight from compressed pages: for each batch row
+ * and query head, softmax(q . k / scale_divisor) . v over the row's tokens,
+ * where k and v are the pages' decoded keys (bit for bit nq_page_decode's
+ * fp16 keys) and values, query head h reading kv head h / (q_heads /
+ * kv_heads).  Output [batch, q_heads, head_dim] has the query's type and
+ * holds the fp16-rounded result; rows with no tokens are zero.
+ *
+ * The caller describes where the tokens are with a chunk plan (device int32
+ * arrays; nexusquant_amd/vllm_backend.py builds it):
+ *   units        [n_units * 16] unit records, each up to 16 consecutive tokens
+ *                of one page (nq_page_desc layout, heads = kv_heads), addressed
+ *                at kv head 0 and the unit's first token t0:
+ *                  [0..1]  key codes + t0 * head_dim        (uint64 address)
+ *                  [2..3]  value codes + t0 * head_dim
+ *                  [4..5]  key scales + t0                 (fp16 elements)
+ *                  [6..7]  value scales + t0
+ *                  [8..9]  positions + t0                  (int32 elements)
+ *                  [10]    tokens the page stores per head (its row stride)
+ *                  [11]    tokens in the unit (1..16)
+ *                  [12]    offset of the unit's first token in its chunk
+ *                  [13..15] unused;
+ *   chunk_units  [n_chunks + 1] units of each chunk (consecutive);
+ *   chunk_row    [n_chunks] batch row of each chunk;
+ *   chunk_tokens [n_chunks] tokens of each chunk, at most
+ *                nq_paged_attention_chunk_tokens();
+ *   row_chunks   [batch + 1] chunks of each row (consecutive, ascending).
+ * workspace: nq_paged_attention_workspace(n_chunks, q_heads, head_dim) bytes.
+ * q_heads / kv_heads may be 1, 2, 4, or 8 (8 with fp16 queries).
+ *
+ * Replaces: NexusQuantPagedAttention.forward   vllm_backend.py:692-765
+ */
+typedef struct nq_attn_desc {
+    int32_t batch, q_heads, kv_heads, head_dim;
+    int32_t q_dtype;             /* NQ_F16 / NQ_BF16 / NQ_F32 */
+    int32_t n_chunks;
+    const void* query;           /* [batch, q_heads, head_dim] */
+    void* out;                   /* [batch, q_heads, head_dim], q_dtype */
+    const int32_t* units;
+    const int32_t* chunk_units;
+    const int32_t* chunk_row;
+    const int32_t* chunk_tokens;
+    const int32_t* row_chunks;
+    const float* rope_cos;
+    const float* rope_sin;
+    const float* rope_cos_minus_sin;  /* optional, as in nq_page_desc */
+    const float* rope_cos_plus_sin;
+    int64_t rope_n_pos;
+    float hadamard_scale;
+    float scale_divisor;         /* logits = q . k / scale_divisor (fp32 sqrt(head_dim)) */
+    void* workspace;
+    int64_t workspace_bytes;
+} nq_attn_desc;
+
+int32_t nq_paged_attention_chunk_tokens(void);
+int64_t nq_paged_attention_workspace(int32_t n_chunks, int32_t q_heads, int32_t head_dim);
+int nq_paged_attention(const nq_attn_desc* desc, void* stream);
 
 /* Library version and the last error message of the calling thread. */
 int nq_abi_version(void);

@@ -14,7 +14,7 @@ from .build import LIB_PATH
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
 NQ_KEEP_ZERO, NQ_KEEP_WRITE_KEPT, NQ_KEEP_WRITE_EVICTED = 0, 1, 2
-ABI_VERSION = 2  # NQ_ABI_VERSION of the header these bindings mirror
+ABI_VERSION = 3  # NQ_ABI_VERSION of the header these bindings mirror
 _P = ctypes.c_void_p
 
 
@@ -48,6 +48,34 @@ class CodesDesc(ctypes.Structure):
     ]
 
 
+class PageDesc(ctypes.Structure):
+    """Mirror of nq_page_desc in include/nexusquant_amd.h."""
+    _fields_ = [
+        ("n_pages", ctypes.c_int32),
+        ("heads", ctypes.c_int32), ("tokens", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32), ("levels", ctypes.c_int32), ("is_key", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("src", _P), ("positions", _P), ("codes", _P), ("scales", _P), ("out", _P),
+        ("rope_cos", _P), ("rope_sin", _P), ("rope_cos_minus_sin", _P), ("rope_cos_plus_sin", _P),
+        ("rope_n_pos", ctypes.c_int64),
+        ("hadamard_scale", ctypes.c_float), ("reserved_f", ctypes.c_float),
+    ]
+
+
+class AttnDesc(ctypes.Structure):
+    """Mirror of nq_attn_desc in include/nexusquant_amd.h."""
+    _fields_ = [
+        ("batch", ctypes.c_int32), ("q_heads", ctypes.c_int32), ("kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("q_dtype", ctypes.c_int32), ("n_chunks", ctypes.c_int32),
+        ("query", _P), ("out", _P), ("units", _P),
+        ("chunk_units", _P), ("chunk_row", _P), ("chunk_tokens", _P), ("row_chunks", _P),
+        ("rope_cos", _P), ("rope_sin", _P), ("rope_cos_minus_sin", _P), ("rope_cos_plus_sin", _P),
+        ("rope_n_pos", ctypes.c_int64),
+        ("hadamard_scale", ctypes.c_float), ("scale_divisor", ctypes.c_float),
+        ("workspace", _P), ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
 # Every exported symbol, with (argtypes, restype).  tests/test_abi.py checks
 # that this list and include/nexusquant_amd.h agree and that the library
 # exports all of them.
@@ -66,6 +94,14 @@ SIGNATURES = {
     "nq_delta_decode": ([_P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "nq_score_real_workspace": ([_I32, _I32, _I32], _I64),
     "nq_score_real": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
+    "nq_page_encode": ([ctypes.POINTER(PageDesc), _P], ctypes.c_int),
+    "nq_page_decode": ([ctypes.POINTER(PageDesc), _P], ctypes.c_int),
+    "nq_page_logits": ([ctypes.POINTER(PageDesc), _P, _I32, _I32, _F32, _P, _P], ctypes.c_int),
+    "nq_paged_attention_chunk_tokens": ([], ctypes.c_int32),
+    "nq_paged_attention_workspace": ([_I32, _I32, _I32], _I64),
+    "nq_paged_attention": ([ctypes.POINTER(AttnDesc), _P], ctypes.c_int),
+    "nq_nibble_pack": ([_P, _I64, _I32, _P, _P], ctypes.c_int),
+    "nq_nibble_unpack": ([_P, _I64, _I32, _I32, _P, _P], ctypes.c_int),
 }
 
 _lock = threading.Lock()

@@ -39,16 +39,30 @@ def sources():
     return sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")))
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *sources()]
+def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed with status {res.returncode}")
+        raise RuntimeError(f"hipcc failed with status {res.returncode}: {' '.join(cmd[-3:])}")
+
+
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compile every csrc/*.hip to an object in parallel (outside the tree), then link."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    inc = ["-I", os.path.join(ROOT, "include")]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = jobs or min(len(sources()), os.cpu_count() or 1, 16)
+    with tempfile.TemporaryDirectory(prefix="nqamd_build_") as objdir:
+        objs = [os.path.join(objdir, os.path.basename(src) + ".o") for src in sources()]
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            list(pool.map(lambda so: _run([hipcc(), *compile_flags, *inc, "-c", so[0], "-o", so[1]], verbose),
+                          zip(sources(), objs)))
+        _run([hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -1,0 +1,535 @@
+// Decode attention straight from compressed pages (the vLLM compressor's
+// int8 2p codes, fp16 row scales and int32 positions) on gfx950.
+//
+// The host cuts every sequence's pages into chunks of at most kChunk tokens;
+// one workgroup of 4 waves takes one (chunk, kv head) and all G query heads
+// that read that kv head, and writes a partial softmax state per query head:
+// the chunk's running max m, its sum of exp l and the unnormalised value sum
+// y.  A combine kernel merges the chunks of a row.
+//
+//  1. Keys, a quad of lanes per token (the page decoder's layout): exact
+//     fp16 Walsh-Hadamard of the integer codes without the top stage, one
+//     scale multiply, the merged top stage + forward RoPE at the stored
+//     position, rounding to fp16 -- bit for bit the keys the page decoder
+//     writes -- then q . k with v_dot2_f32_f16 (fp16 queries) or fp32 FMAs,
+//     divided by fl(sqrt(head_dim)).  Logits go to LDS.
+//  2. Per query head the chunk max x_m of the unscaled logits and
+//     e = exp((x - x_m) / scale_divisor), l = sum e (fixed order); LDS keeps
+//     e * scale_v / 2 per token.
+//  3. Values are never reconstructed per token: the inverse Hadamard is
+//     linear, so sum_t e_t v_t = h_D * S (sum_t e_t (scale_t / 2) c_t) with
+//     c_t the integer codes.  Lanes own D/64 consecutive coordinates and
+//     accumulate e_t (scale_t / 2) c_t over the chunk; the block applies S to
+//     its sum once, and the combine kernel weights the chunks, applies h_D and
+//     divides by the softmax sum.
+//
+// Work items are (chunk, kv head) with the kv head fastest, and block 8k + x
+// takes item x * per_xcd + k: the kv heads of one chunk run on one XCD and
+// share the chunk's RoPE table rows in its L2.
+//
+// Against the reference (which rounds every decoded value to fp16 before the
+// weighted sum, vllm_backend.py:748-763) the result differs by that rounding
+// (below 2^-11 of a value, averaged by the weights) and by summation order.
+#include "nq_rowmath.h"
+
+namespace nq {
+
+constexpr int kChunk = 512;  // tokens per chunk (logits held in LDS)
+
+struct AttnArgs {
+    const void* query;
+    void* out;
+    const int32_t* units;        // [unit * 16]: the unit records (see nq_attn_desc)
+    const int32_t* chunk_units;  // [chunk + 1]
+    const int32_t* chunk_row;
+    const int32_t* chunk_tokens;
+    const int32_t* row_chunks;   // [row + 1]
+    float* part;                 // [chunk * q_heads * (D + 2)]: m, l, S y[D]
+    const float* rope_cos;
+    const float* rope_sin;
+    const float* rope_dm;
+    const float* rope_dp;
+    uint32_t q_heads, kv_heads, rope_n_pos;
+    uint32_t work, per_xcd;      // n_chunks * kv_heads items, ceil(work / 8)
+    float inv_scale;             // 1 / scale_divisor
+    float hscale;
+};
+
+// One unit record: up to 16 consecutive tokens of one page, addressed for kv
+// head 0 (head kh adds kh * stride rows).
+struct UnitRec {
+    const int8_t* kc;
+    const int8_t* vc;
+    const uint16_t* ks;
+    const uint16_t* vs;
+    const int32_t* pos;
+    int32_t stride, n, coff;
+};
+
+__device__ __forceinline__ UnitRec unit_rec(const AttnArgs& a, int u) {
+    const int4* r = reinterpret_cast<const int4*>(a.units + 16 * u);
+    const int4 r0 = r[0], r1 = r[1], r2 = r[2];
+    auto ptr = [](int lo, int hi) { return (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32); };
+    UnitRec x;
+    x.kc = reinterpret_cast<const int8_t*>(ptr(r0.x, r0.y));
+    x.vc = reinterpret_cast<const int8_t*>(ptr(r0.z, r0.w));
+    x.ks = reinterpret_cast<const uint16_t*>(ptr(r1.x, r1.y));
+    x.vs = reinterpret_cast<const uint16_t*>(ptr(r1.z, r1.w));
+    x.pos = reinterpret_cast<const int32_t*>(ptr(r2.x, r2.y));
+    x.stride = r2.z;
+    x.n = r2.w;
+    x.coff = a.units[16 * u + 12];
+    return x;
+}
+
+// int8 codes of one dword -> two exact fp16 pairs (see codes_to_f16 in nq_page.hip)
+__device__ __forceinline__ void attn_codes_f16(uint32_t w, half2v& lo, half2v& hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const half2v bias = {(__fp16)-1152.0f, (__fp16)-1152.0f};
+    lo = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(u, 0x64646464u, 0x00050004u)) + bias;
+    hi = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(u, 0x64646464u, 0x00070006u)) + bias;
+}
+
+template <int DT>
+__device__ __forceinline__ float attn_load_f32(const void* p, size_t i) {
+    if constexpr (DT == NQ_F32) return static_cast<const float*>(p)[i];
+    else if constexpr (DT == NQ_BF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+    else return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// wave-wide reductions (64 lanes) through LDS-free cross-lane moves
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <int D, int G, int QDT>
+__global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
+    constexpr int C = D / 32;
+    constexpr int V2 = D / 64;  // value coordinates per lane in step 3
+    constexpr bool QF16 = QDT == NQ_F16;
+    __shared__ __attribute__((aligned(16))) float s_w[kChunk * G];  // [token][head]: logits, then e * scale_v / 2
+    __shared__ float s_a[kChunk];       // scale_v / 2 per token
+    __shared__ float s_red[4][G];
+    __shared__ float s_acc[4][G][D];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane & 3;
+    const int quad = lane >> 2;
+    const uint32_t w_item = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
+    if (w_item >= a.work) return;  // whole block
+    const uint32_t chunk = w_item / a.kv_heads;
+    const uint32_t kh = w_item % a.kv_heads;
+    const uint32_t row = (uint32_t)a.chunk_row[chunk];
+    const int u0 = a.chunk_units[chunk], u1 = a.chunk_units[chunk + 1];
+    const int n_tok = a.chunk_tokens[chunk] < kChunk ? a.chunk_tokens[chunk] : kChunk;
+
+    // the G query heads of this kv head, lane q's 32 coordinates of each
+    using qreg_t = typename std::conditional<QF16, half2v, float>::type;
+    constexpr int QR = QF16 ? 4 : 8;
+    qreg_t qv[G][C][QR];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const size_t qbase = ((size_t)row * a.q_heads + kh * G + g) * D;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            if constexpr (QF16) {
+                const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.query) + qbase +
+                                                                32 * c + 8 * q);
+                qv[g][c][0] = __builtin_bit_cast(half2v, w.x);
+                qv[g][c][1] = __builtin_bit_cast(half2v, w.y);
+                qv[g][c][2] = __builtin_bit_cast(half2v, w.z);
+                qv[g][c][3] = __builtin_bit_cast(half2v, w.w);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) qv[g][c][i] = attn_load_f32<QDT>(a.query, qbase + 32 * c + 8 * q + i);
+            }
+        }
+    }
+    const float qsig = quad_sign(q);
+
+    // ---- 1. keys and logits, one token per quad, 16 tokens per unit ----
+    // The next unit's record and key codes are loaded while the current one is
+    // decoded (indices clamped, so every load is unconditional and in bounds).
+    struct KeyIn {
+        uint2 w[C];
+        uint32_t ks, vs;
+        int32_t pos;
+    };
+    auto load_keys = [&](const UnitRec& r, KeyIn& k) {
+        const int t = quad < r.n ? quad : 0;
+        const size_t row = (size_t)kh * r.stride + t;
+        const int8_t* crow = r.kc + row * D;
+#pragma unroll
+        for (int c = 0; c < C; ++c) k.w[c] = *reinterpret_cast<const uint2*>(crow + 32 * c + 8 * q);
+        k.ks = r.ks[row];
+        k.vs = r.vs[row];
+        k.pos = r.pos[t];
+    };
+    int u = u0 + wave;
+    UnitRec rc = unit_rec(a, u < u1 ? u : u0);
+    KeyIn kin;
+    load_keys(rc, kin);
+    for (; u < u1; u += 4) {
+        const int un = u + 4 < u1 ? u + 4 : u;
+        const UnitRec rn = unit_rec(a, un);
+        KeyIn knext;
+        load_keys(rn, knext);
+
+        const int t = quad;
+        const bool valid = t < rc.n && rc.coff + t < kChunk;
+        half2v h[C][4];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            attn_codes_f16(kin.w[c].x, h[c][0], h[c][1]);
+            attn_codes_f16(kin.w[c].y, h[c][2], h[c][3]);
+        }
+        const float g = qsig * ((0.5f * f16_bits_to_f32(kin.ks)) * a.hscale);
+        const uint32_t pos = kin.pos < 0 ? 0u : ((uint32_t)kin.pos >= a.rope_n_pos ? a.rope_n_pos - 1u : (uint32_t)kin.pos);
+        float dm[C / 2][8], dp[C / 2][8];
+        load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, pos, q, dm, dp);
+        fwht_row_f16<C, false>(h, q);
+        float x[C][8];
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                x[c][2 * k] = __builtin_fmaf((float)h[c][k].x, g, 0.0f);
+                x[c][2 * k + 1] = __builtin_fmaf((float)h[c][k].y, g, 0.0f);
+            }
+        rope_stage_merged<C>(x, dm, dp);
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) asm("" : "+v"(x[c][i]));  // fp32, then fp16: two roundings
+        half2v kf[C][4];
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) kf[c][k] = half2v{(__fp16)x[c][2 * k], (__fp16)x[c][2 * k + 1]};
+
+#pragma unroll
+        for (int gq = 0; gq < G; ++gq) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                if constexpr (QF16) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_fdot2(kf[c][k], qv[gq][c][k], acc, false);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        acc = __builtin_fmaf((float)kf[c][k].x, qv[gq][c][2 * k], acc);
+                        acc = __builtin_fmaf((float)kf[c][k].y, qv[gq][c][2 * k + 1], acc);
+                    }
+                }
+            }
+            acc += dpp_f32<kQuadXor1>(acc);
+            acc += dpp_f32<kQuadXor2>(acc);
+            if (valid && q == 0) s_w[(rc.coff + t) * G + gq] = acc;
+        }
+        if (valid && q == 1) s_a[rc.coff + t] = 0.5f * f16_bits_to_f32(kin.vs);
+        rc = rn;
+        kin = knext;
+    }
+    __syncthreads();
+
+    // ---- 2. chunk max, exp, sum (fixed order) ----
+    // s_w is [token][head]; a thread's entries i, i + 256, ... all belong to head
+    // i % G (G divides 256), so lanes of one head reduce with xor offsets >= G.
+    const int my_g = threadIdx.x % G;
+    {
+        float v = -__builtin_inff();
+        for (int i = threadIdx.x; i < n_tok * G; i += 256) v = __builtin_fmaxf(v, s_w[i]);
+#pragma unroll
+        for (int o = 32; o >= G; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
+        if (lane < G) s_red[wave][lane] = v;
+    }
+    __syncthreads();
+    float m[G], l[G];
+#pragma unroll
+    for (int gq = 0; gq < G; ++gq)
+        m[gq] = __builtin_fmaxf(__builtin_fmaxf(s_red[0][gq], s_red[1][gq]), __builtin_fmaxf(s_red[2][gq], s_red[3][gq]));
+    __syncthreads();
+    {
+        const float mg = m[my_g];
+        float v = 0.0f;
+        for (int i = threadIdx.x; i < n_tok * G; i += 256) {
+            const float e = expf((s_w[i] - mg) * a.inv_scale);
+            v += e;
+            s_w[i] = e * s_a[i / G];
+        }
+#pragma unroll
+        for (int o = 32; o >= G; o >>= 1) v += __shfl_xor(v, o, 64);
+        if (lane < G) s_red[wave][lane] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int gq = 0; gq < G; ++gq) l[gq] = (s_red[0][gq] + s_red[1][gq]) + (s_red[2][gq] + s_red[3][gq]);
+
+    // ---- 3. values in the lattice domain: lane owns coordinates V2*lane .. +V2-1 ----
+    float acc[G][V2];
+#pragma unroll
+    for (int gq = 0; gq < G; ++gq)
+#pragma unroll
+        for (int v = 0; v < V2; ++v) acc[gq][v] = 0.0f;
+    // a unit's 16 value rows are loaded together, one unit ahead
+    using vword_t = typename std::conditional<V2 == 4, uint32_t, uint16_t>::type;
+    auto load_values = [&](const UnitRec& r, uint32_t (&vw)[16]) {
+        const int8_t* base = r.vc + (size_t)kh * r.stride * D + V2 * lane;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int t = i < r.n ? i : r.n - 1;
+            if constexpr (V2 == 1) vw[i] = (uint32_t)(uint8_t)base[(size_t)t * D];
+            else vw[i] = *reinterpret_cast<const vword_t*>(base + (size_t)t * D);
+        }
+    };
+    u = u0 + wave;
+    rc = unit_rec(a, u < u1 ? u : u0);
+    uint32_t vcur[16];
+    load_values(rc, vcur);
+    for (; u < u1; u += 4) {
+        const int un = u + 4 < u1 ? u + 4 : u;
+        const UnitRec rn = unit_rec(a, un);
+        uint32_t vnext[16];
+        load_values(rn, vnext);
+        int tn = rc.n;
+        if (rc.coff + tn > kChunk) tn = kChunk - rc.coff;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            if (r >= tn) break;
+            float cv[V2];
+            if constexpr (V2 == 1) {
+                cv[0] = (float)(int8_t)vcur[r];
+            } else {
+                half2v h0, h1;
+                attn_codes_f16(vcur[r], h0, h1);
+                cv[0] = (float)h0.x;
+                cv[1] = (float)h0.y;
+                if constexpr (V2 == 4) {
+                    cv[2] = (float)h1.x;
+                    cv[3] = (float)h1.y;
+                }
+            }
+            const int tc = rc.coff + r;
+            float wv[G];
+            if constexpr (G % 4 == 0) {
+#pragma unroll
+                for (int k = 0; k < G / 4; ++k) {
+                    const float4 w4 = reinterpret_cast<const float4*>(s_w + tc * G)[k];
+                    wv[4 * k] = w4.x;
+                    wv[4 * k + 1] = w4.y;
+                    wv[4 * k + 2] = w4.z;
+                    wv[4 * k + 3] = w4.w;
+                }
+            } else {
+#pragma unroll
+                for (int gq = 0; gq < G; ++gq) wv[gq] = s_w[tc * G + gq];
+            }
+#pragma unroll
+            for (int gq = 0; gq < G; ++gq)
+#pragma unroll
+                for (int v = 0; v < V2; ++v) acc[gq][v] = __builtin_fmaf(wv[gq], cv[v], acc[gq][v]);
+        }
+        rc = rn;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) vcur[i] = vnext[i];
+    }
+#pragma unroll
+    for (int gq = 0; gq < G; ++gq)
+#pragma unroll
+        for (int v = 0; v < V2; ++v) s_acc[wave][gq][V2 * lane + v] = acc[gq][v];
+    __syncthreads();
+    // the four waves' sums (fixed order), then the unnormalised Walsh-Hadamard
+    // over D in LDS, in place in s_acc[0]
+    for (int i = threadIdx.x; i < G * D; i += 256) {
+        const int gq = i / D, j = i % D;
+        s_acc[0][gq][j] = (s_acc[0][gq][j] + s_acc[1][gq][j]) + (s_acc[2][gq][j] + s_acc[3][gq][j]);
+    }
+#pragma unroll
+    for (int len = 1; len < D; len <<= 1) {
+        __syncthreads();
+        for (int p = threadIdx.x; p < G * D / 2; p += 256) {
+            const int gq = p / (D / 2), r = p % (D / 2);
+            const int i = (r / len) * 2 * len + (r % len);
+            const float x0 = s_acc[0][gq][i], x1 = s_acc[0][gq][i + len];
+            s_acc[0][gq][i] = x0 + x1;
+            s_acc[0][gq][i + len] = x0 - x1;
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * D; i += 256) {
+        const int gq = i / D, j = i % D;
+        float* pp = a.part + ((size_t)chunk * a.q_heads + kh * G + gq) * (D + 2);
+        pp[2 + j] = s_acc[0][gq][j];
+        if (j == 0) {
+            pp[0] = m[gq] * a.inv_scale;  // the chunk max in the scaled domain
+            pp[1] = l[gq];
+        }
+    }
+}
+
+// Merge the chunks of one (row, query head): 1024 threads, thread (group,
+// coordinate) sums every (1024 / D)-th chunk's weighted S y for its
+// coordinate; the groups are added in a fixed order.
+template <int D, int QDT>
+__global__ __launch_bounds__(1024) void paged_attn_combine(AttnArgs a) {
+    constexpr int NG = 1024 / D;
+    __shared__ float s_y[NG][D];
+    __shared__ float s_l[NG];
+    __shared__ float s_m[16];
+    const uint32_t row = blockIdx.x / a.q_heads;
+    const uint32_t qh = blockIdx.x % a.q_heads;
+    const int c0 = a.row_chunks[row], c1 = a.row_chunks[row + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = tid / D, j = tid % D;
+    float M = -__builtin_inff();
+    for (int c = c0 + tid; c < c1; c += 1024) M = __builtin_fmaxf(M, a.part[((size_t)c * a.q_heads + qh) * (D + 2)]);
+    M = wave_max(M);
+    if (lane == 0) s_m[wave] = M;
+    __syncthreads();
+    M = s_m[0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) M = __builtin_fmaxf(M, s_m[w]);
+    float y = 0.0f, L = 0.0f;
+#pragma unroll 4
+    for (int c = c0 + grp; c < c1; c += NG) {
+        const float* pp = a.part + ((size_t)c * a.q_heads + qh) * (D + 2);
+        const float f = expf(pp[0] - M);
+        y = __builtin_fmaf(f, pp[2 + j], y);
+        L = __builtin_fmaf(f, pp[1], L);
+    }
+    s_y[grp][j] = y;
+    if (j == 0) s_l[grp] = L;
+    __syncthreads();
+    if (grp != 0) return;
+    y = s_y[0][j];
+    L = s_l[0];
+#pragma unroll
+    for (int g = 1; g < NG; ++g) {
+        y += s_y[g][j];
+        L += s_l[g];
+    }
+    const size_t o = ((size_t)row * a.q_heads + qh) * D + j;
+    // attended value, then fp16 (the reference's .to(float16)), then the output type
+    const float val = c1 > c0 ? (y * a.hscale) / L : 0.0f;
+    const uint32_t hb = f32_to_f16_bits(val);
+    if constexpr (QDT == NQ_F32) {
+        static_cast<float*>(a.out)[o] = f16_bits_to_f32(hb);
+    } else if constexpr (QDT == NQ_BF16) {
+        // round to nearest even into bf16 (fp16 values are finite or inf)
+        const uint32_t u = __builtin_bit_cast(uint32_t, f16_bits_to_f32(hb));
+        static_cast<uint16_t*>(a.out)[o] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    } else {
+        static_cast<uint16_t*>(a.out)[o] = (uint16_t)hb;
+    }
+}
+
+template <int D, int G, int QDT>
+static hipError_t launch_attn(const AttnArgs& a, uint32_t n_chunks, uint32_t batch, hipStream_t s) {
+    if (n_chunks > 0) {
+        hipLaunchKernelGGL((paged_attn_kernel<D, G, QDT>), dim3(a.per_xcd * 8u), dim3(256), 0, s, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((paged_attn_combine<D, QDT>), dim3(batch * a.q_heads), dim3(1024), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int D, int QDT>
+static hipError_t attn_groups(int G, const AttnArgs& a, uint32_t n_chunks, uint32_t batch, hipStream_t s) {
+    switch (G) {
+        case 1: return launch_attn<D, 1, QDT>(a, n_chunks, batch, s);
+        case 2: return launch_attn<D, 2, QDT>(a, n_chunks, batch, s);
+        case 4: return launch_attn<D, 4, QDT>(a, n_chunks, batch, s);
+        default:
+            if constexpr (QDT == NQ_F16) return launch_attn<D, 8, QDT>(a, n_chunks, batch, s);
+            return hipErrorInvalidValue;
+    }
+}
+
+template <int D>
+static hipError_t attn_dtype(int qdt, int G, const AttnArgs& a, uint32_t n_chunks, uint32_t batch, hipStream_t s) {
+    switch (qdt) {
+        case NQ_F16: return attn_groups<D, NQ_F16>(G, a, n_chunks, batch, s);
+        case NQ_BF16: return attn_groups<D, NQ_BF16>(G, a, n_chunks, batch, s);
+        default: return attn_groups<D, NQ_F32>(G, a, n_chunks, batch, s);
+    }
+}
+
+}  // namespace nq
+
+extern "C" int32_t nq_paged_attention_chunk_tokens(void) { return nq::kChunk; }
+
+extern "C" int64_t nq_paged_attention_workspace(int32_t n_chunks, int32_t q_heads, int32_t head_dim) {
+    if (n_chunks <= 0 || q_heads <= 0 || head_dim <= 0) return 0;
+    return (int64_t)n_chunks * q_heads * (head_dim + 2) * (int64_t)sizeof(float);
+}
+
+extern "C" int nq_paged_attention(const nq_attn_desc* d, void* stream) {
+    using namespace nq;
+    NQ_CHECK_ARG(d != nullptr, "nq_paged_attention: desc is NULL");
+    NQ_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128 || d->head_dim == 256,
+                 "nq_paged_attention: head_dim %d unsupported (64, 128, 256)", d->head_dim);
+    NQ_CHECK_ARG(d->batch >= 0 && d->q_heads > 0 && d->kv_heads > 0 && d->q_heads % d->kv_heads == 0,
+                 "nq_paged_attention: q_heads %d must be a positive multiple of kv_heads %d", d->q_heads,
+                 d->kv_heads);
+    const int G = d->q_heads / d->kv_heads;
+    NQ_CHECK_ARG(G == 1 || G == 2 || G == 4 || (G == 8 && d->q_dtype == NQ_F16),
+                 "nq_paged_attention: %d query heads per kv head unsupported (1, 2, 4; 8 with fp16 queries)", G);
+    NQ_CHECK_ARG(d->q_dtype == NQ_F16 || d->q_dtype == NQ_BF16 || d->q_dtype == NQ_F32,
+                 "nq_paged_attention: unknown query dtype %d", d->q_dtype);
+    NQ_CHECK_ARG(d->n_chunks >= 0, "nq_paged_attention: n_chunks %d", d->n_chunks);
+    if (d->batch == 0) return NQ_OK;
+    NQ_CHECK_ARG(d->query && d->out && d->row_chunks, "nq_paged_attention: query, out and row_chunks are required");
+    if (d->n_chunks > 0) {
+        NQ_CHECK_ARG(d->units && d->chunk_units && d->chunk_row && d->chunk_tokens,
+                     "nq_paged_attention: chunk plan arrays are required");
+        NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos > 0 && d->rope_n_pos < (1ll << 31),
+                     "nq_paged_attention: keys need RoPE tables");
+        NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                     "nq_paged_attention: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
+        const int64_t need = nq_paged_attention_workspace(d->n_chunks, d->q_heads, d->head_dim);
+        NQ_CHECK_ARG(d->workspace != nullptr && d->workspace_bytes >= need,
+                     "nq_paged_attention: workspace of %lld bytes needed", (long long)need);
+        NQ_CHECK_ARG((uint64_t)d->n_chunks * d->kv_heads < (1ull << 31) - 8, "nq_paged_attention: grid too large");
+        NQ_CHECK_ARG(d->scale_divisor > 0.0f, "nq_paged_attention: scale_divisor must be positive");
+    }
+    NQ_CHECK_ARG((uint64_t)d->batch * d->q_heads < (1ull << 31), "nq_paged_attention: grid too large");
+    AttnArgs a = {};
+    a.query = d->query;
+    a.out = d->out;
+    a.units = d->units;
+    a.chunk_units = d->chunk_units;
+    a.chunk_row = d->chunk_row;
+    a.chunk_tokens = d->chunk_tokens;
+    a.row_chunks = d->row_chunks;
+    a.part = static_cast<float*>(d->workspace);
+    a.rope_cos = d->rope_cos;
+    a.rope_sin = d->rope_sin;
+    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dp = d->rope_cos_plus_sin;
+    a.q_heads = (uint32_t)d->q_heads;
+    a.kv_heads = (uint32_t)d->kv_heads;
+    a.rope_n_pos = (uint32_t)(d->rope_n_pos > 0 ? d->rope_n_pos : 1);
+    a.inv_scale = 1.0f / d->scale_divisor;
+    a.hscale = d->hadamard_scale;
+    a.work = (uint32_t)d->n_chunks * (uint32_t)d->kv_heads;
+    a.per_xcd = (a.work + 7u) / 8u;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e;
+    switch (d->head_dim) {
+        case 64: e = attn_dtype<64>(d->q_dtype, G, a, (uint32_t)d->n_chunks, (uint32_t)d->batch, s); break;
+        case 128: e = attn_dtype<128>(d->q_dtype, G, a, (uint32_t)d->n_chunks, (uint32_t)d->batch, s); break;
+        default: e = attn_dtype<256>(d->q_dtype, G, a, (uint32_t)d->n_chunks, (uint32_t)d->batch, s); break;
+    }
+    NQ_CHECK_HIP(e);
+    return NQ_OK;
+}

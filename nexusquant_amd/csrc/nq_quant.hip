@@ -35,6 +35,13 @@ struct QuantArgs {
     uint32_t n_tensors, bh, work, per_xcd;  // work items = ceil(seq_out/64) * bh * n_tensors
     float hscale;
     int32_t keep_mode;                      // NQ_KEEP_*
+    // page encoding (PAGE instantiations only): rows are a page's (head, token)
+    // rows flattened, token = row % page_tokens; keys rotate at positions[token]
+    const uint64_t* positions;  // per tensor int32 [page_tokens] (keys)
+    const uint64_t* codes8;     // per tensor int8 [rows, D]: 2p
+    const uint64_t* scales16;   // per tensor fp16 [rows]
+    uint32_t page_tokens;
+    uint32_t rope_n_pos;
 };
 
 // ------------------------------------------------------------------ E8 ----
@@ -286,8 +293,9 @@ __device__ __forceinline__ void store_group_words(uint8_t* dst, const uint32_t (
 
 // -------------------------------------------------------------- kernel ----
 
-template <int D, int L, bool IS_KEY, int DT, int DR>
+template <int D, int L, bool IS_KEY, int DT, int DR, bool PAGE = false>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
+    static_assert(!PAGE || DR == D, "page encoding takes power-of-two head dims");
     constexpr int C = D / 32;
     constexpr int RC = RopeChunks<D, DR>::value;
     const int q = threadIdx.x & 3;
@@ -311,6 +319,13 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
         // the host validates the list; clamp anyway so a bad index cannot read out of bounds
         const int32_t gi = a.gather[(size_t)b * a.seq_out + t_out];
         t_in = gi < 0 ? 0u : ((uint32_t)gi >= a.seq_in ? a.seq_in - 1u : (uint32_t)gi);
+    }
+    uint32_t pos_in = t_in;  // RoPE position of the source row
+    if constexpr (PAGE && IS_KEY) {
+        // the host validates positions against the table; clamp anyway so a bad
+        // position cannot read outside it
+        const int32_t pp = reinterpret_cast<const int32_t*>(a.positions[tensor])[t_in % a.page_tokens];
+        pos_in = pp < 0 ? 0u : ((uint32_t)pp >= a.rope_n_pos ? a.rope_n_pos - 1u : (uint32_t)pp);
     }
     bool keep = true;
     if (a.keep) keep = a.keep[(size_t)b * a.seq_in + t_in] != 0;
@@ -342,10 +357,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     constexpr bool MERGED = IS_KEY && DR == D;
     float cs[RC][8], sn[RC][8];  // cos / sin, or fl(cos - sin) / fl(cos + sin) when MERGED
     if constexpr (MERGED) {
-        load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, t_in, q, cs, sn);
+        load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, pos_in, q, cs, sn);
         rope_stage_merged<C>(x, cs, sn);
     } else if constexpr (IS_KEY) {
-        load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t_in, q, cs, sn);
+        load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, pos_in, q, cs, sn);
         apply_rope<D, DR, RC, true>(x, q, cs, sn);
     }
 
@@ -396,6 +411,31 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
         }
         if (a.scales) reinterpret_cast<float*>(a.scales[tensor])[out_row] = scale;
     }
+    if constexpr (PAGE) {
+        // int8 codes 2p and the fp16 row scale, the page format of the vLLM
+        // compressor (vllm_backend.py:305-314, 366-373)
+        if (!active) return;
+        if (q == 0 && a.scales16)
+            reinterpret_cast<uint16_t*>(a.scales16[tensor])[out_row] = (uint16_t)f32_to_f16_bits(scale);
+        int8_t* cdst = reinterpret_cast<int8_t*>(a.codes8[tensor]) + out_row * D;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const float off = coset[c] ? 0.5f : 0.0f;
+            uint32_t w[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float p = __builtin_amdgcn_fmed3f(x[c][4 * k + j] + off, -HL, HL);
+                    v |= ((uint32_t)(int32_t)(2.0f * p) & 0xffu) << (8 * j);
+                }
+                w[k] = v;
+            }
+            *reinterpret_cast<uint2*>(cdst + 32 * c + 8 * q) = make_uint2(w[0], w[1]);
+        }
+        return;
+    } else {
     constexpr int B = SymBits<L>::value;
     constexpr int ROW_BYTES = D / 8 * B;
     const float g = sigma * (a.hscale * scale);  // reconstruction multiplier, sign folded
@@ -520,6 +560,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
         w.w = __builtin_bit_cast(uint32_t, o[3]);
         *reinterpret_cast<uint4*>(dst + (32 * c + 8 * q) / 2) = w;
     }
+    }  // !PAGE
 }
 
 // ---------------------------------------------------------------- host ----
@@ -592,7 +633,7 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
                      "nq_quantize: RoPE table has %lld positions, need %d",
                      (long long)d->rope_n_pos, d->seq_in > d->seq_out ? d->seq_in : d->seq_out);
     }
-    QuantArgs a;
+    QuantArgs a = {};
     a.src = d->src;
     a.recon = d->recon;
     a.syms = d->syms;
@@ -624,6 +665,95 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
         case 96: e = dispatch_levels<128, 96>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
         case 128: e = dispatch_levels<128>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
         default: e = dispatch_levels<256>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
+    }
+    NQ_CHECK_HIP(e);
+    return NQ_OK;
+}
+
+// ------------------------------------------------------- page encoding ----
+
+namespace nq {
+
+template <int D, int L, bool K, int DT>
+static hipError_t launch_page(const QuantArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((quant_rows_kernel<D, L, K, DT, D, true>), dim3(a.per_xcd * 8u), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int D, int L, bool K>
+static hipError_t page_dtype(int dt, const QuantArgs& a, hipStream_t s) {
+    switch (dt) {
+        case NQ_F16: return launch_page<D, L, K, NQ_F16>(a, s);
+        case NQ_BF16: return launch_page<D, L, K, NQ_BF16>(a, s);
+        default: return launch_page<D, L, K, NQ_F32>(a, s);
+    }
+}
+
+template <int D>
+static hipError_t page_levels(int L, bool key, int dt, const QuantArgs& a, hipStream_t s) {
+    switch (L) {
+        case 4: return key ? page_dtype<D, 4, true>(dt, a, s) : page_dtype<D, 4, false>(dt, a, s);
+        case 8: return key ? page_dtype<D, 8, true>(dt, a, s) : page_dtype<D, 8, false>(dt, a, s);
+        default: return key ? page_dtype<D, 16, true>(dt, a, s) : page_dtype<D, 16, false>(dt, a, s);
+    }
+}
+
+}  // namespace nq
+
+extern "C" int nq_page_encode(const nq_page_desc* d, void* stream) {
+    using namespace nq;
+    NQ_CHECK_ARG(d != nullptr, "nq_page_encode: desc is NULL");
+    NQ_CHECK_ARG(d->n_pages >= 0 && d->n_pages <= 65535, "nq_page_encode: n_pages %d out of range", d->n_pages);
+    if (d->n_pages == 0) return NQ_OK;
+    NQ_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128 || d->head_dim == 256,
+                 "nq_page_encode: head_dim %d unsupported (64, 128, 256)", d->head_dim);
+    NQ_CHECK_ARG(d->levels == 4 || d->levels == 8 || d->levels == 16,
+                 "nq_page_encode: levels must be 4, 8 or 16 (bits 2, 3, 4; got %d)", d->levels);
+    NQ_CHECK_ARG(d->dtype == NQ_F16 || d->dtype == NQ_BF16 || d->dtype == NQ_F32,
+                 "nq_page_encode: unknown dtype %d", d->dtype);
+    NQ_CHECK_ARG(d->heads > 0 && d->tokens >= 0, "nq_page_encode: bad geometry");
+    NQ_CHECK_ARG(d->src && d->codes && d->scales, "nq_page_encode: src, codes and scales are required");
+    const uint64_t rows = (uint64_t)d->heads * d->tokens;
+    NQ_CHECK_ARG(rows < (1ull << 31), "nq_page_encode: %llu rows per page exceeds 2^31",
+                 (unsigned long long)rows);
+    if (rows == 0) return NQ_OK;
+    NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                 "nq_page_encode: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
+    if (d->is_key) {
+        NQ_CHECK_ARG(d->positions != nullptr, "nq_page_encode: keys need positions");
+        NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos > 0 && d->rope_n_pos < (1ll << 31),
+                     "nq_page_encode: keys need RoPE tables");
+    }
+    QuantArgs a = {};
+    a.src = d->src;
+    a.rope_cos = d->rope_cos;
+    a.rope_sin = d->rope_sin;
+    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dp = d->rope_cos_plus_sin;
+    a.heads = 1u;  // a page's (head, token) rows are one flat run of rows
+    a.seq_in = a.seq_out = (uint32_t)rows;
+    a.rows = (uint32_t)rows;
+    a.hscale = d->hadamard_scale;
+    a.keep_mode = NQ_KEEP_ZERO;
+    a.n_tensors = (uint32_t)d->n_pages;
+    a.bh = 1u;
+    a.positions = d->positions;
+    a.codes8 = d->codes;
+    a.scales16 = d->scales;
+    a.page_tokens = (uint32_t)(d->tokens > 0 ? d->tokens : 1);
+    a.rope_n_pos = (uint32_t)(d->is_key ? d->rope_n_pos : 1);
+    const uint64_t work = (rows + 63) / 64 * a.n_tensors;
+    NQ_CHECK_ARG(work < (1ull << 32) - 8, "nq_page_encode: %llu work items exceed the grid limit",
+                 (unsigned long long)work);
+    a.work = (uint32_t)work;
+    a.per_xcd = (uint32_t)((work + 7) / 8);
+    hipStream_t s = (hipStream_t)stream;
+    const bool key = d->is_key != 0;
+    hipError_t e;
+    switch (d->head_dim) {
+        case 64: e = page_levels<64>(d->levels, key, d->dtype, a, s); break;
+        case 128: e = page_levels<128>(d->levels, key, d->dtype, a, s); break;
+        default: e = page_levels<256>(d->levels, key, d->dtype, a, s); break;
     }
     NQ_CHECK_HIP(e);
     return NQ_OK;

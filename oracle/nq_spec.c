@@ -55,6 +55,14 @@
  *     resolution except at fp16 rounding ties.  Keep the first d outputs,
  *     round to fp16 (round to nearest even).
  *
+ *  8. Page decode (the vLLM compressor's int8 2p codes and fp16 scales,
+ *     vllm_backend.py:394-429): w = S c on the integer codes c = 2p is exact in
+ *     fp32 in any order; then w * g with g = fl(fl(0.5 * scale) * h_D)
+ *     (0.5 * scale is exact), so each coordinate is rounded once where the
+ *     reference's dense GEMM rounds every product and partial sum.  Keys stop
+ *     w before the top stage and finish with the merged step of 1. at the
+ *     stored position; fp16 round to nearest even.
+ *
  * Code symbols: the group's coset bit is 1 when the half-integer candidate was
  * chosen.  Integer coset: sym = p + L/2.  Half coset: the clamp folds one edge
  * point onto +-L/2 (the top edge when L/2 is even, the bottom edge when L/2 is
@@ -343,3 +351,30 @@ void nqs_quant_rows(int64_t n, int d, int D, int L, float hD,
     }
 }
 
+
+/* Page decode (item 8 above): codes int8 [n, D] (2p), scales fp16 [n]; keys
+ * read cos/sin rows [n, D/2] at their stored positions. */
+void nqs_page_decode(int64_t n, int D, int is_key, float hD, const int8_t* codes, const uint16_t* scales16,
+                     const float* cos_rows, const float* sin_rows, uint16_t* out) {
+    const int half = D / 2;
+    for (int64_t row = 0; row < n; ++row) {
+        float w[NQS_MAXD];
+        for (int i = 0; i < D; ++i) w[i] = (float)codes[row * D + i];
+        fwht_stages(w, D, is_key ? half : D);
+        const float g = (0.5f * nqs_f16_to_f32(scales16[row])) * hD;
+        for (int i = 0; i < D; ++i) w[i] = w[i] * g;
+        uint16_t* o = out + row * D;
+        if (is_key) {
+            const float* c = cos_rows + row * half;
+            const float* s = sin_rows + row * half;
+            for (int i = 0; i < half; ++i) {
+                float lo = w[i], hi = w[i + half];
+                float dm = c[i] - s[i], dp = c[i] + s[i];
+                o[i] = nqs_f32_to_f16(fmaf(lo, dm, hi * dp));
+                o[i + half] = nqs_f32_to_f16(fmaf(lo, dp, -(hi * dm)));
+            }
+        } else {
+            for (int i = 0; i < D; ++i) o[i] = nqs_f32_to_f16(w[i]);
+        }
+    }
+}

@@ -33,6 +33,8 @@ def lib():
         L.nqs_quant_rows.restype = None
         L.nqs_e8_group.argtypes = [P, ctypes.c_float, P, P, P]
         L.nqs_e8_group.restype = None
+        L.nqs_page_decode.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_float, P, P, P, P, P]
+        L.nqs_page_decode.restype = None
         L.nqs_f32_to_f16.argtypes = [ctypes.c_float]
         L.nqs_f32_to_f16.restype = ctypes.c_uint16
         _lib = L
@@ -97,3 +99,24 @@ def e8_groups(x: np.ndarray, L: int):
         f(_ptr(x[i]), float(L // 2), _ptr(p[i]), ctypes.c_void_p(cs[i:].ctypes.data),
           ctypes.c_void_p(mg[i:].ctypes.data))
     return p, cs, mg
+
+
+def page_decode(codes: np.ndarray, scales16: np.ndarray, is_key: bool, cos_rows=None, sin_rows=None):
+    """Run the C oracle's page decode on int8 codes [n, D] and fp16 scales [n]
+    (keys: cos/sin rows [n, D/2] at each row's stored position) -> fp16 [n, D]."""
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    n, D = codes.shape
+    sc = np.ascontiguousarray(scales16, dtype=np.float16).view(np.uint16)
+    out = np.empty((n, D), np.uint16)
+    tabs = [None if t is None else np.ascontiguousarray(t, dtype=np.float32) for t in (cos_rows, sin_rows)]
+    lib().nqs_page_decode(n, D, int(is_key), hadamard_constant(D), _ptr(codes), _ptr(sc),
+                          _ptr(tabs[0]), _ptr(tabs[1]), _ptr(out))
+    return out.view(np.float16)
+
+
+def page_encode(x: np.ndarray, L: int, cos_rows=None, sin_rows=None):
+    """The page encoder's arithmetic (the row quantizer with keys rotated at
+    each row's position): rows x [n, D] -> (int8 codes 2p [n, D], fp16 scales [n],
+    margins [n, D/8])."""
+    o = quant_rows(x, L, cos_in=cos_rows, sin_in=sin_rows, cos_out=cos_rows, sin_out=sin_rows, margins=True)
+    return (2.0 * o["p"]).astype(np.int8), o["scale"].astype(np.float16), o["margin"]

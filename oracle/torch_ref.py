@@ -24,6 +24,9 @@ Pinning (see tests/test_oracle_*.py):
   score_real_from_qk      golden fixtures written through transformers' eager
                           attention (third-party formula, transformers 5.15.0)
   delta_encode/decode     closed form + lossless round trip
+  vllm_* (page caller)    golden fixtures written by the reference's
+                          integrations/vllm_backend.py (compress / decompress /
+                          logits / nibble packing / paged forward)
 """
 
 from __future__ import annotations
@@ -597,3 +600,122 @@ def delta_decode(delta: torch.Tensor) -> torch.Tensor:
     import numpy as np
     x = delta.numpy()
     return torch.from_numpy(np.cumsum(x, axis=1).astype(np.int8))
+
+
+# ---------------------------------------------------------------------------
+# vLLM page caller  (nexusquant/integrations/vllm_backend.py)
+# ---------------------------------------------------------------------------
+
+def vllm_quantize_with_scales(x: torch.Tensor, levels: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(h, s, d) fp32 -> int8 codes 2p (h, s, d), fp32 scales (h, s) (vllm_backend.py:267-314)."""
+    h, s, d = x.shape
+    flat = x.reshape(h * s, d)
+    amax = flat.abs().amax(dim=-1, keepdim=True).clamp(min=1e-8)
+    scale = amax / (levels / 2)
+    normalized = flat / scale
+    pad = (8 - d % 8) % 8
+    if pad > 0:
+        normalized = F.pad(normalized, (0, pad))
+    lp = e8_nearest_point(normalized.reshape(-1, 8)).clamp(-levels / 2, levels / 2)
+    codes_full = lp.reshape(h * s, d + pad)[..., :d]
+    codes = (codes_full * 2).round().clamp(-127, 127).to(torch.int8).reshape(h, s, d)
+    return codes, scale.squeeze(-1).reshape(h, s)
+
+
+def vllm_dequantize(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """(codes * 0.5) * scale in fp32 (vllm_backend.py:316-338)."""
+    return (codes.float() * 0.5) * scales.float().unsqueeze(-1)
+
+
+def _page_tables(positions: torch.Tensor, d: int, base: float):
+    c, sn = rope_cos_sin(positions.to(torch.int32).float(), d, base)
+    return c.unsqueeze(0), sn.unsqueeze(0)
+
+
+def vllm_compress_page(key_page: torch.Tensor, value_page: torch.Tensor, positions: torch.Tensor,
+                       bits: int, base: float):
+    """-> (key_codes, value_codes, key_scales fp16, value_scales fp16) (vllm_backend.py:344-392, 187-224)."""
+    levels = 2 ** bits
+    d = key_page.shape[-1]
+    H = hadamard_matrix(d)
+    k = key_page.float()
+    v = value_page.float()
+    c, sn = _page_tables(positions, d, base)
+    k_nr = _rot_inverse(k, c, sn)
+    k_rot = torch.einsum('hsd,de->hse', k_nr, H.float())
+    kc, ks = vllm_quantize_with_scales(k_rot, levels)
+    v_rot = torch.einsum('hsd,de->hse', v, H.float())
+    vc, vs = vllm_quantize_with_scales(v_rot, levels)
+    return kc, vc, ks.to(torch.float16), vs.to(torch.float16)
+
+
+def vllm_decompress_keys_fp32(key_codes, key_scales, positions, base: float) -> torch.Tensor:
+    """Dequantize, inverse Hadamard, RoPE at the stored positions (vllm_backend.py:410-415, 226-265)."""
+    d = key_codes.shape[-1]
+    H = hadamard_matrix(d)
+    k_rot = vllm_dequantize(key_codes, key_scales)
+    k_nr = torch.einsum('hsd,ed->hse', k_rot, H.float())
+    c, sn = _page_tables(positions, d, base)
+    return _rot_forward(k_nr, c, sn)
+
+
+def vllm_decompress_page(key_codes, value_codes, key_scales, value_scales, positions, base: float):
+    """-> (keys, values) fp16 (vllm_backend.py:394-429)."""
+    d = key_codes.shape[-1]
+    H = hadamard_matrix(d)
+    keys = vllm_decompress_keys_fp32(key_codes, key_scales, positions, base).to(torch.float16)
+    v_rot = vllm_dequantize(value_codes, value_scales)
+    values = torch.einsum('hsd,ed->hse', v_rot, H.float()).to(torch.float16)
+    return keys, values
+
+
+def vllm_decompress_for_attention(key_codes, key_scales, positions, query, base: float) -> torch.Tensor:
+    """Logits (h, q_len, s) = q . k / sqrt(d) on fp32 keys (vllm_backend.py:431-467)."""
+    scale = math.sqrt(key_codes.shape[-1])
+    keys = vllm_decompress_keys_fp32(key_codes, key_scales, positions, base)
+    return torch.einsum('hqd,hsd->hqs', query.float(), keys) / scale
+
+
+def vllm_paged_forward(query: torch.Tensor, pages: dict, block_tables, context_lens, base: float) -> torch.Tensor:
+    """Decode attention over pages {block_id: (kc, vc, ks, vs, positions)} (vllm_backend.py:692-765)."""
+    batch_size, num_heads, head_dim = query.shape
+    scale = math.sqrt(head_dim)
+    output = torch.zeros_like(query)
+    for b in range(batch_size):
+        ctx_len = int(context_lens[b])
+        if ctx_len == 0:
+            continue
+        ks, vs = [], []
+        for block_id in block_tables[b]:
+            if block_id not in pages:
+                continue
+            k_page, v_page = vllm_decompress_page(*pages[block_id], base)
+            ks.append(k_page)
+            vs.append(v_page)
+        if not ks:
+            continue
+        keys = torch.cat(ks, dim=1)[:, :ctx_len, :]
+        values = torch.cat(vs, dim=1)[:, :ctx_len, :]
+        q3 = query[b].unsqueeze(1).float()
+        logits = torch.einsum('hqd,hsd->hqs', q3, keys.float()) / scale
+        w = torch.softmax(logits, dim=-1)
+        att = torch.einsum('hqs,hsd->hqd', w, values.float())
+        output[b] = att.squeeze(1).to(torch.float16)
+    return output
+
+
+def pack_codes_nibble(codes: torch.Tensor) -> torch.Tensor:
+    """(..., d) int8 -> (..., ceil(d/2)) uint8 nibbles (vllm_backend.py:475-515)."""
+    d = codes.shape[-1]
+    c = (codes.to(torch.int32) + 8).clamp(0, 15)
+    if d % 2 != 0:
+        c = F.pad(c, (0, 1))
+    return ((c[..., 0::2] & 0xF) | ((c[..., 1::2] & 0xF) << 4)).to(torch.uint8)
+
+
+def unpack_codes_nibble(packed: torch.Tensor, original_d: int) -> torch.Tensor:
+    """Inverse nibble unpacking (vllm_backend.py:517-536)."""
+    p = packed.to(torch.int32)
+    inter = torch.stack([p & 0xF, (p >> 4) & 0xF], dim=-1)
+    shape = list(inter.shape)[:-2] + [-1]
+    return (inter.reshape(shape)[..., :original_d] - 8).to(torch.int8)

@@ -8,7 +8,7 @@ torch.topk keep masks, and the real-attention scorer through transformers'
 eager attention.  Nothing under /root/reference is copied; only the numbers it
 produces are stored, as small .npz files next to this script.
 
-Usage:  python tests/golden/make_golden.py [/root/reference]
+Usage:  python tests/golden/make_golden.py [/root/reference [evict_soft | vllm_pages]]
 """
 
 from __future__ import annotations
@@ -189,9 +189,69 @@ def make_soft():
          k_out=torch.stack(c.key_cache), v_out=torch.stack(c.value_cache))
 
 
+def make_vllm():
+    """9. vLLM page caller and decode consumer (integrations/vllm_backend.py):
+    compress_page / decompress_page / decompress_for_attention at bits 2, 3, 4
+    (head_dim 128, 128, 64; fp16 and fp32 inputs; non-contiguous absolute
+    positions), nibble packing, and NexusQuantPagedAttention.forward over 16-token
+    pages with a missing block, a partial context, an empty row and a negative
+    context length (Python slice semantics)."""
+    from nexusquant.integrations.vllm_backend import NexusQuantKVCompressor, NexusQuantPagedAttention
+    g = torch.Generator().manual_seed(91)
+    out = {}
+    cases = [("b2", 2, 128, torch.float16, torch.arange(16, dtype=torch.int32) * 3 + 5000),
+             ("b3", 3, 128, torch.float32, torch.randint(0, 131072, (16,), generator=g, dtype=torch.int32)),
+             ("b4", 4, 64, torch.float16, torch.arange(24, dtype=torch.int32) + 777)]
+    for tag, bits, d, dt, pos in cases:
+        n = pos.numel()
+        comp = NexusQuantKVCompressor(head_dim=d, bits=bits, rope_base=500000.0 if tag == "b3" else 10000.0)
+        k = (torch.randn(4, n, d, generator=g) * 2).to(dt)
+        k[:, :, :3] *= 6
+        v = (torch.randn(4, n, d, generator=g) * 0.5).to(dt)
+        page = comp.compress_page(k, v, pos)
+        kd, vd = comp.decompress_page(page)
+        qry = torch.randn(4, 3, d, generator=g).to(torch.float16)
+        logits = comp.decompress_for_attention(page, qry)
+        out.update({f"{tag}_k": k, f"{tag}_v": v, f"{tag}_pos": pos,
+                    f"{tag}_kc": page.key_codes, f"{tag}_vc": page.value_codes,
+                    f"{tag}_ks": page.key_scales, f"{tag}_vs": page.value_scales,
+                    f"{tag}_kdec": kd, f"{tag}_vdec": vd, f"{tag}_q": qry, f"{tag}_logits": logits})
+    codes = torch.randint(-12, 13, (5, 3, 33), generator=g, dtype=torch.int8)
+    out["nib_codes"] = codes
+    out["nib_packed"] = NexusQuantKVCompressor.pack_codes_nibble(codes)
+    out["nib_unpacked"] = NexusQuantKVCompressor.unpack_codes_nibble(out["nib_packed"], 33)
+    # paged decode attention
+    comp = NexusQuantKVCompressor(head_dim=128, bits=2, rope_base=10000.0)
+    attn = NexusQuantPagedAttention(comp)
+    cache = {}
+    pk, pv, pp = [], [], []
+    for bid in range(6):
+        pos = torch.arange(16, dtype=torch.int32) + 16 * bid
+        k = (torch.randn(4, 16, 128, generator=g) * 2).to(torch.float16)
+        v = (torch.randn(4, 16, 128, generator=g) * 0.5).to(torch.float16)
+        cache[bid] = comp.compress_page(k, v, pos)
+        pk.append(k)
+        pv.append(v)
+        pp.append(pos)
+    tables = [[0, 1, 2], [3, 99, 4], [5], [2, 0]]
+    ctx = torch.tensor([40, 20, 0, -5], dtype=torch.int32)
+    query = torch.randn(4, 4, 128, generator=g).to(torch.float16)
+    fwd = attn.forward(query, cache, cache, tables, ctx)
+    out.update({"fwd_k": torch.stack(pk), "fwd_v": torch.stack(pv), "fwd_pos": torch.stack(pp),
+                "fwd_kc": torch.stack([cache[i].key_codes for i in range(6)]),
+                "fwd_vc": torch.stack([cache[i].value_codes for i in range(6)]),
+                "fwd_ks": torch.stack([cache[i].key_scales for i in range(6)]),
+                "fwd_vs": torch.stack([cache[i].value_scales for i in range(6)]),
+                "fwd_query": query, "fwd_ctx": ctx, "fwd_out": fwd})
+    save("vllm_pages", **out)
+
+
 if __name__ == "__main__":
     if sys.argv[2:] == ["evict_soft"]:
         make_soft()
+    elif sys.argv[2:] == ["vllm_pages"]:
+        make_vllm()
     else:
         main()
         make_soft()
+        make_vllm()

@@ -36,7 +36,8 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert sorted(_lib.SIGNATURES) == names, "ctypes signature table out of sync with the header"
 
 
-@pytest.mark.parametrize("cname,pystruct", [("nq_quant_desc", _lib.QuantDesc), ("nq_codes_desc", _lib.CodesDesc)])
+@pytest.mark.parametrize("cname,pystruct", [("nq_quant_desc", _lib.QuantDesc), ("nq_codes_desc", _lib.CodesDesc),
+                                            ("nq_page_desc", _lib.PageDesc), ("nq_attn_desc", _lib.AttnDesc)])
 def test_struct_layout_matches_the_c_compiler(tmp_path, cname, pystruct):
     """ctypes offsets of every descriptor field equal gcc's offsetof on the header."""
     fields = [f[0] for f in pystruct._fields_]
@@ -55,5 +56,5 @@ def test_struct_layout_matches_the_c_compiler(tmp_path, cname, pystruct):
 
 def test_abi_version_and_error_calls_need_no_gpu():
     lib = _lib.load()
-    assert lib.nq_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.nq_abi_version() == _lib.ABI_VERSION == 3
     assert isinstance(lib.nq_last_error(), bytes)
