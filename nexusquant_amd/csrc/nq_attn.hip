@@ -131,28 +131,22 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     const int u0 = a.chunk_units[chunk], u1 = a.chunk_units[chunk + 1];
     const int n_tok = a.chunk_tokens[chunk] < kChunk ? a.chunk_tokens[chunk] : kChunk;
 
-    // the G query heads of this kv head, lane q's 32 coordinates of each
+    // the G query heads of this kv head in LDS (fp16 queries as fp16, others as
+    // fp32); every quad reads the same slices, so the reads are broadcasts
     using qreg_t = typename std::conditional<QF16, half2v, float>::type;
-    constexpr int QR = QF16 ? 4 : 8;
-    qreg_t qv[G][C][QR];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const size_t qbase = ((size_t)row * a.q_heads + kh * G + g) * D;
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            if constexpr (QF16) {
-                const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.query) + qbase +
-                                                                32 * c + 8 * q);
-                qv[g][c][0] = __builtin_bit_cast(half2v, w.x);
-                qv[g][c][1] = __builtin_bit_cast(half2v, w.y);
-                qv[g][c][2] = __builtin_bit_cast(half2v, w.z);
-                qv[g][c][3] = __builtin_bit_cast(half2v, w.w);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) qv[g][c][i] = attn_load_f32<QDT>(a.query, qbase + 32 * c + 8 * q + i);
-            }
+    constexpr int QR = QF16 ? 4 : 8;  // registers per 8 coordinates
+    __shared__ __attribute__((aligned(16))) qreg_t s_q[G][C][4][QR];
+    for (int i = threadIdx.x; i < G * D; i += 256) {
+        const int g = i / D, j = i % D;
+        const size_t qi = ((size_t)row * a.q_heads + kh * G + g) * D + j;
+        const int c = j / 32, qq = (j / 8) % 4, k = j % 8;
+        if constexpr (QF16) {
+            reinterpret_cast<uint16_t*>(&s_q[g][c][qq][0])[k] = static_cast<const uint16_t*>(a.query)[qi];
+        } else {
+            s_q[g][c][qq][k] = attn_load_f32<QDT>(a.query, qi);
         }
     }
+    __syncthreads();
     const float qsig = quad_sign(q);
 
     // ---- 1. keys and logits, one token per quad, 16 tokens per unit ----
@@ -220,14 +214,17 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
             float acc = 0.0f;
 #pragma unroll
             for (int c = 0; c < C; ++c) {
+                qreg_t qv[QR];
+#pragma unroll
+                for (int k = 0; k < QR; ++k) qv[k] = s_q[gq][c][q][k];
                 if constexpr (QF16) {
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_fdot2(kf[c][k], qv[gq][c][k], acc, false);
+                    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_fdot2(kf[c][k], qv[k], acc, false);
                 } else {
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
-                        acc = __builtin_fmaf((float)kf[c][k].x, qv[gq][c][2 * k], acc);
-                        acc = __builtin_fmaf((float)kf[c][k].y, qv[gq][c][2 * k + 1], acc);
+                        acc = __builtin_fmaf((float)kf[c][k].x, qv[2 * k], acc);
+                        acc = __builtin_fmaf((float)kf[c][k].y, qv[2 * k + 1], acc);
                     }
                 }
             }
