@@ -218,6 +218,42 @@ int nq_delta_decode(const uint64_t* deltas, const uint64_t* out, int32_t n_tenso
                     int32_t coords, void* stream);
 
 /*
+ * Merge eviction, run before the hard-eviction quantizer: for each batch row,
+ * every evicted token's value is added into the kept token whose value
+ * centroid is most similar (cosine, first on ties), weighted by
+ * w = fp32(imp_e / (imp_s + imp_e + 1e-8)) (double arithmetic), over the
+ * n_tensors value tensors [batch, heads, seq, head_dim] (heads <= 256) of
+ * the layers whose seq equals the mask's.  Centroids are the fp32 means over
+ * heads, averaged over those layers; merged rows accumulate
+ * v_s = fl(v_s + fl(w_e v_e)) over their evicted tokens in ascending order and
+ * are rounded once to the tensor type; every other row is copied.  keep /
+ * kept_idx / n_kept are nq_keep_mask's outputs.  Optional outputs: the
+ * centroids, and survivor [batch, seq] (the survivor position of each
+ * evicted position, -1 at kept positions).  workspace: nq_merge_workspace
+ * bytes (caller owned).
+ *
+ * Replaces: NexusQuantEvict._apply_merge_eviction  pipeline.py:961-1048
+ */
+typedef struct nq_merge_desc {
+    int32_t n_tensors;
+    int32_t batch, heads, seq, head_dim;
+    int32_t dtype;               /* NQ_F16 / NQ_BF16 / NQ_F32 */
+    const uint64_t* src;         /* value tensors (device array of addresses) */
+    const uint64_t* dst;         /* merged outputs, same shape and type; must not alias src */
+    const uint8_t* keep;         /* [batch, seq] */
+    const int32_t* kept_idx;     /* [batch, seq] */
+    const int32_t* n_kept;       /* [batch] */
+    const float* importance;     /* [batch, seq] */
+    float* centroids;            /* optional [batch, seq, head_dim] */
+    int32_t* survivor;           /* optional [batch, seq] */
+    void* workspace;
+    int64_t workspace_bytes;
+} nq_merge_desc;
+
+int64_t nq_merge_workspace(int32_t batch, int32_t seq, int32_t head_dim);
+int nq_merge_values(const nq_merge_desc* desc, void* stream);
+
+/*
  * Pages of the vLLM compressor: n_pages pages of identical geometry
  * [heads, tokens, head_dim] (head_dim 64, 128 or 256), keys or values, at
  * `levels` 4, 8 or 16 (bits 2, 3, 4).  The format is the reference's

@@ -48,6 +48,16 @@ class CodesDesc(ctypes.Structure):
     ]
 
 
+class MergeDesc(ctypes.Structure):
+    """Mirror of nq_merge_desc in include/nexusquant_amd.h."""
+    _fields_ = [
+        ("n_tensors", ctypes.c_int32), ("batch", ctypes.c_int32), ("heads", ctypes.c_int32),
+        ("seq", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("dtype", ctypes.c_int32),
+        ("src", _P), ("dst", _P), ("keep", _P), ("kept_idx", _P), ("n_kept", _P), ("importance", _P),
+        ("centroids", _P), ("survivor", _P), ("workspace", _P), ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
 class PageDesc(ctypes.Structure):
     """Mirror of nq_page_desc in include/nexusquant_amd.h."""
     _fields_ = [
@@ -94,6 +104,8 @@ SIGNATURES = {
     "nq_delta_decode": ([_P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "nq_score_real_workspace": ([_I32, _I32, _I32], _I64),
     "nq_score_real": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
+    "nq_merge_workspace": ([_I32, _I32, _I32], _I64),
+    "nq_merge_values": ([ctypes.POINTER(MergeDesc), _P], ctypes.c_int),
     "nq_page_encode": ([ctypes.POINTER(PageDesc), _P], ctypes.c_int),
     "nq_page_decode": ([ctypes.POINTER(PageDesc), _P], ctypes.c_int),
     "nq_page_logits": ([ctypes.POINTER(PageDesc), _P, _I32, _I32, _F32, _P, _P], ctypes.c_int),

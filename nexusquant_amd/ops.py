@@ -339,6 +339,58 @@ def keep_mask(importance: torch.Tensor, rate: float, sliding_window: int = 32,
     return keep, kept, n_kept
 
 
+def merge_values(values: Sequence[torch.Tensor], keep: torch.Tensor, kept_idx: torch.Tensor,
+                 n_kept: torch.Tensor, importance: torch.Tensor, *, centroids: bool = False,
+                 survivors: bool = False):
+    """Merge eviction over same-shaped value tensors [b, h, s, d] (nq_merge_values).
+
+    keep / kept_idx / n_kept are keep_mask()'s outputs for this seq.  Returns
+    (merged tensors, centroids [b, s, d] fp32 or None, survivor [b, s] int32 or
+    None: the survivor position of each evicted position, -1 at kept ones).
+    """
+    lib = _lib.load()
+    if not values:
+        return [], None, None
+    v0 = values[0]
+    _lib.require_device(v0, "value tensor")
+    if v0.dim() != 4:
+        raise ValueError(f"expected value tensors [batch, heads, seq, head_dim], got {tuple(v0.shape)}")
+    b, h, s, d = v0.shape
+    for v in values:
+        if v.shape != v0.shape or v.dtype != v0.dtype or v.device != v0.device:
+            raise NotImplementedError("merge eviction over layers of different value shapes or dtypes")
+    if d not in (64, 96, 128, 256) or h > 256:
+        raise NotImplementedError(f"merge eviction takes head_dim 64, 96, 128 or 256 and <= 256 heads "
+                                  f"(got {d}, {h})")
+    if tuple(keep.shape) != (b, s) or tuple(kept_idx.shape) != (b, s) or tuple(importance.shape) != (b, s):
+        raise ValueError("keep, kept_idx and importance must be [batch, seq]")
+    dev = v0.device
+    src = [v.contiguous() for v in values]
+    out = list(torch.empty(len(src), b, h, s, d, dtype=v0.dtype, device=dev).unbind(0))
+    kp = keep.to(device=dev, dtype=torch.uint8).contiguous()
+    ki = kept_idx.to(device=dev, dtype=torch.int32).contiguous()
+    nk = n_kept.to(device=dev, dtype=torch.int32).contiguous()
+    imp = importance.to(device=dev, dtype=torch.float32).contiguous()
+    cent = torch.empty(b, s, d, dtype=torch.float32, device=dev) if centroids else None
+    surv = torch.empty(b, s, dtype=torch.int32, device=dev) if survivors else None
+    ws_bytes = lib.nq_merge_workspace(b, s, d)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    staged = _PtrArrays([src, out], dev)
+    arrays = staged.arrays
+    desc = _lib.MergeDesc(n_tensors=len(src), batch=b, heads=h, seq=s, head_dim=d,
+                          dtype=_lib.dtype_code(v0.dtype), src=_addr(arrays[0]), dst=_addr(arrays[1]),
+                          keep=_addr(kp), kept_idx=_addr(ki), n_kept=_addr(nk), importance=_addr(imp),
+                          centroids=_addr(cent), survivor=_addr(surv), workspace=_addr(ws),
+                          workspace_bytes=ws_bytes)
+    with torch.cuda.device(dev):
+        try:
+            st = lib.nq_merge_values(ctypes.byref(desc), ctypes.c_void_p(_lib.current_stream_handle(dev)))
+        finally:
+            staged.release()
+    _lib.check(st, "nq_merge_values")
+    return out, cent, surv
+
+
 def gather_rows(tensors: Sequence[torch.Tensor], *, gather: Optional[torch.Tensor] = None,
                 keep: Optional[torch.Tensor] = None) -> List[torch.Tensor]:
     """fp16 passthrough of same-shaped tensors: gathered rows or zeroed evicted rows."""

@@ -154,7 +154,7 @@ class NexusQuantEvict:
     convention follow NexusQuantEvict (pipeline.py:535-668, 1050-1244).  Evicted
     rows are zeroed inside the fused quantizer (mask eviction).  soft_eviction
     quantizes evicted rows at levels 2 instead (two launches into the same
-    outputs); merge_eviction is not part of this build's hot path and raises.
+    outputs); merge_eviction folds evicted values into their nearest survivors first.
     """
 
     def __init__(self, head_dim: int = 128, bits: int = 2, key_bits: int = None, value_bits: int = None,
@@ -368,16 +368,26 @@ class NexusQuantEvict:
             for i, li in enumerate(layers):
                 set_layer_kv(past_key_values, li, k_out[i], v_out[i])
 
+    def _merge(self, past_key_values, n_layers: int, seq: int, keep, kept_idx, n_kept, importance) -> None:
+        """Merge eviction (pipeline.py:961-1048): the values of every layer whose
+        seq equals the mask's are replaced by nq_merge_values' merged copies."""
+        from .ops import merge_values
+        layers = [li for li in range(n_layers) if get_layer_kv(past_key_values, li)[1].shape[2] == seq]
+        if not layers:
+            return
+        merged, _, _ = merge_values([get_layer_kv(past_key_values, li)[1] for li in layers], keep, kept_idx,
+                                    n_kept, importance)
+        for li, mv in zip(layers, merged):
+            set_layer_kv(past_key_values, li, get_layer_kv(past_key_values, li)[0], mv)
+
     def compress(self, past_key_values, model=None, input_ids=None):
         """Evict + quantize in place; returns (cache, prefix_attention_mask [b, s] float)."""
-        if self.merge_eviction:
-            raise NotImplementedError("merge_eviction is not part of the gfx950 hot path")
         n = num_layers(past_key_values)
         importance, k_score = self._importance(past_key_values, n, model, input_ids)
         b, _, seq, _ = k_score.shape
         device = k_score.device
         rate = self._resolve_rate(importance, seq)
-        keep, _, _ = self._keep(importance, seq, rate)
+        keep, kept_idx, n_kept = self._keep(importance, seq, rate)
         prefix_attention_mask = keep.float()
         skip = self._skip_layers(past_key_values, n)
         if self.min_context_for_compression > 0 and seq < self.min_context_for_compression:
@@ -386,6 +396,8 @@ class NexusQuantEvict:
             # every position stays visible; evicted rows are only coarser (pipeline.py:1129-1183)
             self._apply(past_key_values, n, skip, keep=keep, soft=True)
             return past_key_values, torch.ones(b, seq, dtype=torch.float32, device=device)
+        if self.merge_eviction:
+            self._merge(past_key_values, n, seq, keep, kept_idx, n_kept, importance)
         self._apply(past_key_values, n, skip, keep=keep)
         return past_key_values, prefix_attention_mask
 

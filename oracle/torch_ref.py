@@ -24,6 +24,8 @@ Pinning (see tests/test_oracle_*.py):
   score_real_from_qk      golden fixtures written through transformers' eager
                           attention (third-party formula, transformers 5.15.0)
   delta_encode/decode     closed form + lossless round trip
+  merge_eviction_values   golden fixture (reference NexusQuantEvict with
+                          merge_eviction=True: survivors, merged values, outputs)
   vllm_* (page caller)    golden fixtures written by the reference's
                           integrations/vllm_backend.py (compress / decompress /
                           logits / nibble packing / paged forward)
@@ -486,6 +488,79 @@ def evict_mask_compress(cache, key_levels: int, value_levels: int, rate: float,
         v_out = v_out * m4.half()
         set_layer_kv(cache, li, k_out, v_out)
     return cache, mask_out
+
+
+def merge_centroids(value_layers: Sequence[torch.Tensor], bi: int) -> Optional[torch.Tensor]:
+    """Mean over heads, averaged over layers, of batch row bi (pipeline.py:997-1013)."""
+    centroid_sum = None
+    count = 0
+    for v_l in value_layers:
+        v_mean = v_l[bi].float().mean(dim=0)
+        centroid_sum = v_mean if centroid_sum is None else centroid_sum + v_mean
+        count += 1
+    return None if centroid_sum is None else centroid_sum / count
+
+
+def merge_survivors(centroids: torch.Tensor, keep_row: torch.Tensor):
+    """(evicted positions, kept positions, survivor kept-list index per evicted,
+    cosine matrix) (pipeline.py:983-1024)."""
+    evict_pos = (~keep_row).nonzero(as_tuple=True)[0]
+    kept_pos = keep_row.nonzero(as_tuple=True)[0]
+    e_n = F.normalize(centroids[evict_pos], dim=-1)
+    k_n = F.normalize(centroids[kept_pos], dim=-1)
+    cos = torch.mm(e_n, k_n.t())
+    return evict_pos, kept_pos, cos.argmax(dim=1), cos
+
+
+def merge_eviction_values(value_layers: Sequence[torch.Tensor], keep: torch.Tensor, importance: torch.Tensor,
+                          survivors: Optional[Sequence[torch.Tensor]] = None) -> List[torch.Tensor]:
+    """MergingPress-style value merging (pipeline.py:961-1048) over the layers
+    whose seq equals the mask's; returns new value tensors.  `survivors[bi]`
+    (kept-list index per evicted position) overrides the cosine argmax."""
+    out = [v.clone() for v in value_layers]
+    b = keep.shape[0]
+    for bi in range(b):
+        km = keep[bi]
+        imp = importance[bi]
+        evict_pos = (~km).nonzero(as_tuple=True)[0]
+        kept_pos = km.nonzero(as_tuple=True)[0]
+        if evict_pos.numel() == 0 or kept_pos.numel() == 0:
+            continue
+        cent = merge_centroids(out, bi)
+        if survivors is None:
+            _, _, nearest, _ = merge_survivors(cent, km)
+        else:
+            nearest = survivors[bi]
+        for li, v_l in enumerate(out):
+            v = v_l[bi].float()
+            for ei, e_pos in enumerate(evict_pos):
+                s_pos = kept_pos[nearest[ei].item()]
+                imp_e = imp[e_pos].item()
+                imp_s = imp[s_pos].item()
+                w = imp_e / (imp_s + imp_e + 1e-8)
+                v[:, s_pos, :] = v[:, s_pos, :] + w * v[:, e_pos, :]
+            new_v = v_l.clone()
+            new_v[bi] = v.to(dtype=v_l.dtype)
+            out[li] = new_v
+    return out
+
+
+def evict_merge_compress(cache, key_levels: int, value_levels: int, rate: float, sliding_window: int = 32,
+                         obs_window: int = 32, rope_base: float = 10000.0, importance=None,
+                         skip_layers: Sequence[int] = ()):
+    """NexusQuantEvict.compress with merge_eviction=True (pipeline.py:1184-1244)."""
+    n = num_layers(cache)
+    k0, _ = get_layer_kv(cache, 0)
+    seq = k0.shape[2]
+    if importance is None:
+        importance = score_keykey(k0.float(), obs_window)
+    keep = build_keep_mask(importance, seq, rate, sliding_window)
+    layers = [li for li in range(n) if get_layer_kv(cache, li)[1].shape[2] == seq]
+    merged = merge_eviction_values([get_layer_kv(cache, li)[1] for li in layers], keep, importance)
+    for li, mv in zip(layers, merged):
+        set_layer_kv(cache, li, get_layer_kv(cache, li)[0], mv)
+    return evict_mask_compress(cache, key_levels, value_levels, rate, sliding_window, obs_window, rope_base,
+                               importance=importance, skip_layers=skip_layers)
 
 
 def evict_soft_compress(cache, key_levels: int, value_levels: int, rate: float,

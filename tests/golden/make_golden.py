@@ -8,7 +8,7 @@ torch.topk keep masks, and the real-attention scorer through transformers'
 eager attention.  Nothing under /root/reference is copied; only the numbers it
 produces are stored, as small .npz files next to this script.
 
-Usage:  python tests/golden/make_golden.py [/root/reference [evict_soft | vllm_pages]]
+Usage:  python tests/golden/make_golden.py [/root/reference [evict_soft | vllm_pages | evict_merge]]
 """
 
 from __future__ import annotations
@@ -189,6 +189,40 @@ def make_soft():
          k_out=torch.stack(c.key_cache), v_out=torch.stack(c.value_cache))
 
 
+def make_merge():
+    """10. Merge eviction (pipeline.py:961-1048): b = 2, 3 layers fp16, K3V2 at rate
+    0.5, first/last layer protected; the merged values, survivors and outputs."""
+    import torch.nn.functional as F
+    ks, vs = synth_kv(101, 3, 2, 2, 96, 64, 10000.0, sink=True)
+    nq = NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.5, sliding_window=8, rope_base=10000.0,
+                         merge_eviction=True, protect_boundary=1)
+    imp = nq._score_importance(ks[0].float())
+    keep = nq._build_keep_mask(imp, 96, eviction_rate=0.5)
+    survivors = []
+    cent_all = []
+    for bi in range(2):
+        cs = None
+        for v in vs:
+            m = v[bi].float().mean(dim=0)
+            cs = m if cs is None else cs + m
+        cent = cs / len(vs)
+        cent_all.append(cent)
+        ev = (~keep[bi]).nonzero(as_tuple=True)[0]
+        kp = keep[bi].nonzero(as_tuple=True)[0]
+        cos = torch.mm(F.normalize(cent[ev], dim=-1), F.normalize(cent[kp], dim=-1).t())
+        sv = torch.full((96,), -1, dtype=torch.int32)
+        sv[ev] = kp[cos.argmax(dim=1)].to(torch.int32)
+        survivors.append(sv)
+    c = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+    nq._apply_merge_eviction(c, keep, imp, 3)
+    merged = torch.stack(c.value_cache)
+    c2 = ListCache([k.clone() for k in ks], [v.clone() for v in vs])
+    _, mask = nq.compress(c2)
+    save("evict_merge", k_in=torch.stack(ks), v_in=torch.stack(vs), importance=imp, keep=keep,
+         centroids=torch.stack(cent_all), survivor=torch.stack(survivors), v_merged=merged, mask=mask,
+         k_out=torch.stack(c2.key_cache), v_out=torch.stack(c2.value_cache))
+
+
 def make_vllm():
     """9. vLLM page caller and decode consumer (integrations/vllm_backend.py):
     compress_page / decompress_page / decompress_for_attention at bits 2, 3, 4
@@ -251,7 +285,10 @@ if __name__ == "__main__":
         make_soft()
     elif sys.argv[2:] == ["vllm_pages"]:
         make_vllm()
+    elif sys.argv[2:] == ["evict_merge"]:
+        make_merge()
     else:
         main()
         make_soft()
         make_vllm()
+        make_merge()

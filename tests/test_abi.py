@@ -37,7 +37,8 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 
 @pytest.mark.parametrize("cname,pystruct", [("nq_quant_desc", _lib.QuantDesc), ("nq_codes_desc", _lib.CodesDesc),
-                                            ("nq_page_desc", _lib.PageDesc), ("nq_attn_desc", _lib.AttnDesc)])
+                                            ("nq_page_desc", _lib.PageDesc), ("nq_attn_desc", _lib.AttnDesc),
+                                            ("nq_merge_desc", _lib.MergeDesc)])
 def test_struct_layout_matches_the_c_compiler(tmp_path, cname, pystruct):
     """ctypes offsets of every descriptor field equal gcc's offsetof on the header."""
     fields = [f[0] for f in pystruct._fields_]

@@ -71,12 +71,17 @@ def test_truncate_batch_gt1_error_message_matches_reference():
         nq.NexusQuantEvictTruncate().compress(Cache())
 
 
-def test_merge_eviction_is_refused():
+def test_merge_eviction_needs_the_device_path():
+    # merge eviction is built; like every path it refuses host tensors
+    from nexusquant_amd._lib import NexusQuantError
+
     class Cache:
         key_cache = [torch.zeros(1, 1, 4, 128)]
         value_cache = [torch.zeros(1, 1, 4, 128)]
-    with pytest.raises(NotImplementedError):
-        nq.NexusQuantEvict(merge_eviction=True).compress(Cache())
+    comp = nq.NexusQuantEvict(merge_eviction=True)
+    assert comp.merge_eviction
+    with pytest.raises(NexusQuantError):
+        comp.compress(Cache())
 
 
 def test_presets_match_reference_table():
