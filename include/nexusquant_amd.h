@@ -254,6 +254,37 @@ int64_t nq_merge_workspace(int32_t batch, int32_t seq, int32_t head_dim);
 int nq_merge_values(const nq_merge_desc* desc, void* stream);
 
 /*
+ * Chunked rANS coding of int8 lattice codes c = 2p (|c| <= levels).  The coder
+ * is the reference's: 32-bit state in [2^16, 2^32), 16-bit renormalisation,
+ * frequencies summing to 4096, symbols s = c + levels (alphabet 2 levels + 1)
+ * when half-integer points occur (has_half), else s = c/2 + levels/2 (alphabet
+ * levels + 1).  The n codes are cut into chunks of `chunk` symbols, each coded
+ * on its own from the initial state, so chunk k's words equal the reference
+ * encoder's output for that chunk's symbols.
+ *   nq_rans_histogram: hist[2 levels + 1] += counts of c + levels (uint32,
+ *     caller-zeroed); codes 16-byte aligned.
+ *   nq_rans_encode: per chunk, words right-aligned in scratch
+ *     (nq_rans_scratch_words(n, chunk) uint16), their counts in n_words
+ *     [n_chunks], and offset [n_chunks + 1] = exclusive scan of the counts.
+ *   nq_rans_compact: words[offset[k] ..] = chunk k's words.
+ *   nq_rans_decode: codes from the compacted words and offsets.
+ * freq: uint16 [alphabet], summing to 4096, nonzero for every symbol present.
+ *
+ * Replaces: _build_freq_table / _rans_encode / _rans_decode use in
+ *           encode_e8 / decode_e8   entropy_coder.py:163-345, 376-484
+ *           (the reference codes one sequential stream on the host)
+ */
+int nq_rans_histogram(const int8_t* codes, int64_t n, int32_t levels, uint32_t* hist, void* stream);
+int64_t nq_rans_scratch_words(int64_t n, int32_t chunk);
+int nq_rans_encode(const int8_t* codes, int64_t n, int32_t levels, int32_t has_half, const uint16_t* freq,
+                   int32_t alphabet, int32_t chunk, uint16_t* scratch, uint32_t* n_words, uint64_t* offset,
+                   void* stream);
+int nq_rans_compact(const uint16_t* scratch, const uint32_t* n_words, const uint64_t* offset, int64_t n,
+                    int32_t chunk, uint16_t* words, void* stream);
+int nq_rans_decode(const uint16_t* words, const uint64_t* offset, int64_t n, int32_t levels, int32_t has_half,
+                   const uint16_t* freq, int32_t alphabet, int32_t chunk, int8_t* codes, void* stream);
+
+/*
  * Pages of the vLLM compressor: n_pages pages of identical geometry
  * [heads, tokens, head_dim] (head_dim 64, 128 or 256), keys or values, at
  * `levels` 4, 8 or 16 (bits 2, 3, 4).  The format is the reference's

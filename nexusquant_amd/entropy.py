@@ -1,0 +1,217 @@
+"""GPU rANS entropy stage for lattice codes (nexusquant/core/entropy_coder.py).
+
+The codes (int8 c = 2p of the relaxed-E8 points, as nq_codes_to_int8 and the
+page encoder write them) are histogrammed, coded and decoded on the device by
+nq_rans_* (nq_rans.hip).  The coder is the reference's 32-bit / 16-bit-word
+rANS with 12-bit probabilities; the stream is cut into chunks that are coded
+independently (one lane each), so each chunk's words equal the reference
+encoder's output for that chunk.  The frequency table follows the reference's
+normalisation rule exactly (build_freq_table), computed on the host from the
+device histogram (at most 33 entries).
+
+NQR1 container (little endian):
+    b"NQR1", u16 version = 1, u8 levels, u8 has_half, u16 alphabet, u16 pad,
+    u64 n_symbols, u32 chunk, u32 n_chunks, u16 freq[alphabet] (padded to 4 bytes),
+    u64 offsets[n_chunks + 1] (in 16-bit words), u16 words[offsets[-1]],
+    then an optional fp32 scale section: u64 n_scales, f32 scales[n_scales].
+The reference's encode_e8 writes one stream with fp16 scales; NQR1 keeps the
+fp32 scales (lossless) and the chunk offsets that make decoding parallel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import struct
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from .ops import _addr
+
+PROB_BITS = 12
+M = 1 << PROB_BITS
+DEFAULT_CHUNK = 4096
+_MAGIC = b"NQR1"
+
+
+def build_freq_table(counts: np.ndarray) -> np.ndarray:
+    """Frequencies summing to 4096 from symbol counts, by the reference's rule
+    (entropy_coder.py:175-243): every seen symbol gets 1, the rest is shared in
+    proportion to the counts (floored), leftovers go to the largest fractional
+    parts, an excess is taken back from the rarest symbols."""
+    counts = np.asarray(counts, dtype=np.int64)
+    alphabet = len(counts)
+    total = counts.sum()
+    if total == 0:
+        freqs = np.ones(alphabet, dtype=np.int64) * (M // alphabet)
+        freqs[0] += M - freqs.sum()
+    else:
+        seen = counts > 0
+        n_seen = int(seen.sum())
+        freqs = np.zeros(alphabet, dtype=np.int64)
+        freqs[seen] = 1
+        remaining = M - n_seen
+        if remaining > 0:
+            prop = (counts[seen].astype(np.float64) / total) * remaining
+            extra = np.floor(prop).astype(np.int64)
+            freqs[seen] += extra
+            diff = int(M - freqs.sum())
+            seen_idx = np.where(seen)[0]
+            if diff > 0:
+                order = seen_idx[np.argsort(-(prop - extra))]
+                for i in range(diff):
+                    freqs[order[i % len(order)]] += 1
+            elif diff < 0:
+                order = seen_idx[np.argsort(counts[seen])]
+                removed = 0
+                for idx in order:
+                    while freqs[idx] > 1 and removed < -diff:
+                        freqs[idx] -= 1
+                        removed += 1
+                    if removed >= -diff:
+                        break
+        elif remaining < 0:
+            seen_idx = np.where(seen)[0]
+            order = seen_idx[np.argsort(-counts[seen])]
+            freqs[:] = 0
+            for i in range(min(M, len(order))):
+                freqs[order[i]] = 1
+    if freqs.sum() != M:
+        raise AssertionError(f"frequency table sums to {freqs.sum()}, not {M}")
+    return freqs.astype(np.uint16)
+
+
+@dataclasses.dataclass
+class RansStream:
+    """Device-resident chunked rANS stream of n int8 codes."""
+    words: torch.Tensor     # int16 view of the uint16 words
+    offsets: torch.Tensor   # int64 [n_chunks + 1]
+    freq: np.ndarray        # uint16 [alphabet]
+    levels: int
+    has_half: bool
+    n: int
+    chunk: int
+    shape: tuple
+
+    @property
+    def alphabet(self) -> int:
+        return len(self.freq)
+
+    def nbytes(self) -> int:
+        """Coded size: words, chunk offsets and the frequency table."""
+        return 2 * self.words.numel() + 8 * self.offsets.numel() + 2 * self.alphabet
+
+
+def _stream(dev) -> ctypes.c_void_p:
+    return ctypes.c_void_p(_lib.current_stream_handle(dev))
+
+
+def rans_encode(codes: torch.Tensor, levels: int, chunk: int = DEFAULT_CHUNK) -> RansStream:
+    """rANS-code int8 codes c = 2p (|c| <= levels) on the device."""
+    lib = _lib.load()
+    _lib.require_device(codes, "codes")
+    if codes.dtype != torch.int8:
+        raise TypeError(f"codes must be int8 (2p), got {codes.dtype}")
+    if levels not in (2, 4, 8, 16):
+        raise ValueError(f"levels must be 2, 4, 8 or 16, got {levels}")
+    dev = codes.device
+    flat = codes.contiguous().reshape(-1)
+    if flat.data_ptr() % 16:
+        flat = flat.clone()
+    n = flat.numel()
+    hist = torch.zeros(2 * levels + 1, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.nq_rans_histogram(_addr(flat), n, levels, _addr(hist), _stream(dev)), "nq_rans_histogram")
+    h = hist.cpu().numpy().astype(np.int64)
+    has_half = bool(h[1::2].sum() > 0) if levels > 0 else False
+    # odd bins hold the half-integer codes (c + L odd <=> c odd for even L)
+    counts = h if has_half else h[0::2]
+    freq = build_freq_table(counts)
+    alphabet = len(freq)
+    n_chunks = (n + chunk - 1) // chunk
+    freq_d = torch.from_numpy(freq.view(np.int16).copy()).to(dev)
+    scratch = torch.empty(max(int(lib.nq_rans_scratch_words(n, chunk)), 1), dtype=torch.int16, device=dev)
+    n_words = torch.empty(max(n_chunks, 1), dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_chunks + 1, dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.nq_rans_encode(_addr(flat), n, levels, int(has_half), _addr(freq_d), alphabet, chunk,
+                                      _addr(scratch), _addr(n_words), _addr(offsets), _stream(dev)),
+                   "nq_rans_encode")
+        total = int(offsets[-1].item())
+        words = torch.empty(max(total, 1), dtype=torch.int16, device=dev)
+        _lib.check(lib.nq_rans_compact(_addr(scratch), _addr(n_words), _addr(offsets), n, chunk, _addr(words),
+                                       _stream(dev)), "nq_rans_compact")
+    return RansStream(words=words[:total], offsets=offsets, freq=freq, levels=levels, has_half=has_half, n=n,
+                      chunk=chunk, shape=tuple(codes.shape))
+
+
+def rans_decode(stream: RansStream, device=None) -> torch.Tensor:
+    """int8 codes of a RansStream, in its original shape."""
+    lib = _lib.load()
+    dev = stream.words.device if device is None else torch.device(device)
+    out = torch.empty(stream.n, dtype=torch.int8, device=dev)
+    if stream.n:
+        words = stream.words.to(dev)
+        if words.numel() == 0:
+            words = torch.zeros(1, dtype=torch.int16, device=dev)
+        offsets = stream.offsets.to(dev)
+        freq_d = torch.from_numpy(stream.freq.view(np.int16).copy()).to(dev)
+        with torch.cuda.device(dev):
+            _lib.check(lib.nq_rans_decode(_addr(words), _addr(offsets), stream.n, stream.levels, int(stream.has_half),
+                                          _addr(freq_d), stream.alphabet, stream.chunk, _addr(out), _stream(dev)),
+                       "nq_rans_decode")
+    return out.reshape(stream.shape)
+
+
+def pack_nqr1(stream: RansStream, scales: Optional[torch.Tensor] = None) -> bytes:
+    """NQR1 bytes of a stream (and optional fp32 scales)."""
+    freq = stream.freq.astype("<u2").tobytes()
+    freq += b"\0" * ((-len(freq)) % 4)
+    n_chunks = stream.offsets.numel() - 1
+    head = _MAGIC + struct.pack("<HBBHHQII", 1, stream.levels, int(stream.has_half), stream.alphabet, 0,
+                                stream.n, stream.chunk, n_chunks)
+    body = stream.offsets.cpu().numpy().astype("<u8").tobytes() + stream.words.cpu().numpy().view("<u2").tobytes()
+    tail = b""
+    if scales is not None:
+        sc = scales.detach().float().cpu().numpy().reshape(-1).astype("<f4")
+        tail = struct.pack("<Q", sc.size) + sc.tobytes()
+    return head + freq + body + tail
+
+
+def unpack_nqr1(blob: bytes, shape=None, device="cuda"):
+    """(RansStream on `device`, fp32 scales or None) from NQR1 bytes."""
+    if blob[:4] != _MAGIC:
+        raise ValueError("not an NQR1 stream")
+    version, levels, has_half, alphabet, _, n, chunk, n_chunks = struct.unpack_from("<HBBHHQII", blob, 4)
+    if version != 1:
+        raise ValueError(f"NQR1 version {version} unsupported")
+    at = 4 + struct.calcsize("<HBBHHQII")
+    freq = np.frombuffer(blob, dtype="<u2", count=alphabet, offset=at).astype(np.uint16)
+    at += 2 * alphabet + ((-2 * alphabet) % 4)
+    offsets = np.frombuffer(blob, dtype="<u8", count=n_chunks + 1, offset=at).astype(np.int64)
+    at += 8 * (n_chunks + 1)
+    n_words = int(offsets[-1])
+    words = np.frombuffer(blob, dtype="<u2", count=n_words, offset=at).view(np.int16)
+    at += 2 * n_words
+    scales = None
+    if at < len(blob):
+        (ns,) = struct.unpack_from("<Q", blob, at)
+        scales = torch.from_numpy(np.frombuffer(blob, dtype="<f4", count=ns, offset=at + 8).copy())
+    dev = torch.device(device)
+    stream = RansStream(words=torch.from_numpy(words.copy()).to(dev), offsets=torch.from_numpy(offsets.copy()).to(dev),
+                        freq=freq, levels=levels, has_half=bool(has_half), n=n, chunk=chunk,
+                        shape=tuple(shape) if shape is not None else (n,))
+    return stream, scales
+
+
+def shannon_bits(counts: np.ndarray) -> float:
+    """Total Shannon information of a symbol histogram, in bits."""
+    c = np.asarray(counts, dtype=np.float64)
+    c = c[c > 0]
+    if c.size == 0:
+        return 0.0
+    p = c / c.sum()
+    return float(-(c * np.log2(p)).sum())

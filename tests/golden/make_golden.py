@@ -8,7 +8,7 @@ torch.topk keep masks, and the real-attention scorer through transformers'
 eager attention.  Nothing under /root/reference is copied; only the numbers it
 produces are stored, as small .npz files next to this script.
 
-Usage:  python tests/golden/make_golden.py [/root/reference [evict_soft | vllm_pages | evict_merge]]
+Usage:  python tests/golden/make_golden.py [/root/reference [evict_soft | vllm_pages | evict_merge | rans]]
 """
 
 from __future__ import annotations
@@ -223,6 +223,39 @@ def make_merge():
          k_out=torch.stack(c2.key_cache), v_out=torch.stack(c2.value_cache))
 
 
+def make_rans():
+    """11. rANS entropy coder (core/entropy_coder.py): symbol mapping, frequency
+    table and the encoder's 16-bit word stream for E8 code streams at levels
+    4, 8, 16, an integer-only stream, a skewed stream and a one-symbol stream."""
+    from nexusquant.core import entropy_coder as ec
+    from nexusquant.core.e8_lattice import E8Lattice
+    g = torch.Generator().manual_seed(111)
+    out = {}
+    cases = []
+    for L, n_rows in ((8, 96), (4, 64), (16, 48)):
+        x = torch.randn(n_rows, 128, generator=g)
+        amax = x.abs().amax(dim=-1, keepdim=True).clamp(min=1e-8)
+        p = E8Lattice.nearest_point((x / (amax / (L / 2))).reshape(-1, 8)).clamp(-L / 2, L / 2)
+        cases.append((f"l{L}", L, p.reshape(-1).numpy()))
+    ints = torch.randint(-3, 4, (5000,), generator=g).float()
+    cases.append(("int", 8, ints.numpy()))
+    skew = torch.zeros(20000)
+    skew[torch.randint(0, 20000, (37,), generator=g)] = 2.5
+    skew[torch.randint(0, 20000, (5,), generator=g)] = -3.5
+    cases.append(("skew", 8, skew.numpy()))
+    cases.append(("one", 4, np.array([1.5], np.float32)))
+    for tag, L, pts in cases:
+        sym, has_half, alpha = ec._lattice_to_symbols(pts.astype(np.float32), L)
+        freqs, cum = ec._build_freq_table(sym, alpha)
+        words = ec._rans_encode(sym, freqs, cum)
+        back = ec._rans_decode(words, len(sym), freqs, cum, alpha)
+        assert np.array_equal(back, sym)
+        out.update({f"{tag}_points": pts.astype(np.float32), f"{tag}_levels": L, f"{tag}_symbols": sym,
+                    f"{tag}_has_half": int(has_half), f"{tag}_alphabet": alpha, f"{tag}_freqs": freqs,
+                    f"{tag}_words": np.array(words, dtype=np.uint16)})
+    save("rans", **out)
+
+
 def make_vllm():
     """9. vLLM page caller and decode consumer (integrations/vllm_backend.py):
     compress_page / decompress_page / decompress_for_attention at bits 2, 3, 4
@@ -287,8 +320,11 @@ if __name__ == "__main__":
         make_vllm()
     elif sys.argv[2:] == ["evict_merge"]:
         make_merge()
+    elif sys.argv[2:] == ["rans"]:
+        make_rans()
     else:
         main()
         make_soft()
         make_vllm()
         make_merge()
+        make_rans()
