@@ -195,9 +195,64 @@ def aux_workload(name, steps, warmup):
                    gbs_fp16_compressed=round(2 * elems / (step_ms * 1e-3) / 1e9, 1))
     elif name in ("decode70b", "decode7b"):
         out.update(decode_workload(name, steps, warmup))
+    elif name == "rans":
+        out.update(rans_workload(steps, warmup))
+    elif name == "merge":
+        ks, vs = _aux_cache(torch, gen, dev, 32, 4, 8, 8192, 128, 10000.0, True)
+        comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.25, sliding_window=32,
+                                  obs_window=32, rope_base=10000.0, merge_eviction=True)
+        from nexusquant_amd.ops import keep_mask, merge_values
+        imp = comp._score_importance(ks[0])
+        keep, kept, n_kept = keep_mask(imp, 0.25, 32)
+        merge_ms = _timed(torch, lambda: merge_values(vs, keep, kept, n_kept, imp), steps, warmup) * 1e3
+        step_ms = _timed(torch, lambda: comp.compress(Cache(ks, vs)), steps, warmup) * 1e3
+        v_bytes = 32 * 4 * 8 * 8192 * 128 * 2
+        out.update(config={"workload": "merge eviction, C3 shape: 32 layers x K,V fp16 [4, 8, 8192, 128], "
+                           "25% eviction, K3V2"},
+                   ms_per_step=round(step_ms, 3), value=round(step_ms, 3), merge_ms=round(merge_ms, 3),
+                   merge_value_gbs=round(2 * v_bytes / (merge_ms * 1e-3) / 1e9, 1))
     else:
         raise SystemExit(f"unknown workload {name}")
     print(json.dumps(out), flush=True)
+
+
+def rans_workload(steps, warmup):
+    """rANS stage on one C2 layer's key codes (K3: levels 8; 8 x 131072 x 128 int8
+    codes): histogram + encode + compact, and decode, both on the device.  The CPU
+    leg times the restated reference coder (oracle/rans_ref.py, the reference's
+    own algorithm in pure Python) on a 50 000-symbol sample."""
+    import numpy as np
+    import torch
+    from nexusquant_amd.codec import codes_int8
+    from nexusquant_amd.entropy import rans_decode, rans_encode, shannon_bits
+    from nexusquant_amd.ops import quantize_tensors
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(1, 8, 131072, 128, device=dev, generator=gen).to(torch.bfloat16)
+    _, cd = quantize_tensors([x], is_key=False, levels=8, recon=False, codes=True)
+    codes = codes_int8(cd)[0].reshape(-1)
+    n = codes.numel()
+    holder = {}
+    enc_ms = _timed(torch, lambda: holder.__setitem__("st", rans_encode(codes, 8)), steps, warmup) * 1e3
+    st = holder["st"]
+    dec_ms = _timed(torch, lambda: rans_decode(st), steps, warmup) * 1e3
+    assert torch.equal(rans_decode(st), codes.reshape(st.shape))
+    c = codes.cpu().numpy()
+    sym = c.astype(np.int64) + 8 if st.has_half else c.astype(np.int64) // 2 + 4
+    counts = np.bincount(sym, minlength=st.alphabet)
+    bps = 16.0 * st.words.numel() / n
+    from oracle import rans_ref
+    sample = sym[:50000]
+    t0 = time.perf_counter()
+    rans_ref.rans_encode(sample, st.freq)
+    cpu_s = time.perf_counter() - t0
+    return dict(config={"workload": f"rANS of {n} int8 K3 codes (one Llama-3-70B layer's keys, 131072 tokens)"},
+                ms_per_step=round(enc_ms + dec_ms, 3), value=round(enc_ms + dec_ms, 3),
+                encode_ms=round(enc_ms, 3), decode_ms=round(dec_ms, 3),
+                encode_gsym_s=round(n / (enc_ms * 1e-3) / 1e9, 2), decode_gsym_s=round(n / (dec_ms * 1e-3) / 1e9, 2),
+                bits_per_symbol=round(bps, 4), shannon_bits_per_symbol=round(shannon_bits(counts) / n, 4),
+                cpu_baseline={"value": round(len(sample) / cpu_s / 1e6, 4), "unit": "Msymbols/s", "cores": 1,
+                              "kind": "port", "sample": "restated reference encoder, 50000 symbols"})
 
 
 def decode_workload(name, steps, warmup):
@@ -278,7 +333,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="c2",
                     help="c2 (headline, default), a secondary config: c3, c4, c5a, c5b, aux (all four), "
-                         "decode70b / decode7b (paged decode attention from compressed pages), "
+                         "decode70b / decode7b (paged decode attention from compressed pages), rans (GPU "
+                         "entropy stage), merge (merge eviction), "
                          "or copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.workload != "c2":

@@ -43,6 +43,43 @@ __device__ __forceinline__ void store_elem(void* p, size_t i, float v) {
     }
 }
 
+// 8 consecutive elements <-> fp32 (16-byte loads for fp16 / bf16, 2 x 16 for fp32)
+template <int DT>
+__device__ __forceinline__ void load8_elem(const void* p, size_t i, float (&x)[8]) {
+    if constexpr (DT == NQ_F32) {
+        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i + 4);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+        const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if constexpr (DT == NQ_BF16) {
+                x[2 * k] = bf16_bits_to_f32(ws[k] & 0xffffu);
+                x[2 * k + 1] = bf16_bits_to_f32(ws[k] >> 16);
+            } else {
+                x[2 * k] = f16_bits_to_f32(ws[k] & 0xffffu);
+                x[2 * k + 1] = f16_bits_to_f32(ws[k] >> 16);
+            }
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void copy8_elem(const void* src, void* dst, size_t i) {
+    if constexpr (DT == NQ_F32) {
+        reinterpret_cast<float4*>(static_cast<float*>(dst) + i)[0] =
+            reinterpret_cast<const float4*>(static_cast<const float*>(src) + i)[0];
+        reinterpret_cast<float4*>(static_cast<float*>(dst) + i + 4)[0] =
+            reinterpret_cast<const float4*>(static_cast<const float*>(src) + i + 4)[0];
+    } else {
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(dst) + i) =
+            *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + i);
+    }
+}
+
 __global__ __launch_bounds__(256) void nq_fill_i32(int32_t* p, int64_t n, int32_t v) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = v;
@@ -78,31 +115,44 @@ struct MergeLayout {
     }
 };
 
-// 1. centroids [b, s, d]
+// 1. centroids [b, s, d]; a thread owns 8 consecutive coordinates
 template <int DT>
 __global__ __launch_bounds__(256) void merge_centroid_kernel(const uint64_t* src, int n_layers, int b, int h,
                                                              int s, int d, float* cent) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t i8 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
     const size_t total = (size_t)b * s * d;
-    if (i >= total) return;
-    const int j = (int)(i % d);
-    const size_t bt = i / d;
+    if (i8 >= total) return;
+    const int j = (int)(i8 % d);
+    const size_t bt = i8 / d;
     const int t = (int)(bt % s);
     const int bi = (int)(bt / s);
-    float acc = 0.0f;
+    float acc[8];
     for (int l = 0; l < n_layers; ++l) {
         const void* v = reinterpret_cast<const void*>(src[l]);
-        float sum = 0.0f;
+        float sum[8];
         for (int h0 = 0; h0 < h; h0 += 16) {
-            float run = 0.0f;
+            float run[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
             const int h1 = h0 + 16 < h ? h0 + 16 : h;
-            for (int hh = h0; hh < h1; ++hh) run += load_elem<DT>(v, (((size_t)bi * h + hh) * s + t) * d + j);
-            sum = h0 == 0 ? run : sum + run;
+            for (int hh = h0; hh < h1; ++hh) {
+                float x[8];
+                load8_elem<DT>(v, (((size_t)bi * h + hh) * s + t) * d + j, x);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) run[k] += x[k];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sum[k] = h0 == 0 ? run[k] : sum[k] + run[k];
         }
-        const float mean = sum / (float)h;
-        acc = l == 0 ? mean : acc + mean;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float mean = sum[k] / (float)h;
+            acc[k] = l == 0 ? mean : acc[k] + mean;
+        }
     }
-    cent[i] = acc / (float)n_layers;
+    float4* o = reinterpret_cast<float4*>(cent + i8);
+    o[0] = make_float4(acc[0] / (float)n_layers, acc[1] / (float)n_layers, acc[2] / (float)n_layers,
+                       acc[3] / (float)n_layers);
+    o[1] = make_float4(acc[4] / (float)n_layers, acc[5] / (float)n_layers, acc[6] / (float)n_layers,
+                       acc[7] / (float)n_layers);
 }
 
 // 2. unit vectors, one wave per row
@@ -365,8 +415,8 @@ __global__ __launch_bounds__(1024) void merge_list_kernel(ListArgs a) {
     }
 }
 
-// 5. merged rows: one wave per (layer, row, head, token); lanes stride the
-//    coordinates.  Every row is written (copied unless it is a survivor).
+// 5. merged rows: D/8 lanes per (layer, row, head, token), 8 coordinates per
+//    lane.  Every row is written (copied unless it is a survivor with merges).
 struct ApplyArgs {
     const uint64_t* src;
     const uint64_t* dst;
@@ -382,31 +432,39 @@ struct ApplyArgs {
 
 template <int DT>
 __global__ __launch_bounds__(256) void merge_apply_kernel(ApplyArgs a) {
-    const uint64_t r = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lanes_per_row = a.d / 8;
+    const uint64_t r = ((uint64_t)blockIdx.x * 256 + threadIdx.x) / lanes_per_row;
     if (r >= a.rows) return;
-    const int lane = threadIdx.x & 63;
+    const int j = (int)(((uint64_t)blockIdx.x * 256 + threadIdx.x) % lanes_per_row) * 8;
     const int t = (int)(r % a.s);
     const uint64_t bh = (r / a.s) % ((uint64_t)a.b * a.h);
     const int layer = (int)(r / a.s / ((uint64_t)a.b * a.h));
     const int bi = (int)(bh / a.h);
     const void* src = reinterpret_cast<const void*>(a.src[layer]);
     void* dst = reinterpret_cast<void*>(a.dst[layer]);
-    const size_t row_off = (bh * a.s + t) * (size_t)a.d;
+    const size_t row_off = (bh * a.s + t) * (size_t)a.d + j;
     const size_t rb = (size_t)bi * a.s;
     const int kl = a.kept_local[rb + t];
     const int beg = kl >= 0 ? a.offset[rb + kl] : 0;
     const int end = kl >= 0 ? a.count[rb + kl] : 0;
-    const size_t head_base = bh * a.s * (size_t)a.d;
-    for (int j = lane; j < a.d; j += 64) {
-        float v = load_elem<DT>(src, row_off + j);
-        for (int i = beg; i < end; ++i) {
-            const int e = a.list[rb + i];
-            const int pe = a.ev_idx[rb + e];
-            const float x = load_elem<DT>(src, head_base + (size_t)pe * a.d + j);
-            v = v + a.weight[rb + e] * x;  // two roundings, as the reference's separate ops
-        }
-        store_elem<DT>(dst, row_off + j, v);
+    if (end <= beg) {
+        copy8_elem<DT>(src, dst, row_off);
+        return;
     }
+    const size_t head_base = bh * a.s * (size_t)a.d + j;
+    float v[8];
+    load8_elem<DT>(src, row_off, v);
+    for (int i = beg; i < end; ++i) {
+        const int e = a.list[rb + i];
+        const int pe = a.ev_idx[rb + e];
+        const float w = a.weight[rb + e];
+        float x[8];
+        load8_elem<DT>(src, head_base + (size_t)pe * a.d, x);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = v[k] + w * x[k];  // two roundings, as the reference's separate ops
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) store_elem<DT>(dst, row_off + k, v[k]);
 }
 
 }  // namespace nq
@@ -454,7 +512,7 @@ extern "C" int nq_merge_values(const nq_merge_desc* d, void* stream) {
     int32_t* kept_local = reinterpret_cast<int32_t*>(w + L.kept_local);
     hipStream_t st = (hipStream_t)stream;
 
-    const int64_t n_el = bs * D;
+    const int64_t n_el = bs * D / 8;  // 8 coordinates per thread
 #define NQ_CENT(DT)                                                                                           \
     hipLaunchKernelGGL(merge_centroid_kernel<DT>, dim3((uint32_t)((n_el + 255) / 256)), dim3(256), 0, st, d->src, \
                        d->n_tensors, b, h, s, D, cent)
@@ -532,8 +590,9 @@ extern "C" int nq_merge_values(const nq_merge_desc* d, void* stream) {
     ap.s = s;
     ap.d = D;
     ap.rows = (uint64_t)d->n_tensors * b * h * s;
-    NQ_CHECK_ARG((ap.rows + 3) / 4 < (1ull << 31), "nq_merge_values: too many rows");
-    const dim3 g((uint32_t)((ap.rows + 3) / 4));
+    const uint64_t threads = ap.rows * (uint64_t)(D / 8);
+    NQ_CHECK_ARG((threads + 255) / 256 < (1ull << 31), "nq_merge_values: too many rows");
+    const dim3 g((uint32_t)((threads + 255) / 256));
     if (d->dtype == NQ_F16) hipLaunchKernelGGL(merge_apply_kernel<NQ_F16>, g, dim3(256), 0, st, ap);
     else if (d->dtype == NQ_BF16) hipLaunchKernelGGL(merge_apply_kernel<NQ_BF16>, g, dim3(256), 0, st, ap);
     else hipLaunchKernelGGL(merge_apply_kernel<NQ_F32>, g, dim3(256), 0, st, ap);

@@ -366,6 +366,7 @@ def merge_values(values: Sequence[torch.Tensor], keep: torch.Tensor, kept_idx: t
         raise ValueError("keep, kept_idx and importance must be [batch, seq]")
     dev = v0.device
     src = [v.contiguous() for v in values]
+    src = [v if v.data_ptr() % 16 == 0 else v.clone() for v in src]  # 16-byte vector accesses
     out = list(torch.empty(len(src), b, h, s, d, dtype=v0.dtype, device=dev).unbind(0))
     kp = keep.to(device=dev, dtype=torch.uint8).contiguous()
     ki = kept_idx.to(device=dev, dtype=torch.int32).contiguous()
