@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define NQ_ABI_VERSION 3
+#define NQ_ABI_VERSION 4
 
 /* status codes */
 #define NQ_OK 0
@@ -61,8 +61,8 @@ extern "C" {
  * RoPE tables are fp32 [rope_n_pos, head_dim/2]; keys use row position
  * src (inverse) and t (forward).  For power-of-two head dims the kernel
  * folds the rotation into the top Hadamard stage, whose pairs (i, i + d/2)
- * are the RoPE pairs; it then needs fl(cos - sin) and fl(cos + sin), which it
- * reads from rope_cos_minus_sin / rope_cos_plus_sin when given (same layout)
+ * are the RoPE pairs; it then needs fl(sin - cos) and fl(cos + sin), which it
+ * reads from rope_sin_minus_cos / rope_cos_plus_sin when given (same layout)
  * and otherwise forms from rope_cos / rope_sin.  Either way the results are
  * identical; the precomputed tables save two operations per pair.
  *
@@ -97,7 +97,7 @@ typedef struct nq_quant_desc {
     int64_t rope_n_pos;
     float hadamard_scale;   /* h_D of the reference's Sylvester matrix */
     float reserved_f;
-    const float* rope_cos_minus_sin;  /* optional, [rope_n_pos, head_dim/2]; NULL: formed in-kernel */
+    const float* rope_sin_minus_cos;  /* optional, [rope_n_pos, head_dim/2]; NULL: formed in-kernel */
     const float* rope_cos_plus_sin;
 } nq_quant_desc;
 
@@ -183,7 +183,7 @@ typedef struct nq_codes_desc {
     int64_t rope_n_pos;
     float hadamard_scale;
     float reserved_f;
-    const float* rope_cos_minus_sin;  /* optional, as in nq_quant_desc */
+    const float* rope_sin_minus_cos;  /* optional, as in nq_quant_desc */
     const float* rope_cos_plus_sin;
 } nq_codes_desc;
 
@@ -308,7 +308,7 @@ typedef struct nq_page_desc {
     const uint64_t* out;       /* decode: fp16 [heads, tokens, head_dim] per page */
     const float* rope_cos;     /* fp32 [rope_n_pos, head_dim/2], keys */
     const float* rope_sin;
-    const float* rope_cos_minus_sin;  /* optional fl(cos - sin) / fl(cos + sin) */
+    const float* rope_sin_minus_cos;  /* optional fl(sin - cos) / fl(cos + sin) */
     const float* rope_cos_plus_sin;
     int64_t rope_n_pos;        /* positions must lie in [0, rope_n_pos) */
     float hadamard_scale;
@@ -403,7 +403,7 @@ typedef struct nq_attn_desc {
     const int32_t* row_chunks;
     const float* rope_cos;
     const float* rope_sin;
-    const float* rope_cos_minus_sin;  /* optional, as in nq_page_desc */
+    const float* rope_sin_minus_cos;  /* optional, as in nq_page_desc */
     const float* rope_cos_plus_sin;
     int64_t rope_n_pos;
     float hadamard_scale;

@@ -14,7 +14,7 @@ from .build import LIB_PATH
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
 NQ_KEEP_ZERO, NQ_KEEP_WRITE_KEPT, NQ_KEEP_WRITE_EVICTED = 0, 1, 2
-ABI_VERSION = 3  # NQ_ABI_VERSION of the header these bindings mirror
+ABI_VERSION = 4  # NQ_ABI_VERSION of the header these bindings mirror
 _P = ctypes.c_void_p
 
 
@@ -30,7 +30,7 @@ class QuantDesc(ctypes.Structure):
         ("gather", _P), ("keep", _P), ("rope_cos", _P), ("rope_sin", _P),
         ("rope_n_pos", ctypes.c_int64),
         ("hadamard_scale", ctypes.c_float), ("reserved_f", ctypes.c_float),
-        ("rope_cos_minus_sin", _P), ("rope_cos_plus_sin", _P),
+        ("rope_sin_minus_cos", _P), ("rope_cos_plus_sin", _P),
     ]
 
 
@@ -44,7 +44,7 @@ class CodesDesc(ctypes.Structure):
         ("syms", _P), ("cosets", _P), ("scales", _P), ("out", _P),
         ("rope_cos", _P), ("rope_sin", _P), ("rope_n_pos", ctypes.c_int64),
         ("hadamard_scale", ctypes.c_float), ("reserved_f", ctypes.c_float),
-        ("rope_cos_minus_sin", _P), ("rope_cos_plus_sin", _P),
+        ("rope_sin_minus_cos", _P), ("rope_cos_plus_sin", _P),
     ]
 
 
@@ -66,7 +66,7 @@ class PageDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32), ("levels", ctypes.c_int32), ("is_key", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
         ("src", _P), ("positions", _P), ("codes", _P), ("scales", _P), ("out", _P),
-        ("rope_cos", _P), ("rope_sin", _P), ("rope_cos_minus_sin", _P), ("rope_cos_plus_sin", _P),
+        ("rope_cos", _P), ("rope_sin", _P), ("rope_sin_minus_cos", _P), ("rope_cos_plus_sin", _P),
         ("rope_n_pos", ctypes.c_int64),
         ("hadamard_scale", ctypes.c_float), ("reserved_f", ctypes.c_float),
     ]
@@ -79,7 +79,7 @@ class AttnDesc(ctypes.Structure):
         ("head_dim", ctypes.c_int32), ("q_dtype", ctypes.c_int32), ("n_chunks", ctypes.c_int32),
         ("query", _P), ("out", _P), ("units", _P),
         ("chunk_units", _P), ("chunk_row", _P), ("chunk_tokens", _P), ("row_chunks", _P),
-        ("rope_cos", _P), ("rope_sin", _P), ("rope_cos_minus_sin", _P), ("rope_cos_plus_sin", _P),
+        ("rope_cos", _P), ("rope_sin", _P), ("rope_sin_minus_cos", _P), ("rope_cos_plus_sin", _P),
         ("rope_n_pos", ctypes.c_int64),
         ("hadamard_scale", ctypes.c_float), ("scale_divisor", ctypes.c_float),
         ("workspace", _P), ("workspace_bytes", ctypes.c_int64),

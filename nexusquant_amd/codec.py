@@ -48,7 +48,7 @@ def _codes_desc(codes: Sequence[PackedCodes], outs: Sequence[torch.Tensor], rope
                           levels=c0.levels, is_key=int(rope is not None), syms=_addr(arrays[0]),
                           cosets=_addr(arrays[1]), scales=_addr(arrays[2]), out=_addr(arrays[3]),
                           rope_cos=_addr(cos), rope_sin=_addr(sin), rope_n_pos=n_pos,
-                          rope_cos_minus_sin=_addr(dm), rope_cos_plus_sin=_addr(dp),
+                          rope_sin_minus_cos=_addr(dm), rope_cos_plus_sin=_addr(dp),
                           hadamard_scale=hadamard_constant(c0.padded_dim))
     return desc, staged
 

@@ -491,8 +491,8 @@ extern "C" int nq_paged_attention(const nq_attn_desc* d, void* stream) {
                      "nq_paged_attention: chunk plan arrays are required");
         NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos > 0 && d->rope_n_pos < (1ll << 31),
                      "nq_paged_attention: keys need RoPE tables");
-        NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
-                     "nq_paged_attention: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
+        NQ_CHECK_ARG((d->rope_sin_minus_cos == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                     "nq_paged_attention: give both or neither of rope_sin_minus_cos / rope_cos_plus_sin");
         const int64_t need = nq_paged_attention_workspace(d->n_chunks, d->q_heads, d->head_dim);
         NQ_CHECK_ARG(d->workspace != nullptr && d->workspace_bytes >= need,
                      "nq_paged_attention: workspace of %lld bytes needed", (long long)need);
@@ -511,7 +511,7 @@ extern "C" int nq_paged_attention(const nq_attn_desc* d, void* stream) {
     a.part = static_cast<float*>(d->workspace);
     a.rope_cos = d->rope_cos;
     a.rope_sin = d->rope_sin;
-    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dm = d->rope_sin_minus_cos;
     a.rope_dp = d->rope_cos_plus_sin;
     a.q_heads = (uint32_t)d->q_heads;
     a.kv_heads = (uint32_t)d->kv_heads;

@@ -262,9 +262,9 @@ static int run_codec(const nq_codes_desc* d, int kind, void* stream) {
     NQ_CHECK_ARG(d->syms && d->cosets && d->scales && d->out, "nq codes: NULL pointer array");
     if (kind == 0 && d->is_key) {
         NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos >= d->seq, "nq_dequantize: RoPE table too short");
-        NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
-                     "nq_dequantize: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
-        NQ_CHECK_ARG(d->rope_cos_minus_sin == nullptr || d->head_dim != 96,
+        NQ_CHECK_ARG((d->rope_sin_minus_cos == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                     "nq_dequantize: give both or neither of rope_sin_minus_cos / rope_cos_plus_sin");
+        NQ_CHECK_ARG(d->rope_sin_minus_cos == nullptr || d->head_dim != 96,
                      "nq_dequantize: head_dim 96 keys take cos / sin tables only");
     }
     const uint64_t rows = (uint64_t)d->batch * d->heads * d->seq;
@@ -276,7 +276,7 @@ static int run_codec(const nq_codes_desc* d, int kind, void* stream) {
     a.out = d->out;
     a.rope_cos = d->rope_cos;
     a.rope_sin = d->rope_sin;
-    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dm = d->rope_sin_minus_cos;
     a.rope_dp = d->rope_cos_plus_sin;
     a.heads = (uint32_t)d->heads;
     a.seq = (uint32_t)d->seq;

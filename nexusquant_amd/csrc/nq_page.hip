@@ -204,8 +204,8 @@ extern "C" int nq_page_decode(const nq_page_desc* d, void* stream) {
     NQ_CHECK_ARG(rows < (1ull << 31), "nq_page_decode: %llu rows per page exceeds 2^31",
                  (unsigned long long)rows);
     if (rows == 0) return NQ_OK;
-    NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
-                 "nq_page_decode: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
+    NQ_CHECK_ARG((d->rope_sin_minus_cos == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                 "nq_page_decode: give both or neither of rope_sin_minus_cos / rope_cos_plus_sin");
     if (d->is_key) {
         NQ_CHECK_ARG(d->positions != nullptr, "nq_page_decode: keys need positions");
         NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos > 0 && d->rope_n_pos < (1ll << 31),
@@ -220,7 +220,7 @@ extern "C" int nq_page_decode(const nq_page_desc* d, void* stream) {
     a.out = d->out;
     a.rope_cos = d->rope_cos;
     a.rope_sin = d->rope_sin;
-    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dm = d->rope_sin_minus_cos;
     a.rope_dp = d->rope_cos_plus_sin;
     a.rows = (uint32_t)rows;
     a.tokens = (uint32_t)d->tokens;
@@ -256,15 +256,15 @@ extern "C" int nq_page_logits(const nq_page_desc* d, const void* query, int32_t 
                  "nq_page_logits: codes, scales, positions, query and logits are required");
     NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos > 0 && d->rope_n_pos < (1ll << 31),
                  "nq_page_logits: keys need RoPE tables");
-    NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
-                 "nq_page_logits: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
+    NQ_CHECK_ARG((d->rope_sin_minus_cos == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                 "nq_page_logits: give both or neither of rope_sin_minus_cos / rope_cos_plus_sin");
     PageArgs a = {};
     a.codes = d->codes;
     a.scales = d->scales;
     a.positions = d->positions;
     a.rope_cos = d->rope_cos;
     a.rope_sin = d->rope_sin;
-    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dm = d->rope_sin_minus_cos;
     a.rope_dp = d->rope_cos_plus_sin;
     a.rows = (uint32_t)rows;
     a.tokens = (uint32_t)d->tokens;

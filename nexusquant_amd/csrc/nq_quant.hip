@@ -29,7 +29,7 @@ struct QuantArgs {
     const uint8_t* keep;
     const float* rope_cos;
     const float* rope_sin;
-    const float* rope_dm;   // optional fl(cos - sin) / fl(cos + sin) tables
+    const float* rope_dm;   // optional fl(sin - cos) / fl(cos + sin) tables
     const float* rope_dp;
     uint32_t heads, seq_in, seq_out, rows;
     uint32_t n_tensors, bh, work, per_xcd;  // work items = ceil(seq_out/64) * bh * n_tensors
@@ -355,7 +355,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     // Keys with DR == D: inverse RoPE and the top Hadamard stage in one step
     // (their pairs coincide); the other stages follow in fwht_row.
     constexpr bool MERGED = IS_KEY && DR == D;
-    float cs[RC][8], sn[RC][8];  // cos / sin, or fl(cos - sin) / fl(cos + sin) when MERGED
+    float cs[RC][8], sn[RC][8];  // cos / sin, or fl(sin - cos) / fl(cos + sin) when MERGED
     if constexpr (MERGED) {
         load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, pos_in, q, cs, sn);
         rope_stage_merged<C>(x, cs, sn);
@@ -529,7 +529,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     }
 
     if constexpr (MERGED) {
-        // the top inverse Hadamard stage and forward RoPE in one step
+        // the top inverse Hadamard stage and forward RoPE in one step.  The tables
+        // stay live through the quantizer: reloading them here cuts 8 VGPRs but
+        // not the occupancy, and the extra loads cost more than they save.
         if (a.gather && t_out != t_in)
             load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, t_out, q, cs, sn);
         rope_stage_merged<C>(x, cs, sn);
@@ -623,9 +625,9 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     const uint64_t rows = (uint64_t)d->batch * d->heads * d->seq_out;
     NQ_CHECK_ARG(rows < (1ull << 31), "nq_quantize: %llu rows per tensor exceeds 2^31", (unsigned long long)rows);
     if (rows == 0) return NQ_OK;
-    NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
-                 "nq_quantize: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
-    NQ_CHECK_ARG(d->rope_cos_minus_sin == nullptr || d->head_dim != 96,
+    NQ_CHECK_ARG((d->rope_sin_minus_cos == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                 "nq_quantize: give both or neither of rope_sin_minus_cos / rope_cos_plus_sin");
+    NQ_CHECK_ARG(d->rope_sin_minus_cos == nullptr || d->head_dim != 96,
                  "nq_quantize: head_dim 96 keys take cos / sin tables only");
     if (d->is_key) {
         NQ_CHECK_ARG(d->rope_cos && d->rope_sin, "nq_quantize: keys need RoPE tables");
@@ -643,7 +645,7 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     a.keep = d->keep;
     a.rope_cos = d->rope_cos;
     a.rope_sin = d->rope_sin;
-    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dm = d->rope_sin_minus_cos;
     a.rope_dp = d->rope_cos_plus_sin;
     a.heads = (uint32_t)d->heads;
     a.seq_in = (uint32_t)d->seq_in;
@@ -717,8 +719,8 @@ extern "C" int nq_page_encode(const nq_page_desc* d, void* stream) {
     NQ_CHECK_ARG(rows < (1ull << 31), "nq_page_encode: %llu rows per page exceeds 2^31",
                  (unsigned long long)rows);
     if (rows == 0) return NQ_OK;
-    NQ_CHECK_ARG((d->rope_cos_minus_sin == nullptr) == (d->rope_cos_plus_sin == nullptr),
-                 "nq_page_encode: give both or neither of rope_cos_minus_sin / rope_cos_plus_sin");
+    NQ_CHECK_ARG((d->rope_sin_minus_cos == nullptr) == (d->rope_cos_plus_sin == nullptr),
+                 "nq_page_encode: give both or neither of rope_sin_minus_cos / rope_cos_plus_sin");
     if (d->is_key) {
         NQ_CHECK_ARG(d->positions != nullptr, "nq_page_encode: keys need positions");
         NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos > 0 && d->rope_n_pos < (1ll << 31),
@@ -728,7 +730,7 @@ extern "C" int nq_page_encode(const nq_page_desc* d, void* stream) {
     a.src = d->src;
     a.rope_cos = d->rope_cos;
     a.rope_sin = d->rope_sin;
-    a.rope_dm = d->rope_cos_minus_sin;
+    a.rope_dm = d->rope_sin_minus_cos;
     a.rope_dp = d->rope_cos_plus_sin;
     a.heads = 1u;  // a page's (head, token) rows are one flat run of rows
     a.seq_in = a.seq_out = (uint32_t)rows;

@@ -262,6 +262,9 @@ __device__ __forceinline__ void apply_rope(float (&x)[D / 32][8], int q, const f
 // on the input side (inverse RoPE, then the stage), and the same map on the
 // output side (the inverse stage, then forward RoPE).  With dm = fl(c - s)
 // and dp = fl(c + s):  lo' = fma(lo, dm, fl(hi dp)), hi' = fma(lo, dp, -fl(hi dm)).
+// The tables hold nm = fl(s - c) = -dm instead, so both products need no
+// negated operand: lo' = fma(-lo, nm, fl(hi dp)), hi' = fma(lo, dp, fl(hi nm)),
+// the same numbers (negation is exact).
 
 template <int D>
 __device__ __forceinline__ void load_rope_merged(const float* cos_t, const float* sin_t, const float* dm_t,
@@ -283,7 +286,7 @@ __device__ __forceinline__ void load_rope_merged(const float* cos_t, const float
             load8f(sin_t + base + 32 * c + 8 * q, sn);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                dm[c][i] = cs[i] - sn[i];
+                dm[c][i] = sn[i] - cs[i];  // fl(s - c)
                 dp[c][i] = cs[i] + sn[i];
             }
         }
@@ -298,8 +301,8 @@ __device__ __forceinline__ void rope_stage_merged(float (&x)[C][8], const float 
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float lo = x[c][i], hi = x[c + C / 2][i];
-            x[c][i] = __builtin_fmaf(lo, dm[c][i], hi * dp[c][i]);
-            x[c + C / 2][i] = __builtin_fmaf(lo, dp[c][i], -(hi * dm[c][i]));
+            x[c][i] = __builtin_fmaf(-lo, dm[c][i], hi * dp[c][i]);  // dm holds fl(s - c)
+            x[c + C / 2][i] = __builtin_fmaf(lo, dp[c][i], hi * dm[c][i]);
         }
     }
 }

@@ -260,7 +260,7 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
         cosets=_addr(arrays["cosets"]), scales=_addr(arrays["scales"]),
         gather=_addr(g), keep=_addr(k), rope_cos=_addr(cos), rope_sin=_addr(sin),
         rope_n_pos=n_pos, hadamard_scale=hadamard_constant(D),
-        rope_cos_minus_sin=_addr(dm), rope_cos_plus_sin=_addr(dp))
+        rope_sin_minus_cos=_addr(dm), rope_cos_plus_sin=_addr(dp))
     with torch.cuda.device(dev):
         try:
             if launch_events is not None:

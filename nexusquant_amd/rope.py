@@ -83,7 +83,7 @@ def device_table(n_pos: int, head_dim: int, base: float, rope_scaling: Optional[
 
 def device_merged_table(n_pos: int, head_dim: int, base: float, rope_scaling: Optional[dict],
                         device) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Cached device fl(cos - sin), fl(cos + sin) [>= n_pos, head_dim/2] (fp32, built on the
+    """Cached device fl(sin - cos), fl(cos + sin) [>= n_pos, head_dim/2] (fp32, built on the
     host from host_table).  The fused kernels fold RoPE into the top Hadamard stage
     with these; they are the same numbers the kernels would form from cos and sin."""
     device = torch.device(device)
@@ -94,7 +94,7 @@ def device_merged_table(n_pos: int, head_dim: int, base: float, rope_scaling: Op
             return hit
         n = max(_ROUND, -(-n_pos // _ROUND) * _ROUND)
         c, s = host_table(n, head_dim, base, rope_scaling)
-        tab = ((c - s).to(device), (c + s).to(device))
+        tab = ((s - c).to(device), (c + s).to(device))
         _cache[key] = tab
         return tab
 

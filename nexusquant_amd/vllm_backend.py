@@ -145,7 +145,7 @@ class NexusQuantKVCompressor:
             levels=self.levels, is_key=int(is_key), src=_addr(arrays.get("src")),
             positions=_addr(arrays.get("positions")), codes=_addr(arrays.get("codes")),
             scales=_addr(arrays.get("scales")), out=_addr(arrays.get("out")),
-            rope_cos=_addr(cos), rope_sin=_addr(sin), rope_cos_minus_sin=_addr(dm), rope_cos_plus_sin=_addr(dp),
+            rope_cos=_addr(cos), rope_sin=_addr(sin), rope_sin_minus_cos=_addr(dm), rope_cos_plus_sin=_addr(dp),
             rope_n_pos=n_pos, hadamard_scale=hadamard_constant(self.head_dim))
 
     # ------------------------------------------------------------- public API
@@ -567,7 +567,7 @@ class NexusQuantPagedAttention:
             n_chunks=plan.n_chunks, query=_addr(q), out=_addr(out), units=at("units"),
             chunk_units=at("chunk_units"),
             chunk_row=at("chunk_row"), chunk_tokens=at("chunk_tokens"), row_chunks=at("row_chunks"),
-            rope_cos=_addr(cos), rope_sin=_addr(sin), rope_cos_minus_sin=_addr(dm), rope_cos_plus_sin=_addr(dp),
+            rope_cos=_addr(cos), rope_sin=_addr(sin), rope_sin_minus_cos=_addr(dm), rope_cos_plus_sin=_addr(dp),
             rope_n_pos=n_pos, hadamard_scale=hadamard_constant(d),
             scale_divisor=float(np.float32(math.sqrt(d))), workspace=_addr(workspace), workspace_bytes=ws_bytes)
         with torch.cuda.device(dev):

@@ -79,7 +79,7 @@ def _subsample_rows(x_np, heads, toks):
 
 @pytest.mark.parametrize("D,L", [(128, 8), (64, 4), (256, 2), (128, 16)])
 def test_merged_rope_tables_match_in_kernel_tables(D, L):
-    # precomputed fl(cos - sin) / fl(cos + sin) tables and the ones the kernel
+    # precomputed fl(sin - cos) / fl(cos + sin) tables and the ones the kernel
     # forms from cos / sin give identical outputs
     print(f"[gpu] merged tables D={D} L={L}", flush=True)
     x = _inputs((1, 2, 130, D), torch.bfloat16, seed=D + L).to(DEV)
