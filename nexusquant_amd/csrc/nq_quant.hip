@@ -19,30 +19,49 @@
 
 namespace nq {
 
-struct QuantArgs {
+// Per-tensor device address tables (n_tensors entries each; null when the
+// output is not written).  The kernel takes them as __restrict__ arguments so
+// that, being read-only, their entries load into scalar registers inside the
+// sub-item loop.
+struct QuantTables {
     const uint64_t* src;
     const uint64_t* recon;
     const uint64_t* syms;
     const uint64_t* cosets;
     const uint64_t* scales;
+    const uint64_t* positions;  // pages: per tensor int32 [page_tokens] (keys)
+    const uint64_t* codes8;     // pages: per tensor int8 [rows, D]: 2p
+    const uint64_t* scales16;   // pages: per tensor fp16 [rows]
+};
+
+struct QuantArgs {
     const int32_t* gather;
     const uint8_t* keep;
     const float* rope_cos;
     const float* rope_sin;
     const float* rope_dm;   // optional fl(sin - cos) / fl(cos + sin) tables
     const float* rope_dp;
-    uint32_t heads, seq_in, seq_out, rows;
-    uint32_t n_tensors, bh, work, per_xcd;  // work items = ceil(seq_out/64) * bh * n_tensors
+    uint32_t heads, seq_in, seq_out, n_tensors;
+    uint32_t batch, hn, group, n_groups;    // hn = heads * n_tensors sub-items per batch row, in groups
+    uint32_t work, per_xcd;                 // work items = ceil(seq_out/64) * batch * n_groups
     float hscale;
     int32_t keep_mode;                      // NQ_KEEP_*
     // page encoding (PAGE instantiations only): rows are a page's (head, token)
     // rows flattened, token = row % page_tokens; keys rotate at positions[token]
-    const uint64_t* positions;  // per tensor int32 [page_tokens] (keys)
-    const uint64_t* codes8;     // per tensor int8 [rows, D]: 2p
-    const uint64_t* scales16;   // per tensor fp16 [rows]
     uint32_t page_tokens;
     uint32_t rope_n_pos;
 };
+
+#define NQ_GLOBAL __attribute__((address_space(1)))
+
+// A device address as a pointer the compiler knows to be global memory (it is
+// made in the global address space, then cast to a generic pointer, which
+// address-space inference folds back): accesses through it compile to global
+// rather than flat instructions, and stores count on vmcnt only.
+template <class T>
+__device__ __forceinline__ T* gptr(uint64_t addr) {
+    return (T*)(NQ_GLOBAL T*)addr;
+}
 
 // ------------------------------------------------------------------ E8 ----
 
@@ -269,7 +288,8 @@ __device__ __forceinline__ void store_group_words(uint8_t* dst, const uint32_t (
         } else {
 #pragma unroll
             for (int c = 0; c < C; c += 4)
-                *reinterpret_cast<uint2*>(dst + 2 * c) = make_uint2(w[c] | (w[c + 1] << 16), w[c + 2] | (w[c + 3] << 16));
+                *reinterpret_cast<uint2*>(dst + 2 * c) =
+                    make_uint2(w[c] | (w[c + 1] << 16), w[c + 2] | (w[c + 3] << 16));
         }
     } else {
         static_assert(B == 3, "3-byte groups");
@@ -293,74 +313,51 @@ __device__ __forceinline__ void store_group_words(uint8_t* dst, const uint32_t (
 
 // -------------------------------------------------------------- kernel ----
 
-template <int D, int L, bool IS_KEY, int DT, int DR, bool PAGE = false>
-__global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
-    static_assert(!PAGE || DR == D, "page encoding takes power-of-two head dims");
+// Staging of a sub-item's source rows through LDS.  A wave's 16 rows arrive as
+// NSEG direct-to-LDS loads of 16 bytes per lane (segment s of the wave holds
+// lane l's bytes at 16 l), issued one sub-item ahead so that the HBM reads of
+// the next rows overlap the arithmetic on the current ones without holding
+// VGPRs.  Blocks whose staging would exceed 32 KB (fp32 rows of 256) load
+// straight into registers instead.
+template <int D, int DR, int DT>
+struct RowStaging {
+    static constexpr int in_bytes = DT == NQ_F32 ? 4 : 2;
+    static constexpr int chunks = (DR + 31) / 32;   // chunks that hold source data
+    static constexpr int parts = in_bytes / 2;      // 16-byte pieces per chunk
+    static constexpr int nseg = chunks * parts;     // loads per lane per sub-item
+    static constexpr bool pipe = 4 * nseg * 1024 <= 32768;
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+// One sub-item's outputs (null when not written).
+struct RowOut {
+    uint16_t* recon;
+    uint8_t* syms;
+    uint8_t* cosets;
+    float* scales;
+    int8_t* codes8;
+    uint16_t* scales16;
+};
+
+// The row computation of one sub-item: x holds the source row (zero padded,
+// zeroed for evicted rows); cs / sn the source position's RoPE rows for keys.
+// With a gather list, keys load the output position's RoPE rows into cs / sn
+// before the forward rotation.
+template <int D, int L, bool IS_KEY, int DR, bool PAGE>
+__device__ __forceinline__ void quant_row_body(const QuantArgs& a, float (&x)[D / 32][8],
+                                               float (&cs)[RopeChunks<D, DR>::value][8],
+                                               float (&sn)[RopeChunks<D, DR>::value][8], int q, const RowOut& o,
+                                               uint32_t bh, uint32_t t_in, uint32_t t_out, bool active) {
     constexpr int C = D / 32;
     constexpr int RC = RopeChunks<D, DR>::value;
-    const int q = threadIdx.x & 3;
-    // Block -> work item.  Consecutive block ids go round-robin to the 8 XCDs, so
-    // block 8k + x takes work item x * per_xcd + k: each XCD walks a contiguous
-    // range.  Work items are ordered (token tile, batch*head, tensor) with the
-    // tensor fastest, so the blocks that read one token tile's RoPE rows run back
-    // to back on one XCD and find them in its L2.  The whole block exits together.
-    const uint32_t w = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
-    if (w >= a.work) return;
-    const uint32_t tensor = w % a.n_tensors;
-    const uint32_t rest = w / a.n_tensors;
-    const uint32_t bh = rest % a.bh;
-    const uint32_t tile = rest / a.bh;
-    const uint32_t t_raw = tile * 64u + (threadIdx.x >> 2);
-    const bool in_range = t_raw < a.seq_out;
-    const uint32_t t_out = in_range ? t_raw : a.seq_out - 1u;  // idle quads recompute a valid row
-    const uint32_t b = bh / a.heads;
-    uint32_t t_in = t_out;
-    if (a.gather) {
-        // the host validates the list; clamp anyway so a bad index cannot read out of bounds
-        const int32_t gi = a.gather[(size_t)b * a.seq_out + t_out];
-        t_in = gi < 0 ? 0u : ((uint32_t)gi >= a.seq_in ? a.seq_in - 1u : (uint32_t)gi);
-    }
-    uint32_t pos_in = t_in;  // RoPE position of the source row
-    if constexpr (PAGE && IS_KEY) {
-        // the host validates positions against the table; clamp anyway so a bad
-        // position cannot read outside it
-        const int32_t pp = reinterpret_cast<const int32_t*>(a.positions[tensor])[t_in % a.page_tokens];
-        pos_in = pp < 0 ? 0u : ((uint32_t)pp >= a.rope_n_pos ? a.rope_n_pos - 1u : (uint32_t)pp);
-    }
-    bool keep = true;
-    if (a.keep) keep = a.keep[(size_t)b * a.seq_in + t_in] != 0;
-    // rows this launch writes: all, or (soft eviction) only the kept / only the evicted ones
-    const bool active = in_range && (a.keep_mode == NQ_KEEP_ZERO || keep == (a.keep_mode == NQ_KEEP_WRITE_KEPT));
-    if (a.keep_mode != NQ_KEEP_ZERO) keep = true;  // selected rows are quantized as they are
-
-    float x[C][8];
-    const void* src = reinterpret_cast<const void*>(a.src[tensor]);
-    const int64_t in_off = ((int64_t)bh * a.seq_in + t_in) * DR;
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        if (32 * c < DR) {
-            load8<DT>(src, in_off + 32 * c + 8 * q, x[c]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[c][i] = 0.0f;  // zero padding to D
-        }
-    }
-    if (!keep) {
-#pragma unroll
-        for (int c = 0; c < C; ++c)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[c][i] = 0.0f;
-    }
-
     // Keys with DR == D: inverse RoPE and the top Hadamard stage in one step
     // (their pairs coincide); the other stages follow in fwht_row.
     constexpr bool MERGED = IS_KEY && DR == D;
-    float cs[RC][8], sn[RC][8];  // cos / sin, or fl(sin - cos) / fl(cos + sin) when MERGED
     if constexpr (MERGED) {
-        load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, pos_in, q, cs, sn);
         rope_stage_merged<C>(x, cs, sn);
     } else if constexpr (IS_KEY) {
-        load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, pos_in, q, cs, sn);
         apply_rope<D, DR, RC, true>(x, q, cs, sn);
     }
 
@@ -403,21 +400,20 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     cbits |= dpp_u32<kQuadXor1>(cbits);
     cbits |= dpp_u32<kQuadXor2>(cbits);
     if (active && q == 0) {
-        if (a.cosets) {
-            uint8_t* cdst = reinterpret_cast<uint8_t*>(a.cosets[tensor]) + out_row * (D / 64);
+        if (o.cosets) {
+            uint8_t* cdst = o.cosets + out_row * (D / 64);
             if constexpr (D == 64) *cdst = (uint8_t)cbits;
             else if constexpr (D == 128) *reinterpret_cast<uint16_t*>(cdst) = (uint16_t)cbits;
             else *reinterpret_cast<uint32_t*>(cdst) = cbits;
         }
-        if (a.scales) reinterpret_cast<float*>(a.scales[tensor])[out_row] = scale;
+        if (o.scales) o.scales[out_row] = scale;
     }
     if constexpr (PAGE) {
         // int8 codes 2p and the fp16 row scale, the page format of the vLLM
         // compressor (vllm_backend.py:305-314, 366-373)
         if (!active) return;
-        if (q == 0 && a.scales16)
-            reinterpret_cast<uint16_t*>(a.scales16[tensor])[out_row] = (uint16_t)f32_to_f16_bits(scale);
-        int8_t* cdst = reinterpret_cast<int8_t*>(a.codes8[tensor]) + out_row * D;
+        if (q == 0 && o.scales16) o.scales16[out_row] = (uint16_t)f32_to_f16_bits(scale);
+        int8_t* cdst = o.codes8 + out_row * D;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
             const float off = coset[c] ? 0.5f : 0.0f;
@@ -453,14 +449,14 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) u[c][k] = pk_fma_clamp(pk_f16_bits(x[c][k], x[c][k + 4]), inv_l, off);
         }
-        if (a.syms && active) {
+        if (o.syms && active) {
             uint32_t wds[C];
 #pragma unroll
             for (int c = 0; c < C; ++c) wds[c] = group_symbols<L>(u[c]);
-            uint8_t* dst = reinterpret_cast<uint8_t*>(a.syms[tensor]) + out_row * ROW_BYTES + q * (C * B);
+            uint8_t* dst = o.syms + out_row * ROW_BYTES + q * (C * B);
             store_group_words<B, C>(dst, wds);
         }
-        if (!a.recon) return;
+        if (!o.recon) return;
         // Walsh-Hadamard of U in fp16 (exact: multiples of 1/(2L), |.| <= D).
         // S U = (S p)/L + (D/2) e_0, so every output but coordinate 0 (lane 0,
         // chunk 0, register 0 low half) is (S p)/L; that one is corrected by
@@ -495,14 +491,14 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) x[c][i] = __builtin_amdgcn_fmed3f(x[c][i] + off, -HL, HL);
         }
-        if (a.syms && active) {
+        if (o.syms && active) {
             int cs[C];
 #pragma unroll
             for (int c = 0; c < C; ++c) cs[c] = coset[c] ? 1 : 0;
-            uint8_t* dst = reinterpret_cast<uint8_t*>(a.syms[tensor]) + out_row * ROW_BYTES;
+            uint8_t* dst = o.syms + out_row * ROW_BYTES;
             store_symbols<L, C>(dst, q, x, cs);
         }
-        if (!a.recon) return;
+        if (!o.recon) return;
         constexpr bool EXACT_F16 = D * (L / 2) <= 1024;
         if constexpr (EXACT_F16) {
             half2v hp[C][4];
@@ -540,7 +536,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
         apply_rope<D, DR, RC, false>(x, q, cs, sn);
     }
     if (!active) return;
-    half2v* dst = reinterpret_cast<half2v*>(reinterpret_cast<uint16_t*>(a.recon[tensor]) + out_row * DR);
+    uint16_t* dst = o.recon + out_row * DR;
     // The fp32 result is rounded to fp16 in a second step, as the reference does
     // (fp32 tensor, then .half()).  The empty asm pins the fp32 value: without it
     // the backend folds fma + convert into v_fma_mix{lo,hi}_f16, which rounds
@@ -552,50 +548,201 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
 #pragma unroll
     for (int c = 0; c < C; ++c) {
         if (32 * c >= DR) continue;  // padding coordinates are not part of the output
-        half2v o[4];
+        half2v hv[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = half2v{(__fp16)x[c][2 * k], (__fp16)x[c][2 * k + 1]};
+        for (int k = 0; k < 4; ++k) hv[k] = half2v{(__fp16)x[c][2 * k], (__fp16)x[c][2 * k + 1]};
         uint4 w;
-        w.x = __builtin_bit_cast(uint32_t, o[0]);
-        w.y = __builtin_bit_cast(uint32_t, o[1]);
-        w.z = __builtin_bit_cast(uint32_t, o[2]);
-        w.w = __builtin_bit_cast(uint32_t, o[3]);
-        *reinterpret_cast<uint4*>(dst + (32 * c + 8 * q) / 2) = w;
+        w.x = __builtin_bit_cast(uint32_t, hv[0]);
+        w.y = __builtin_bit_cast(uint32_t, hv[1]);
+        w.z = __builtin_bit_cast(uint32_t, hv[2]);
+        w.w = __builtin_bit_cast(uint32_t, hv[3]);
+        *reinterpret_cast<uint4*>(dst + 32 * c + 8 * q) = w;
     }
     }  // !PAGE
 }
 
+// lgkmcnt(0) with the other counters left open (gfx9 s_waitcnt encoding)
+constexpr int kWaitLgkm0 = 0xc07f;
+
+template <int D, int L, bool IS_KEY, int DT, int DR, bool PAGE = false>
+__global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
+                                                         const uint64_t* __restrict__ tab_recon,
+                                                         const uint64_t* __restrict__ tab_syms,
+                                                         const uint64_t* __restrict__ tab_cosets,
+                                                         const uint64_t* __restrict__ tab_scales,
+                                                         const uint64_t* __restrict__ tab_positions,
+                                                         const uint64_t* __restrict__ tab_codes8,
+                                                         const uint64_t* __restrict__ tab_scales16) {
+    static_assert(!PAGE || DR == D, "page encoding takes power-of-two head dims");
+    constexpr int C = D / 32;
+    constexpr int RC = RopeChunks<D, DR>::value;
+    constexpr bool MERGED = IS_KEY && DR == D;
+    using ST = RowStaging<D, DR, DT>;
+    const int q = threadIdx.x & 3;
+    // Block -> work item.  Consecutive block ids go round-robin to the 8 XCDs, so
+    // block 8k + x takes work item x * per_xcd + k: each XCD walks a contiguous
+    // range.  A work item is one 64-token tile of one batch row and a group of
+    // sub-items j, the (head, tensor) pairs of that row with the tensor fastest,
+    // which every wave runs back to back for its 16 tokens.  Items are ordered
+    // (tile, batch, group) with the group fastest, so the blocks that read one
+    // tile's RoPE rows run back to back on one XCD and find them in its L2.  The
+    // whole block exits together.
+    const uint32_t w = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
+    if (w >= a.work) return;
+    const uint32_t grp = w % a.n_groups;
+    const uint32_t rest = w / a.n_groups;
+    const uint32_t b = rest % a.batch;
+    const uint32_t tile = rest / a.batch;
+    const uint32_t t_raw = tile * 64u + (threadIdx.x >> 2);
+    const bool in_range = t_raw < a.seq_out;
+    const uint32_t t_out = in_range ? t_raw : a.seq_out - 1u;  // idle quads recompute a valid row
+    uint32_t t_in = t_out;
+    if (a.gather) {
+        // the host validates the list; clamp anyway so a bad index cannot read out of bounds
+        const int32_t gi = a.gather[(size_t)b * a.seq_out + t_out];
+        t_in = gi < 0 ? 0u : ((uint32_t)gi >= a.seq_in ? a.seq_in - 1u : (uint32_t)gi);
+    }
+    bool keep = true;
+    if (a.keep) keep = a.keep[(size_t)b * a.seq_in + t_in] != 0;
+    // rows this launch writes: all, or (soft eviction) only the kept / only the evicted ones
+    const bool active = in_range && (a.keep_mode == NQ_KEEP_ZERO || keep == (a.keep_mode == NQ_KEEP_WRITE_KEPT));
+    if (a.keep_mode != NQ_KEEP_ZERO) keep = true;  // selected rows are quantized as they are
+    const uint32_t j0 = grp * a.group;
+    const uint32_t j1 = j0 + a.group < a.hn ? j0 + a.group : a.hn;
+
+    // Keys: the RoPE rows of the source position, loaded once for the work item
+    // unless each sub-item loads its own (a gather list reloads the output
+    // position's rows after the quantizer; pages rotate at per-page positions).
+    float cs[RC][8], sn[RC][8];  // cos / sin, or fl(sin - cos) / fl(cos + sin) when MERGED
+    auto load_tables = [&](uint32_t pos) {
+        if constexpr (MERGED) load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, pos, q, cs, sn);
+        else load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, pos, q, cs, sn);
+    };
+
+    auto row_elems = [&](uint32_t j) -> int64_t {  // element offset of this lane's first coordinate
+        const uint32_t bh = b * a.heads + j / a.n_tensors;
+        return ((int64_t)bh * a.seq_in + t_in) * DR + 8 * q;
+    };
+    __shared__ __attribute__((aligned(16))) uint8_t stage[ST::pipe ? 4 * ST::nseg * 1024 : 16];
+    uint8_t* wstage = stage + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * (ST::nseg * 1024);
+    const uint32_t lane = threadIdx.x & 63u;
+    auto stage_rows = [&](uint32_t j) {
+        const uint8_t* p = reinterpret_cast<const uint8_t*>(tab_src[j % a.n_tensors]) + row_elems(j) * ST::in_bytes;
+#pragma unroll
+        for (int c = 0; c < ST::chunks; ++c)
+#pragma unroll
+            for (int h = 0; h < ST::parts; ++h)
+                __builtin_amdgcn_global_load_lds((global_void_t*)(p + 32 * c * ST::in_bytes + 16 * h),
+                                                 (lds_void_t*)(wstage + (c * ST::parts + h) * 1024), 16, 0, 0);
+    };
+
+    if constexpr (IS_KEY && !PAGE) {
+        if (!a.gather) load_tables(t_in);
+    }
+    if constexpr (ST::pipe) stage_rows(j0);
+    for (uint32_t j = j0; j < j1; ++j) {
+        const uint32_t tensor = j % a.n_tensors;
+        const uint32_t bh = b * a.heads + j / a.n_tensors;
+        float x[C][8];
+        if constexpr (ST::pipe) {
+            uint4 raw[ST::nseg];
+#pragma unroll
+            for (int s = 0; s < ST::nseg; ++s) raw[s] = *reinterpret_cast<const uint4*>(wstage + s * 1024 + lane * 16);
+#pragma unroll
+            for (int c = 0; c < ST::chunks; ++c) cvt8<DT>(&raw[c * ST::parts], x[c]);
+            // the reads have landed before the next sub-item's loads overwrite the segments
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            if (j + 1 < j1) stage_rows(j + 1);
+        } else {
+            const void* src = reinterpret_cast<const void*>(tab_src[tensor]);
+            const int64_t off = row_elems(j);
+#pragma unroll
+            for (int c = 0; c < ST::chunks; ++c) load8<DT>(src, off + 32 * c, x[c]);
+        }
+#pragma unroll
+        for (int c = ST::chunks; c < C; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[c][i] = 0.0f;  // zero padding to D
+        if (!keep) {
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[c][i] = 0.0f;
+        }
+        if constexpr (IS_KEY && PAGE) {
+            // the host validates positions against the table; clamp anyway so a bad
+            // position cannot read outside it
+            const int32_t pp = gptr<const int32_t>(tab_positions[tensor])[t_in % a.page_tokens];
+            load_tables(pp < 0 ? 0u : ((uint32_t)pp >= a.rope_n_pos ? a.rope_n_pos - 1u : (uint32_t)pp));
+        } else if constexpr (IS_KEY) {
+            if (a.gather) load_tables(t_in);
+        }
+        RowOut o;
+        o.recon = tab_recon ? gptr<uint16_t>(tab_recon[tensor]) : nullptr;
+        o.syms = tab_syms ? gptr<uint8_t>(tab_syms[tensor]) : nullptr;
+        o.cosets = tab_cosets ? gptr<uint8_t>(tab_cosets[tensor]) : nullptr;
+        o.scales = tab_scales ? gptr<float>(tab_scales[tensor]) : nullptr;
+        if constexpr (PAGE) {
+            o.codes8 = gptr<int8_t>(tab_codes8[tensor]);
+            o.scales16 = tab_scales16 ? gptr<uint16_t>(tab_scales16[tensor]) : nullptr;
+        } else {
+            o.codes8 = nullptr;
+            o.scales16 = nullptr;
+        }
+        quant_row_body<D, L, IS_KEY, DR, PAGE>(a, x, cs, sn, q, o, bh, t_in, t_out, active);
+    }
+}
+
 // ---------------------------------------------------------------- host ----
 
-template <int D, int L, bool K, int DT, int DR>
-static hipError_t launch_quant(const QuantArgs& a, uint32_t n_tensors, hipStream_t s) {
-    (void)n_tensors;
-    dim3 grid(a.per_xcd * 8u);
-    hipLaunchKernelGGL((quant_rows_kernel<D, L, K, DT, DR>), grid, dim3(256), 0, s, a);
+#ifndef NQ_QUANT_GROUP
+#define NQ_QUANT_GROUP 8
+#endif
+
+// Sub-items per work item: NQ_QUANT_GROUP, fewer while the grid would fall
+// below 8192 blocks (32 per CU).  Sets group, n_groups, hn, work and per_xcd
+// from heads, n_tensors and batch; returns the work item count (the caller
+// rejects counts beyond the grid limit before launching).
+static uint64_t plan_work(QuantArgs& a, uint64_t tiles) {
+    a.hn = a.heads * a.n_tensors;
+    uint32_t g = a.hn < (uint32_t)NQ_QUANT_GROUP ? a.hn : (uint32_t)NQ_QUANT_GROUP;
+    while (g > 1 && tiles * a.batch * ((a.hn + g - 1) / g) < 8192) g >>= 1;
+    a.group = g;
+    a.n_groups = (a.hn + g - 1) / g;
+    const uint64_t work = tiles * a.batch * a.n_groups;
+    a.work = (uint32_t)work;
+    a.per_xcd = (uint32_t)((work + 7) / 8);
+    return work;
+}
+
+template <int D, int L, bool K, int DT, int DR, bool PAGE = false>
+static hipError_t launch_quant(const QuantArgs& a, const QuantTables& t, hipStream_t s) {
+    hipLaunchKernelGGL((quant_rows_kernel<D, L, K, DT, DR, PAGE>), dim3(a.per_xcd * 8u), dim3(256), 0, s, a, t.src,
+                       t.recon, t.syms, t.cosets, t.scales, t.positions, t.codes8, t.scales16);
     return hipGetLastError();
 }
 
 template <int D, int L, bool K, int DR>
-static hipError_t dispatch_dtype(int dt, const QuantArgs& a, uint32_t n, hipStream_t s) {
+static hipError_t dispatch_dtype(int dt, const QuantArgs& a, const QuantTables& t, hipStream_t s) {
     switch (dt) {
-        case NQ_F16: return launch_quant<D, L, K, NQ_F16, DR>(a, n, s);
-        case NQ_BF16: return launch_quant<D, L, K, NQ_BF16, DR>(a, n, s);
-        default: return launch_quant<D, L, K, NQ_F32, DR>(a, n, s);
+        case NQ_F16: return launch_quant<D, L, K, NQ_F16, DR>(a, t, s);
+        case NQ_BF16: return launch_quant<D, L, K, NQ_BF16, DR>(a, t, s);
+        default: return launch_quant<D, L, K, NQ_F32, DR>(a, t, s);
     }
 }
 
 template <int D, int L, int DR>
-static hipError_t dispatch_key(bool key, int dt, const QuantArgs& a, uint32_t n, hipStream_t s) {
-    return key ? dispatch_dtype<D, L, true, DR>(dt, a, n, s) : dispatch_dtype<D, L, false, DR>(dt, a, n, s);
+static hipError_t dispatch_key(bool key, int dt, const QuantArgs& a, const QuantTables& t, hipStream_t s) {
+    return key ? dispatch_dtype<D, L, true, DR>(dt, a, t, s) : dispatch_dtype<D, L, false, DR>(dt, a, t, s);
 }
 
 template <int D, int DR = D>
-static hipError_t dispatch_levels(int L, bool key, int dt, const QuantArgs& a, uint32_t n, hipStream_t s) {
+static hipError_t dispatch_levels(int L, bool key, int dt, const QuantArgs& a, const QuantTables& t, hipStream_t s) {
     switch (L) {
-        case 2: return dispatch_key<D, 2, DR>(key, dt, a, n, s);
-        case 4: return dispatch_key<D, 4, DR>(key, dt, a, n, s);
-        case 8: return dispatch_key<D, 8, DR>(key, dt, a, n, s);
-        default: return dispatch_key<D, 16, DR>(key, dt, a, n, s);
+        case 2: return dispatch_key<D, 2, DR>(key, dt, a, t, s);
+        case 4: return dispatch_key<D, 4, DR>(key, dt, a, t, s);
+        case 8: return dispatch_key<D, 8, DR>(key, dt, a, t, s);
+        default: return dispatch_key<D, 16, DR>(key, dt, a, t, s);
     }
 }
 
@@ -635,12 +782,13 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
                      "nq_quantize: RoPE table has %lld positions, need %d",
                      (long long)d->rope_n_pos, d->seq_in > d->seq_out ? d->seq_in : d->seq_out);
     }
+    QuantTables t = {};
+    t.src = d->src;
+    t.recon = d->recon;
+    t.syms = d->syms;
+    t.cosets = d->cosets;
+    t.scales = d->scales;
     QuantArgs a = {};
-    a.src = d->src;
-    a.recon = d->recon;
-    a.syms = d->syms;
-    a.cosets = d->cosets;
-    a.scales = d->scales;
     a.gather = d->gather;
     a.keep = d->keep;
     a.rope_cos = d->rope_cos;
@@ -650,23 +798,20 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     a.heads = (uint32_t)d->heads;
     a.seq_in = (uint32_t)d->seq_in;
     a.seq_out = (uint32_t)d->seq_out;
-    a.rows = (uint32_t)rows;
     a.hscale = d->hadamard_scale;
     a.keep_mode = d->keep_mode;
     a.n_tensors = (uint32_t)d->n_tensors;
-    a.bh = (uint32_t)d->batch * (uint32_t)d->heads;
-    const uint64_t work = (uint64_t)((d->seq_out + 63) / 64) * a.bh * a.n_tensors;
+    a.batch = (uint32_t)d->batch;
+    const uint64_t work = plan_work(a, (uint64_t)(d->seq_out + 63) / 64);
     NQ_CHECK_ARG(work < (1ull << 32) - 8, "nq_quantize: %llu work items exceed the grid limit",
                  (unsigned long long)work);
-    a.work = (uint32_t)work;
-    a.per_xcd = (uint32_t)((work + 7) / 8);
     hipStream_t s = (hipStream_t)stream;
     hipError_t e;
     switch (d->head_dim) {
-        case 64: e = dispatch_levels<64>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
-        case 96: e = dispatch_levels<128, 96>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
-        case 128: e = dispatch_levels<128>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
-        default: e = dispatch_levels<256>(d->levels, d->is_key != 0, d->dtype, a, d->n_tensors, s); break;
+        case 64: e = dispatch_levels<64>(d->levels, d->is_key != 0, d->dtype, a, t, s); break;
+        case 96: e = dispatch_levels<128, 96>(d->levels, d->is_key != 0, d->dtype, a, t, s); break;
+        case 128: e = dispatch_levels<128>(d->levels, d->is_key != 0, d->dtype, a, t, s); break;
+        default: e = dispatch_levels<256>(d->levels, d->is_key != 0, d->dtype, a, t, s); break;
     }
     NQ_CHECK_HIP(e);
     return NQ_OK;
@@ -676,27 +821,21 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
 
 namespace nq {
 
-template <int D, int L, bool K, int DT>
-static hipError_t launch_page(const QuantArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((quant_rows_kernel<D, L, K, DT, D, true>), dim3(a.per_xcd * 8u), dim3(256), 0, s, a);
-    return hipGetLastError();
-}
-
 template <int D, int L, bool K>
-static hipError_t page_dtype(int dt, const QuantArgs& a, hipStream_t s) {
+static hipError_t page_dtype(int dt, const QuantArgs& a, const QuantTables& t, hipStream_t s) {
     switch (dt) {
-        case NQ_F16: return launch_page<D, L, K, NQ_F16>(a, s);
-        case NQ_BF16: return launch_page<D, L, K, NQ_BF16>(a, s);
-        default: return launch_page<D, L, K, NQ_F32>(a, s);
+        case NQ_F16: return launch_quant<D, L, K, NQ_F16, D, true>(a, t, s);
+        case NQ_BF16: return launch_quant<D, L, K, NQ_BF16, D, true>(a, t, s);
+        default: return launch_quant<D, L, K, NQ_F32, D, true>(a, t, s);
     }
 }
 
 template <int D>
-static hipError_t page_levels(int L, bool key, int dt, const QuantArgs& a, hipStream_t s) {
+static hipError_t page_levels(int L, bool key, int dt, const QuantArgs& a, const QuantTables& t, hipStream_t s) {
     switch (L) {
-        case 4: return key ? page_dtype<D, 4, true>(dt, a, s) : page_dtype<D, 4, false>(dt, a, s);
-        case 8: return key ? page_dtype<D, 8, true>(dt, a, s) : page_dtype<D, 8, false>(dt, a, s);
-        default: return key ? page_dtype<D, 16, true>(dt, a, s) : page_dtype<D, 16, false>(dt, a, s);
+        case 4: return key ? page_dtype<D, 4, true>(dt, a, t, s) : page_dtype<D, 4, false>(dt, a, t, s);
+        case 8: return key ? page_dtype<D, 8, true>(dt, a, t, s) : page_dtype<D, 8, false>(dt, a, t, s);
+        default: return key ? page_dtype<D, 16, true>(dt, a, t, s) : page_dtype<D, 16, false>(dt, a, t, s);
     }
 }
 
@@ -726,36 +865,34 @@ extern "C" int nq_page_encode(const nq_page_desc* d, void* stream) {
         NQ_CHECK_ARG(d->rope_cos && d->rope_sin && d->rope_n_pos > 0 && d->rope_n_pos < (1ll << 31),
                      "nq_page_encode: keys need RoPE tables");
     }
+    QuantTables t = {};
+    t.src = d->src;
+    t.positions = d->positions;
+    t.codes8 = d->codes;
+    t.scales16 = d->scales;
     QuantArgs a = {};
-    a.src = d->src;
     a.rope_cos = d->rope_cos;
     a.rope_sin = d->rope_sin;
     a.rope_dm = d->rope_sin_minus_cos;
     a.rope_dp = d->rope_cos_plus_sin;
     a.heads = 1u;  // a page's (head, token) rows are one flat run of rows
     a.seq_in = a.seq_out = (uint32_t)rows;
-    a.rows = (uint32_t)rows;
     a.hscale = d->hadamard_scale;
     a.keep_mode = NQ_KEEP_ZERO;
     a.n_tensors = (uint32_t)d->n_pages;
-    a.bh = 1u;
-    a.positions = d->positions;
-    a.codes8 = d->codes;
-    a.scales16 = d->scales;
+    a.batch = 1u;
     a.page_tokens = (uint32_t)(d->tokens > 0 ? d->tokens : 1);
     a.rope_n_pos = (uint32_t)(d->is_key ? d->rope_n_pos : 1);
-    const uint64_t work = (rows + 63) / 64 * a.n_tensors;
+    const uint64_t work = plan_work(a, (rows + 63) / 64);
     NQ_CHECK_ARG(work < (1ull << 32) - 8, "nq_page_encode: %llu work items exceed the grid limit",
                  (unsigned long long)work);
-    a.work = (uint32_t)work;
-    a.per_xcd = (uint32_t)((work + 7) / 8);
     hipStream_t s = (hipStream_t)stream;
     const bool key = d->is_key != 0;
     hipError_t e;
     switch (d->head_dim) {
-        case 64: e = page_levels<64>(d->levels, key, d->dtype, a, s); break;
-        case 128: e = page_levels<128>(d->levels, key, d->dtype, a, s); break;
-        default: e = page_levels<256>(d->levels, key, d->dtype, a, s); break;
+        case 64: e = page_levels<64>(d->levels, key, d->dtype, a, t, s); break;
+        case 128: e = page_levels<128>(d->levels, key, d->dtype, a, t, s); break;
+        default: e = page_levels<256>(d->levels, key, d->dtype, a, t, s); break;
     }
     NQ_CHECK_HIP(e);
     return NQ_OK;

@@ -14,17 +14,17 @@ struct SymBits {
 
 // ------------------------------------------------------------- loads ------
 
+// 8 coordinates from their raw bytes: one uint4 of fp16 / bf16, two of fp32.
 template <int DT>
-__device__ __forceinline__ void load8(const void* base, int64_t elem_off, float* out) {
+__device__ __forceinline__ void cvt8(const uint4* r, float* out) {
     if constexpr (DT == NQ_F32) {
-        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem_off);
-        float4 a = p[0], b = p[1];
-        out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-        out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+        const uint4 a = r[0], b = r[1];
+        const uint32_t ws[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) out[k] = __builtin_bit_cast(float, ws[k]);
     } else {
-        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem_off);
-        uint4 w = *p;
-        uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        const uint4 w = r[0];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             if constexpr (DT == NQ_BF16) {
@@ -36,6 +36,16 @@ __device__ __forceinline__ void load8(const void* base, int64_t elem_off, float*
             }
         }
     }
+}
+
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t elem_off, float* out) {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(base) +
+                                                    elem_off * (DT == NQ_F32 ? 4 : 2));
+    uint4 r[2];
+    r[0] = p[0];
+    if constexpr (DT == NQ_F32) r[1] = p[1];
+    cvt8<DT>(r, out);
 }
 
 __device__ __forceinline__ void load8f(const float* p, float* out) {
