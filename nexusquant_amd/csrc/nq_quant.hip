@@ -43,7 +43,7 @@ struct QuantArgs {
     const float* rope_dp;
     uint32_t heads, seq_in, seq_out, n_tensors;
     uint32_t batch, hn, group, n_groups;    // hn = heads * n_tensors sub-items per batch row, in groups
-    uint32_t work, per_xcd;                 // work items = ceil(seq_out/64) * batch * n_groups
+    uint32_t n_tiles, work, per_xcd;        // work items = n_tiles * batch * n_groups, n_tiles = ceil(seq_out/64)
     float hscale;
     int32_t keep_mode;                      // NQ_KEEP_*
     // page encoding (PAGE instantiations only): rows are a page's (head, token)
@@ -463,14 +463,14 @@ __device__ __forceinline__ void quant_row_body(const QuantArgs& a, float (&x)[D 
         // subtracting (L/2) D after the exact multiply by L.  Without the top
         // stage (MERGED) the constant lands as (L/2)(D/2) on coordinates 0 and
         // D/2 (lane 0, chunks 0 and C/2).
+        const float gl = g * (float)L;  // exact
+        const float dc = q == 0 ? HL * (float)(MERGED ? D / 2 : D) : 0.0f;
         half2v hp[C][4];
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
             for (int k = 0; k < 4; ++k) hp[c][k] = __builtin_bit_cast(half2v, u[c][k]);
         fwht_row_f16<C, !MERGED>(hp, q);
-        const float gl = g * (float)L;  // exact
-        const float dc = q == 0 ? HL * (float)(MERGED ? D / 2 : D) : 0.0f;
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
@@ -584,15 +584,18 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a, const uint
     // range.  A work item is one 64-token tile of one batch row and a group of
     // sub-items j, the (head, tensor) pairs of that row with the tensor fastest,
     // which every wave runs back to back for its 16 tokens.  Items are ordered
-    // (tile, batch, group) with the group fastest, so the blocks that read one
-    // tile's RoPE rows run back to back on one XCD and find them in its L2.  The
-    // whole block exits together.
+    // (group, batch, tile) with the tile fastest: the blocks resident on one XCD
+    // at a time cover consecutive tiles of one group, so they stream a few
+    // contiguous regions of the group's tensors instead of one small piece of
+    // every tensor (measured: 6% faster on the 80-layer 128K cache, and less
+    // sensitive to where the buffers land in physical memory).  The whole block
+    // exits together.
     const uint32_t w = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
     if (w >= a.work) return;
-    const uint32_t grp = w % a.n_groups;
-    const uint32_t rest = w / a.n_groups;
+    const uint32_t tile = w % a.n_tiles;
+    const uint32_t rest = w / a.n_tiles;
     const uint32_t b = rest % a.batch;
-    const uint32_t tile = rest / a.batch;
+    const uint32_t grp = rest / a.batch;
     const uint32_t t_raw = tile * 64u + (threadIdx.x >> 2);
     const bool in_range = t_raw < a.seq_out;
     const uint32_t t_out = in_range ? t_raw : a.seq_out - 1u;  // idle quads recompute a valid row
@@ -695,20 +698,19 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a, const uint
 
 // ---------------------------------------------------------------- host ----
 
-#ifndef NQ_QUANT_GROUP
-#define NQ_QUANT_GROUP 8
-#endif
+// Sub-items per work item: 8 (16 and 1 measured slower), fewer while the grid
+// would fall below 8192 blocks (32 per CU).  Sets group, n_groups, hn, n_tiles,
+// work and per_xcd from heads, n_tensors and batch; returns the work item count
+// (the caller rejects counts beyond the grid limit before launching).
+constexpr uint32_t kMaxGroup = 8;
 
-// Sub-items per work item: NQ_QUANT_GROUP, fewer while the grid would fall
-// below 8192 blocks (32 per CU).  Sets group, n_groups, hn, work and per_xcd
-// from heads, n_tensors and batch; returns the work item count (the caller
-// rejects counts beyond the grid limit before launching).
 static uint64_t plan_work(QuantArgs& a, uint64_t tiles) {
     a.hn = a.heads * a.n_tensors;
-    uint32_t g = a.hn < (uint32_t)NQ_QUANT_GROUP ? a.hn : (uint32_t)NQ_QUANT_GROUP;
+    uint32_t g = a.hn < kMaxGroup ? a.hn : kMaxGroup;
     while (g > 1 && tiles * a.batch * ((a.hn + g - 1) / g) < 8192) g >>= 1;
     a.group = g;
     a.n_groups = (a.hn + g - 1) / g;
+    a.n_tiles = (uint32_t)tiles;
     const uint64_t work = tiles * a.batch * a.n_groups;
     a.work = (uint32_t)work;
     a.per_xcd = (uint32_t)((work + 7) / 8);
