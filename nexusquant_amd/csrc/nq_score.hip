@@ -386,6 +386,40 @@ __device__ __forceinline__ void tile_store(char* lds, const uint4 (&r)[RealTile<
     }
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+// vmcnt(0) with the other counters left open (gfx9 s_waitcnt encoding)
+constexpr int kWaitVm0 = 0x0f70;
+
+// Rows [row0, row0 + 64) of a [seq, D] matrix into one LDS stage by direct-to-LDS
+// loads, in the padded layout tile_store writes (row r at r * ROWB).  The stage
+// is UPR = ROWB / 16 windows of 64 16-byte slots; window w goes to wave w mod 4,
+// and lane l of it fills slot 64 w + l: row (64 w + l) / UPR, unit
+// (64 w + l) mod UPR, the pad unit (D / 8) masked off.  Rows past seq are
+// clamped.  Nothing passes through registers, so a stage in flight costs no
+// VGPRs; the caller waits (vmcnt) and then synchronises the workgroup.
+template <int D>
+__device__ __forceinline__ void tile_dma(const uint16_t* base, int row0, int seq, char* buf) {
+    constexpr int UPR = RealTile<D>::ROWB / 16;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < (UPR + 3) / 4; ++k) {
+        const int w = 4 * k + wave;
+        if (w < UPR) {
+            const int slot = 64 * w + lane;
+            const int r = slot / UPR, u = slot - r * UPR;
+            if (u < D / 8) {
+                int row = row0 + r;
+                row = row < seq ? row : seq - 1;
+                __builtin_amdgcn_global_load_lds((global_void_t*)(base + (size_t)row * D + 8 * u),
+                                                 (lds_void_t*)(buf + 1024 * w), 16, 0, 0);
+            }
+        }
+    }
+}
+
 // 32x32 logits: A from registers (this lane's row, K chunks), B from 32 LDS rows.
 template <int DT, int D>
 __device__ __forceinline__ f32x16 logits_regs_lds(const uint4 (&a)[RealTile<D>::KS], const char* lds, int c, int g) {
@@ -473,23 +507,23 @@ __device__ __forceinline__ float add_rounded2(float acc, float p0, float p1, boo
     }
 }
 
-// One pass over the 64-key LDS stages of a query block: two LDS buffers, the
-// next stage's global loads issued before the current stage is computed and
-// stored to the other buffer after it (one barrier per stage).
+// One pass over the 64-key LDS stages of a query block, two LDS buffers: the
+// next stage's direct-to-LDS loads are issued before the current stage is
+// computed, and each thread waits for its own part before the one barrier per
+// stage.  The buffers are separate arrays used in fixed roles (the loop is
+// unrolled by two), so the compiler can see that the reads of the current
+// buffer do not depend on the loads into the other one.
 template <int DT, int D, int PASS>
-__device__ __forceinline__ void rowstats_sweep(const RealArgs& a, const uint16_t* kbase, char* lds,
+__device__ __forceinline__ void rowstats_sweep(const RealArgs& a, const uint16_t* kbase, char* lds0, char* lds1,
                                                const uint4 (&qa)[RealTile<D>::KS], int n_it, bool live,
                                                int q0, int lane, float (&m)[16], float (&z)[16]) {
     const int g = lane >> 5, c = lane & 31;
     const int my_diag = q0 / 32;  // this wave's diagonal 32-key block
-    uint4 stage[RealTile<D>::PER_THREAD];
-    tile_load<D>(kbase, 0, a.seq, stage);
-    tile_store<D>(lds, stage);
+    tile_dma<D>(kbase, 0, a.seq, lds0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
-#pragma unroll 1
-    for (int it = 0; it < n_it; ++it) {
-        const char* cur = lds + (it & 1) * RealTile<D>::BUF;
-        if (it + 1 < n_it) tile_load<D>(kbase, (it + 1) * 64, a.seq, stage);
+    auto stage = [&](int it, const char* cur, char* nxt) {
+        if (it + 1 < n_it) tile_dma<D>(kbase, (it + 1) * 64, a.seq, nxt);
         if (live) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -526,14 +560,21 @@ __device__ __forceinline__ void rowstats_sweep(const RealArgs& a, const uint16_t
                 }
             }
         }
-        if (it + 1 < n_it) tile_store<D>(lds + ((it + 1) & 1) * RealTile<D>::BUF, stage);
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this thread's part of the next stage has landed
         __syncthreads();
+    };
+#pragma unroll 1
+    for (int it = 0; it < n_it; it += 2) {
+        stage(it, lds0, lds1);
+        if (it + 1 < n_it) stage(it + 1, lds1, lds0);
     }
 }
 
 template <int DT, int D>
-__global__ __launch_bounds__(256) void real_rowstats(RealArgs a) {
-    __shared__ __align__(16) char lds[2 * RealTile<D>::BUF];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1))) void real_rowstats(
+    RealArgs a) {
+    __shared__ __align__(16) char lds0[RealTile<D>::BUF];
+    __shared__ __align__(16) char lds1[RealTile<D>::BUF];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 5, c = lane & 31;
     // items ordered (batch x kv head, query block from the last, query head of
     // the group): an XCD range covers whole KV groups, whose keys stay in its L2
@@ -563,11 +604,11 @@ __global__ __launch_bounds__(256) void real_rowstats(RealArgs a) {
         m[j] = -__builtin_inff();
         z[j] = 0.0f;
     }
-    rowstats_sweep<DT, D, 0>(a, kbase, lds, qa, n_it, live, q0, lane, m, z);
+    rowstats_sweep<DT, D, 0>(a, kbase, lds0, lds1, qa, n_it, live, q0, lane, m, z);
     // row max of the raw logits -> max of the eager logits -> -max * log2(e)
 #pragma unroll
     for (int j = 0; j < 16; ++j) m[j] = -(eager_logit<DT>(reduce32_max(m[j]), a.scaling) * kLog2e);
-    rowstats_sweep<DT, D, 1>(a, kbase, lds, qa, n_it, live, q0, lane, m, z);
+    rowstats_sweep<DT, D, 1>(a, kbase, lds0, lds1, qa, n_it, live, q0, lane, m, z);
     if (!live) return;
     const size_t stat = (size_t)bhq * a.seq;
 #pragma unroll
@@ -583,9 +624,9 @@ __global__ __launch_bounds__(256) void real_rowstats(RealArgs a) {
 
 template <int DT, int D>
 __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
-    __shared__ __align__(16) char lds[2 * RealTile<D>::BUF];
-    __shared__ __align__(16) float st_nm[2][64];
-    __shared__ __align__(16) float st_rz[2][64];
+    __shared__ __align__(16) char lds0[RealTile<D>::BUF];
+    __shared__ __align__(16) char lds1[RealTile<D>::BUF];
+    __shared__ __align__(16) float st_nm0[64], st_rz0[64], st_nm1[64], st_rz1[64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 5, c = lane & 31;
     // items ordered (batch x query head, key block): an XCD range walks its
     // query heads one after the other, so the streamed queries stay in its L2
@@ -608,33 +649,23 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
     uint4 kr[RealTile<D>::KS];
     row_operand<D>(kbase, key, a.seq, g, kr);
     float col = 0.0f;
-    const int t = threadIdx.x;
-    uint4 stage[RealTile<D>::PER_THREAD];
-    float snm = 0.0f, srz = 0.0f;  // threads 0..63 carry the row statistics of one row
-    tile_load<D>(qbase, it0 * 64, a.seq, stage);
-    if (t < 64) {
-        const int i = min(it0 * 64 + t, a.seq - 1);
-        snm = a.row_max[stat + i];
-        srz = a.row_sum[stat + i];
-    }
-    tile_store<D>(lds, stage);
-    if (t < 64) {
-        st_nm[0][t] = snm;
-        st_rz[0][t] = srz;
-    }
-    __syncthreads();
-#pragma unroll 1
-    for (int it = it0; it < n_it; ++it) {
-        const int cb = (it - it0) & 1;
-        const char* cur = lds + cb * RealTile<D>::BUF;
-        if (it + 1 < n_it) {
-            tile_load<D>(qbase, (it + 1) * 64, a.seq, stage);
-            if (t < 64) {
-                const int i = min((it + 1) * 64 + t, a.seq - 1);
-                snm = a.row_max[stat + i];
-                srz = a.row_sum[stat + i];
-            }
+    // One stage: 64 query rows by direct-to-LDS loads, and (wave 0) their row
+    // statistics, one dword per lane.  Two buffers in fixed roles as in
+    // rowstats_sweep; each thread waits for its own loads before the barrier.
+    auto load_stage = [&](int it, char* buf, float* nm, float* rz) {
+        tile_dma<D>(qbase, it * 64, a.seq, buf);
+        if (wave == 0) {
+            const int i = min(it * 64 + lane, a.seq - 1);
+            __builtin_amdgcn_global_load_lds((global_void_t*)(a.row_max + stat + i), (lds_void_t*)nm, 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void_t*)(a.row_sum + stat + i), (lds_void_t*)rz, 4, 0, 0);
         }
+    };
+    load_stage(it0, lds0, st_nm0, st_rz0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    auto stage = [&](int it, const char* cur, const float* cnm, const float* crz, char* nxt, float* nnm,
+                     float* nrz) {
+        if (it + 1 < n_it) load_stage(it + 1, nxt, nnm, nrz);
         if (live) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -646,8 +677,8 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
 #pragma unroll
                 for (int jq = 0; jq < 4; ++jq) {
                     const int r0 = 8 * jq + 4 * g;  // rows r0 .. r0 + 3 of the 32-row block
-                    const float4 nm4 = *reinterpret_cast<const float4*>(&st_nm[cb][32 * h + r0]);
-                    const float4 rz4 = *reinterpret_cast<const float4*>(&st_rz[cb][32 * h + r0]);
+                    const float4 nm4 = *reinterpret_cast<const float4*>(&cnm[32 * h + r0]);
+                    const float4 rz4 = *reinterpret_cast<const float4*>(&crz[32 * h + r0]);
                     const float nm[4] = {nm4.x, nm4.y, nm4.z, nm4.w};
                     const float rz[4] = {rz4.x, rz4.y, rz4.z, rz4.w};
 #pragma unroll
@@ -669,14 +700,13 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
                 }
             }
         }
-        if (it + 1 < n_it) {
-            tile_store<D>(lds + (cb ^ 1) * RealTile<D>::BUF, stage);
-            if (t < 64) {
-                st_nm[cb ^ 1][t] = snm;
-                st_rz[cb ^ 1][t] = srz;
-            }
-        }
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this thread's part of the next stage has landed
         __syncthreads();
+    };
+#pragma unroll 1
+    for (int it = it0; it < n_it; it += 2) {
+        stage(it, lds0, st_nm0, st_rz0, lds1, st_nm1, st_rz1);
+        if (it + 1 < n_it) stage(it + 1, lds1, st_nm1, st_rz1, lds0, st_nm0, st_rz0);
     }
     col += __shfl_xor(col, 32, 64);
     if (g == 0 && key < a.seq) a.colsum[stat + key] = col;
