@@ -67,19 +67,6 @@ __device__ __forceinline__ void load8_elem(const void* p, size_t i, float (&x)[8
     }
 }
 
-template <int DT>
-__device__ __forceinline__ void copy8_elem(const void* src, void* dst, size_t i) {
-    if constexpr (DT == NQ_F32) {
-        reinterpret_cast<float4*>(static_cast<float*>(dst) + i)[0] =
-            reinterpret_cast<const float4*>(static_cast<const float*>(src) + i)[0];
-        reinterpret_cast<float4*>(static_cast<float*>(dst) + i + 4)[0] =
-            reinterpret_cast<const float4*>(static_cast<const float*>(src) + i + 4)[0];
-    } else {
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(dst) + i) =
-            *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + i);
-    }
-}
-
 __global__ __launch_bounds__(256) void nq_fill_i32(int32_t* p, int64_t n, int32_t v) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = v;
@@ -427,44 +414,58 @@ struct ApplyArgs {
     const int32_t* ev_idx;
     const float* weight;
     int n_layers, b, h, s, d;
-    uint64_t rows;           // n_layers * b * h * s
 };
 
+// Grid: x over (token, 8-element piece) of one head's rows, y over batch x head
+// (strided when there are more than the grid allows), z over the layers; all
+// index arithmetic is 32-bit, the row split a shift for power-of-two head dims.
 template <int DT>
 __global__ __launch_bounds__(256) void merge_apply_kernel(ApplyArgs a) {
-    const int lanes_per_row = a.d / 8;
-    const uint64_t r = ((uint64_t)blockIdx.x * 256 + threadIdx.x) / lanes_per_row;
-    if (r >= a.rows) return;
-    const int j = (int)(((uint64_t)blockIdx.x * 256 + threadIdx.x) % lanes_per_row) * 8;
-    const int t = (int)(r % a.s);
-    const uint64_t bh = (r / a.s) % ((uint64_t)a.b * a.h);
-    const int layer = (int)(r / a.s / ((uint64_t)a.b * a.h));
-    const int bi = (int)(bh / a.h);
+    const uint32_t lanes_per_row = (uint32_t)a.d / 8u;
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t t = (lanes_per_row & (lanes_per_row - 1u)) == 0u ? idx >> __builtin_ctz(lanes_per_row)
+                                                                     : idx / lanes_per_row;
+    if (t >= (uint32_t)a.s) return;
+    const int j = (int)(idx - t * lanes_per_row) * 8;
+    const int layer = blockIdx.z;
     const void* src = reinterpret_cast<const void*>(a.src[layer]);
     void* dst = reinterpret_cast<void*>(a.dst[layer]);
-    const size_t row_off = (bh * a.s + t) * (size_t)a.d + j;
-    const size_t rb = (size_t)bi * a.s;
-    const int kl = a.kept_local[rb + t];
-    const int beg = kl >= 0 ? a.offset[rb + kl] : 0;
-    const int end = kl >= 0 ? a.count[rb + kl] : 0;
-    if (end <= beg) {
-        copy8_elem<DT>(src, dst, row_off);
-        return;
-    }
-    const size_t head_base = bh * a.s * (size_t)a.d + j;
-    float v[8];
-    load8_elem<DT>(src, row_off, v);
-    for (int i = beg; i < end; ++i) {
-        const int e = a.list[rb + i];
-        const int pe = a.ev_idx[rb + e];
-        const float w = a.weight[rb + e];
-        float x[8];
-        load8_elem<DT>(src, head_base + (size_t)pe * a.d, x);
+    const uint32_t bh_count = (uint32_t)a.b * (uint32_t)a.h;
+    for (uint32_t bh = blockIdx.y; bh < bh_count; bh += gridDim.y) {
+        const uint32_t bi = bh / (uint32_t)a.h;
+        const size_t row_off = ((size_t)bh * a.s + t) * (size_t)a.d + j;
+        const size_t rb = (size_t)bi * a.s;
+        // the row's own 8 elements load alongside its list entry (both are needed
+        // on either path), so the two memory latencies overlap
+        constexpr int NW = DT == NQ_F32 ? 2 : 1;
+        const uint4* sp = reinterpret_cast<const uint4*>(static_cast<const char*>(src) + row_off * (DT == NQ_F32 ? 4 : 2));
+        uint4 raw[NW];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = v[k] + w * x[k];  // two roundings, as the reference's separate ops
-    }
+        for (int k = 0; k < NW; ++k) raw[k] = sp[k];
+        const int kl = a.kept_local[rb + t];
+        const int beg = kl >= 0 ? a.offset[rb + kl] : 0;
+        const int end = kl >= 0 ? a.count[rb + kl] : 0;
+        uint4* dp = reinterpret_cast<uint4*>(static_cast<char*>(dst) + row_off * (DT == NQ_F32 ? 4 : 2));
+        if (end <= beg) {  // no merges: the bits unchanged
 #pragma unroll
-    for (int k = 0; k < 8; ++k) store_elem<DT>(dst, row_off + k, v[k]);
+            for (int k = 0; k < NW; ++k) dp[k] = raw[k];
+            continue;
+        }
+        const size_t head_base = (size_t)bh * a.s * (size_t)a.d + j;
+        float v[8];
+        load8_elem<DT>(src, row_off, v);
+        for (int i = beg; i < end; ++i) {
+            const int e = a.list[rb + i];
+            const int pe = a.ev_idx[rb + e];
+            const float w = a.weight[rb + e];
+            float x[8];
+            load8_elem<DT>(src, head_base + (size_t)pe * a.d, x);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = v[k] + w * x[k];  // two roundings, as the reference's separate ops
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) store_elem<DT>(dst, row_off + k, v[k]);
+    }
 }
 
 }  // namespace nq
@@ -589,10 +590,10 @@ extern "C" int nq_merge_values(const nq_merge_desc* d, void* stream) {
     ap.h = h;
     ap.s = s;
     ap.d = D;
-    ap.rows = (uint64_t)d->n_tensors * b * h * s;
-    const uint64_t threads = ap.rows * (uint64_t)(D / 8);
-    NQ_CHECK_ARG((threads + 255) / 256 < (1ull << 31), "nq_merge_values: too many rows");
-    const dim3 g((uint32_t)((threads + 255) / 256));
+    const uint64_t threads = (uint64_t)s * (uint64_t)(D / 8);  // per (layer, batch, head)
+    NQ_CHECK_ARG(threads < (1ull << 31), "nq_merge_values: sequence too long");
+    const uint32_t bh = (uint32_t)b * (uint32_t)h;
+    const dim3 g((uint32_t)((threads + 255) / 256), bh < 65535u ? bh : 65535u, (uint32_t)d->n_tensors);
     if (d->dtype == NQ_F16) hipLaunchKernelGGL(merge_apply_kernel<NQ_F16>, g, dim3(256), 0, st, ap);
     else if (d->dtype == NQ_BF16) hipLaunchKernelGGL(merge_apply_kernel<NQ_BF16>, g, dim3(256), 0, st, ap);
     else hipLaunchKernelGGL(merge_apply_kernel<NQ_F32>, g, dim3(256), 0, st, ap);

@@ -561,8 +561,9 @@ __device__ __forceinline__ void quant_row_body(const QuantArgs& a, float (&x)[D 
     }  // !PAGE
 }
 
-// lgkmcnt(0) with the other counters left open (gfx9 s_waitcnt encoding)
+// lgkmcnt(0) / vmcnt(0) with the other counters left open (gfx9 s_waitcnt encoding)
 constexpr int kWaitLgkm0 = 0xc07f;
+constexpr int kWaitVm0 = 0x0f70;
 
 template <int D, int L, bool IS_KEY, int DT, int DR, bool PAGE = false>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
@@ -648,6 +649,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a, const uint
         const uint32_t bh = b * a.heads + j / a.n_tensors;
         float x[C][8];
         if constexpr (ST::pipe) {
+            // the wave's own loads of this sub-item's rows have landed (each wave
+            // reads back only what it staged, so no barrier is needed)
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
             uint4 raw[ST::nseg];
 #pragma unroll
             for (int s = 0; s < ST::nseg; ++s) raw[s] = *reinterpret_cast<const uint4*>(wstage + s * 1024 + lane * 16);
