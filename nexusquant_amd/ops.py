@@ -171,7 +171,7 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
             (rows this launch does not write keep their contents).
     launch_events: optional (start, end) torch.cuda.Event pair recorded on the
     launch stream immediately around the kernel launch.
-    merged_tables: pass the precomputed fl(cos - sin) / fl(cos + sin) tables for
+    merged_tables: pass the precomputed fl(sin - cos) / fl(cos + sin) tables for
             keys (False: the kernel forms them from cos / sin; same results).
     Returns (fp16 reconstructions or None, PackedCodes or None), one per tensor.
     """
