@@ -11,17 +11,18 @@
 //     fp16 Walsh-Hadamard of the integer codes without the top stage, one
 //     scale multiply, the merged top stage + forward RoPE at the stored
 //     position, rounding to fp16 -- bit for bit the keys the page decoder
-//     writes -- then q . k with v_dot2_f32_f16 (fp16 queries) or fp32 FMAs,
-//     divided by fl(sqrt(head_dim)).  Logits go to LDS.
+//     writes -- then q . k divided by fl(sqrt(head_dim)): a 16x16x32 fp16 MFMA
+//     per 32 coordinates for fp16 queries with 8 heads per kv head, else
+//     v_dot2_f32_f16 (fp16 queries) or fp32 FMAs.  Logits go to LDS.
 //  2. Per query head the chunk max x_m of the unscaled logits and
 //     e = exp((x - x_m) / scale_divisor), l = sum e (fixed order); LDS keeps
-//     e * scale_v / 2 per token.
+//     the weight e * scale_v / 2 per token as an fp16 pair hi + lo.
 //  3. Values are never reconstructed per token: the inverse Hadamard is
 //     linear, so sum_t e_t v_t = h_D * S (sum_t e_t (scale_t / 2) c_t) with
-//     c_t the integer codes.  Lanes own D/64 consecutive coordinates and
-//     accumulate e_t (scale_t / 2) c_t over the chunk; the block applies S to
-//     its sum once, and the combine kernel weights the chunks, applies h_D and
-//     divides by the softmax sum.
+//     c_t the integer codes (exact in fp16).  The matrix cores accumulate
+//     weights x codes over the chunk, 32 tokens per MFMA; the block applies
+//     S to its sum once, and the combine kernel weights the chunks, applies
+//     h_D and divides by the softmax sum.
 //
 // Work items are (chunk, kv head) with the kv head fastest, and block 8k + x
 // takes item x * per_xcd + k: the kv heads of one chunk run on one XCD and
@@ -97,6 +98,10 @@ __device__ __forceinline__ float attn_load_f32(const void* p, size_t i) {
     else return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
 }
 
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
 // wave-wide reductions (64 lanes) through LDS-free cross-lane moves
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -110,13 +115,14 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 template <int D, int G, int QDT>
-__global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 2))) void paged_attn_kernel(
+    AttnArgs a) {
     constexpr int C = D / 32;
-    constexpr int V2 = D / 64;  // value coordinates per lane in step 3
     constexpr bool QF16 = QDT == NQ_F16;
     __shared__ __attribute__((aligned(16))) float s_w[kChunk * G];  // [token][head]: logits, then e * scale_v / 2
     __shared__ float s_a[kChunk];       // scale_v / 2 per token
-    __shared__ float s_red[4][G];
+    __shared__ float s_red[4][G];   // per wave: each head's max, then
+    __shared__ float s_sum[4][G];   // its sum of exp
     __shared__ float s_acc[4][G][D];
 
     const int lane = threadIdx.x & 63;
@@ -148,6 +154,21 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     }
     __syncthreads();
     const float qsig = quad_sign(q);
+
+    // fp16 queries with 8 heads per kv head take q . k on the matrix cores: per
+    // unit and chunk c one 16x16x32 fp16 MFMA with the unit's 16 keys as the A
+    // rows and the query heads as the B columns (heads 8..15 zero).  Lane l
+    // holds B for head l % 16 over coordinates 32c + 8 (l / 16) .. + 7.
+    constexpr bool QK_MFMA = QF16 && G == 8;
+    half8v qb[QK_MFMA ? C : 1];
+    if constexpr (QK_MFMA) {
+        const int n = lane & 15, kg = lane >> 4;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const uint4 v = n < G ? *reinterpret_cast<const uint4*>(&s_q[n][c][kg][0]) : make_uint4(0u, 0u, 0u, 0u);
+            qb[c] = __builtin_bit_cast(half8v, v);
+        }
+    }
 
     // ---- 1. keys and logits, one token per quad, 16 tokens per unit ----
     // The next unit's record and key codes are loaded while the current one is
@@ -209,28 +230,51 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) kf[c][k] = half2v{(__fp16)x[c][2 * k], (__fp16)x[c][2 * k + 1]};
 
-#pragma unroll
-        for (int gq = 0; gq < G; ++gq) {
-            float acc = 0.0f;
+        if constexpr (QK_MFMA) {
+            // keys to the MFMA A layout: lane 16g + t takes token t's coordinates
+            // 32c + 8g .. + 7 from lane 4t + g (the quad layout)
+            const int addr_in = 4 * (4 * (lane & 15) + (lane >> 4));
+            float4v lg = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int c = 0; c < C; ++c) {
-                qreg_t qv[QR];
+                u32x4v bw;
 #pragma unroll
-                for (int k = 0; k < QR; ++k) qv[k] = s_q[gq][c][q][k];
-                if constexpr (QF16) {
+                for (int k = 0; k < 4; ++k)
+                    bw[k] = (uint32_t)__builtin_amdgcn_ds_bpermute(addr_in, (int)__builtin_bit_cast(uint32_t, kf[c][k]));
+                lg = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, bw), qb[c], lg, 0, 0, 0);
+            }
+            // lane l holds the logits of tokens 4 (l / 16) + i for head l % 16
+            const int n = lane & 15;
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_fdot2(kf[c][k], qv[k], acc, false);
-                } else {
+            for (int i = 0; i < 4; ++i) {
+                const int tt = 4 * (lane >> 4) + i;
+                const float v = lg[i];
+                if (n < G && tt < rc.n && rc.coff + tt < kChunk) s_w[(rc.coff + tt) * G + n] = v;
+            }
+        } else {
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        acc = __builtin_fmaf((float)kf[c][k].x, qv[2 * k], acc);
-                        acc = __builtin_fmaf((float)kf[c][k].y, qv[2 * k + 1], acc);
+            for (int gq = 0; gq < G; ++gq) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    qreg_t qv[QR];
+#pragma unroll
+                    for (int k = 0; k < QR; ++k) qv[k] = s_q[gq][c][q][k];
+                    if constexpr (QF16) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_fdot2(kf[c][k], qv[k], acc, false);
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            acc = __builtin_fmaf((float)kf[c][k].x, qv[2 * k], acc);
+                            acc = __builtin_fmaf((float)kf[c][k].y, qv[2 * k + 1], acc);
+                        }
                     }
                 }
+                acc += dpp_f32<kQuadXor1>(acc);
+                acc += dpp_f32<kQuadXor2>(acc);
+                if (valid && q == 0) s_w[(rc.coff + t) * G + gq] = acc;
             }
-            acc += dpp_f32<kQuadXor1>(acc);
-            acc += dpp_f32<kQuadXor2>(acc);
-            if (valid && q == 0) s_w[(rc.coff + t) * G + gq] = acc;
         }
         if (valid && q == 1) s_a[rc.coff + t] = 0.5f * f16_bits_to_f32(kin.vs);
         rc = rn;
@@ -242,107 +286,163 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
     // s_w is [token][head]; a thread's entries i, i + 256, ... all belong to head
     // i % G (G divides 256), so lanes of one head reduce with xor offsets >= G.
     const int my_g = threadIdx.x % G;
+    __shared__ float s_amax[4];
     {
         float v = -__builtin_inff();
         for (int i = threadIdx.x; i < n_tok * G; i += 256) v = __builtin_fmaxf(v, s_w[i]);
 #pragma unroll
         for (int o = 32; o >= G; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
         if (lane < G) s_red[wave][lane] = v;
+        float am = 0.0f;
+        for (int t = threadIdx.x; t < n_tok; t += 256) am = __builtin_fmaxf(am, s_a[t]);
+        am = wave_max(am);
+        if (lane == 0) s_amax[wave] = am;
     }
     __syncthreads();
-    float m[G], l[G];
-#pragma unroll
-    for (int gq = 0; gq < G; ++gq)
-        m[gq] = __builtin_fmaxf(__builtin_fmaxf(s_red[0][gq], s_red[1][gq]), __builtin_fmaxf(s_red[2][gq], s_red[3][gq]));
-    __syncthreads();
+    // a head's chunk max and exp sum stay in LDS (read again for the output)
+    auto head_max = [&](int gq) {
+        return __builtin_fmaxf(__builtin_fmaxf(s_red[0][gq], s_red[1][gq]), __builtin_fmaxf(s_red[2][gq], s_red[3][gq]));
+    };
+    auto head_sum = [&](int gq) { return (s_sum[0][gq] + s_sum[1][gq]) + (s_sum[2][gq] + s_sum[3][gq]); };
+    // Step 3 takes the weights e * scale_v / 2 as an fp16 pair hi + lo (22
+    // significant bits), scaled by 2^(14 - x) where 2^x > the chunk's largest
+    // scale_v / 2, so the largest weight sits just under 2^14 and small ones
+    // stay clear of fp16's subnormals; the sum is scaled back by 2^(x - 14).
+    int wexp = 0;
     {
-        const float mg = m[my_g];
+        const float am = __builtin_fmaxf(__builtin_fmaxf(s_amax[0], s_amax[1]), __builtin_fmaxf(s_amax[2], s_amax[3]));
+        if (am > 0.0f) (void)__builtin_frexpf(am, &wexp);
+    }
+    const float wmul = __builtin_ldexpf(1.0f, 14 - wexp);
+    {
+        const float mg = head_max(my_g);
         float v = 0.0f;
         for (int i = threadIdx.x; i < n_tok * G; i += 256) {
             const float e = expf((s_w[i] - mg) * a.inv_scale);
             v += e;
-            s_w[i] = e * s_a[i / G];
+            const float w = (e * s_a[i / G]) * wmul;
+            const __fp16 hi = (__fp16)w;
+            const __fp16 lo = (__fp16)(w - (float)hi);
+            s_w[i] = __builtin_bit_cast(float, half2v{hi, lo});
         }
 #pragma unroll
         for (int o = 32; o >= G; o >>= 1) v += __shfl_xor(v, o, 64);
-        if (lane < G) s_red[wave][lane] = v;
+        if (lane < G) s_sum[wave][lane] = v;
     }
     __syncthreads();
-#pragma unroll
-    for (int gq = 0; gq < G; ++gq) l[gq] = (s_red[0][gq] + s_red[1][gq]) + (s_red[2][gq] + s_red[3][gq]);
 
-    // ---- 3. values in the lattice domain: lane owns coordinates V2*lane .. +V2-1 ----
-    float acc[G][V2];
+    // ---- 3. values in the lattice domain, on the matrix cores ----
+    // Per pair of units (32 tokens) and column block j one 16x16x32 fp16 MFMA
+    // Y_j += W X_j: the K index is (unit, token), W's rows are (part, head) --
+    // rows 0..G-1 the heads' hi weights, rows G..2G-1 their lo weights, the
+    // rest zero -- and X_j's column n is coordinate NB * n + j.  Lane (n, kg)
+    // holds the tokens 8 (kg & 1) .. + 7 of unit kg >> 1: NB consecutive code
+    // bytes of each of those 8 rows (one load per row) and the matching weights.
+    constexpr int NB = D / 16;
+    using cword_t = typename std::conditional<NB == 4, uint32_t,
+                                              typename std::conditional<NB == 8, uint2, uint4>::type>::type;
+    const int n16 = lane & 15, kg = lane >> 4;
+    const bool second = kg >= 2;
+    const int tb = 8 * (kg & 1);
+    const bool has_w = n16 < 2 * G;
+    const int w_half = 2 * (n16 % G) + (n16 >= G ? 1 : 0);  // fp16 index within a token's G hi/lo pairs
+    const _Float16* s_wh = reinterpret_cast<const _Float16*>(s_w);
+    struct ValRec {
+        const int8_t* vc;
+        int32_t stride, n, nw, coff;
+    };
+    // this lane's unit of the pair (pu, pu + 1); a missing second unit reads the
+    // first's rows under zero weights
+    auto val_rec = [&](int pu) {
+        const bool has_b = pu + 1 < u1;
+        const UnitRec ra = unit_rec(a, pu);
+        const UnitRec rb = unit_rec(a, has_b ? pu + 1 : pu);
+        ValRec v;
+        v.vc = second ? rb.vc : ra.vc;
+        v.stride = second ? rb.stride : ra.stride;
+        v.n = second ? rb.n : ra.n;
+        v.coff = second ? rb.coff : ra.coff;
+        int nw = second ? (has_b ? rb.n : 0) : ra.n;
+        if (v.coff + nw > kChunk) nw = kChunk - v.coff;
+        v.nw = nw;
+        return v;
+    };
+    auto load_codes = [&](const ValRec& r, uint32_t (&cw)[8][NB / 4]) {
+        const int8_t* base = r.vc + (size_t)kh * r.stride * D + NB * n16;
 #pragma unroll
-    for (int gq = 0; gq < G; ++gq)
+        for (int s = 0; s < 8; ++s) {
+            const int t = tb + s < r.n ? tb + s : r.n - 1;
+            const cword_t x = *reinterpret_cast<const cword_t*>(base + (size_t)t * D);
+            const uint32_t* xw = reinterpret_cast<const uint32_t*>(&x);
 #pragma unroll
-        for (int v = 0; v < V2; ++v) acc[gq][v] = 0.0f;
-    // a unit's 16 value rows are loaded together, one unit ahead
-    using vword_t = typename std::conditional<V2 == 4, uint32_t, uint16_t>::type;
-    auto load_values = [&](const UnitRec& r, uint32_t (&vw)[16]) {
-        const int8_t* base = r.vc + (size_t)kh * r.stride * D + V2 * lane;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int t = i < r.n ? i : r.n - 1;
-            if constexpr (V2 == 1) vw[i] = (uint32_t)(uint8_t)base[(size_t)t * D];
-            else vw[i] = *reinterpret_cast<const vword_t*>(base + (size_t)t * D);
+            for (int w = 0; w < NB / 4; ++w) cw[s][w] = xw[w];
         }
     };
-    u = u0 + wave;
-    rc = unit_rec(a, u < u1 ? u : u0);
-    uint32_t vcur[16];
-    load_values(rc, vcur);
-    for (; u < u1; u += 4) {
-        const int un = u + 4 < u1 ? u + 4 : u;
-        const UnitRec rn = unit_rec(a, un);
-        uint32_t vnext[16];
-        load_values(rn, vnext);
-        int tn = rc.n;
-        if (rc.coff + tn > kChunk) tn = kChunk - rc.coff;
+    float4v pacc[NB];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            if (r >= tn) break;
-            float cv[V2];
-            if constexpr (V2 == 1) {
-                cv[0] = (float)(int8_t)vcur[r];
-            } else {
-                half2v h0, h1;
-                attn_codes_f16(vcur[r], h0, h1);
-                cv[0] = (float)h0.x;
-                cv[1] = (float)h0.y;
-                if constexpr (V2 == 4) {
-                    cv[2] = (float)h1.x;
-                    cv[3] = (float)h1.y;
-                }
-            }
-            const int tc = rc.coff + r;
-            float wv[G];
-            if constexpr (G % 4 == 0) {
+    for (int j = 0; j < NB; ++j) pacc[j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    const half2v bias = {(__fp16)-1152.0f, (__fp16)-1152.0f};
+    u = u0 + 2 * wave;
+    ValRec vr = val_rec(u < u1 ? u : u0);
+    uint32_t ccur[8][NB / 4];
+    load_codes(vr, ccur);
+    for (; u < u1; u += 8) {
+        const int un = u + 8 < u1 ? u + 8 : u;
+        const ValRec vn = val_rec(un);
+        uint32_t cnext[8][NB / 4];
+        load_codes(vn, cnext);
+        half8v wa;
 #pragma unroll
-                for (int k = 0; k < G / 4; ++k) {
-                    const float4 w4 = reinterpret_cast<const float4*>(s_w + tc * G)[k];
-                    wv[4 * k] = w4.x;
-                    wv[4 * k + 1] = w4.y;
-                    wv[4 * k + 2] = w4.z;
-                    wv[4 * k + 3] = w4.w;
-                }
-            } else {
-#pragma unroll
-                for (int gq = 0; gq < G; ++gq) wv[gq] = s_w[tc * G + gq];
-            }
-#pragma unroll
-            for (int gq = 0; gq < G; ++gq)
-#pragma unroll
-                for (int v = 0; v < V2; ++v) acc[gq][v] = __builtin_fmaf(wv[gq], cv[v], acc[gq][v]);
+        for (int s = 0; s < 8; ++s) {
+            const bool ok = has_w && tb + s < vr.nw;
+            const _Float16 w = s_wh[ok ? 2 * G * (vr.coff + tb + s) + w_half : 0];
+            wa[s] = ok ? w : (_Float16)0.0f;
         }
-        rc = rn;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) vcur[i] = vnext[i];
+        for (int w = 0; w < NB / 4; ++w) {
+            // bytes b of dword w of tokens 2p, 2p + 1 -> one fp16 pair of column block 4w + b
+            uint32_t hb[4][4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t x0 = ccur[2 * p][w] ^ 0x80808080u, x1 = ccur[2 * p + 1][w] ^ 0x80808080u;
+                const uint32_t lo = __builtin_amdgcn_perm(x1, x0, 0x05010400u);  // x0.b0 x1.b0 x0.b1 x1.b1
+                const uint32_t hi = __builtin_amdgcn_perm(x1, x0, 0x07030602u);  // x0.b2 x1.b2 x0.b3 x1.b3
+                hb[0][p] = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00050004u);
+                hb[1][p] = __builtin_amdgcn_perm(lo, 0x64646464u, 0x00070006u);
+                hb[2][p] = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00050004u);
+                hb[3][p] = __builtin_amdgcn_perm(hi, 0x64646464u, 0x00070006u);
+            }
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                u32x4v xb;
+#pragma unroll
+                for (int p = 0; p < 4; ++p) xb[p] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, hb[b][p]) + bias);
+                pacc[4 * w + b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, __builtin_bit_cast(half8v, xb),
+                                                                          pacc[4 * w + b], 0, 0, 0);
+            }
+        }
+        vr = vn;
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int w = 0; w < NB / 4; ++w) ccur[s][w] = cnext[s][w];
     }
+    // lane l holds rows 4 kg + i of Y_j at column n16: a head's hi row plus its
+    // lo row (G rows further: 4G lanes on for G >= 4, in the same lane below)
+    constexpr int RI = G < 4 ? G : 4;  // rows of a lane that hold a head's hi sum
 #pragma unroll
-    for (int gq = 0; gq < G; ++gq)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int v = 0; v < V2; ++v) s_acc[wave][gq][V2 * lane + v] = acc[gq][v];
+        for (int i = 0; i < RI; ++i) {
+            if constexpr (G >= 4) pacc[j][i] += __shfl_xor(pacc[j][i], 4 * G, 64);
+            else pacc[j][i] += pacc[j][i + G];
+        }
+    if (4 * kg < G) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < RI; ++i) s_acc[wave][4 * kg + i][NB * n16 + j] = pacc[j][i];
+    }
     __syncthreads();
     // the four waves' sums (fixed order), then the unnormalised Walsh-Hadamard
     // over D in LDS, in place in s_acc[0]
@@ -362,13 +462,14 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
+    const float wunscale = __builtin_ldexpf(1.0f, wexp - 14);
     for (int i = threadIdx.x; i < G * D; i += 256) {
         const int gq = i / D, j = i % D;
         float* pp = a.part + ((size_t)chunk * a.q_heads + kh * G + gq) * (D + 2);
-        pp[2 + j] = s_acc[0][gq][j];
+        pp[2 + j] = s_acc[0][gq][j] * wunscale;
         if (j == 0) {
-            pp[0] = m[gq] * a.inv_scale;  // the chunk max in the scaled domain
-            pp[1] = l[gq];
+            pp[0] = head_max(gq) * a.inv_scale;  // the chunk max in the scaled domain
+            pp[1] = head_sum(gq);
         }
     }
 }
