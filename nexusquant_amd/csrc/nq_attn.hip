@@ -68,15 +68,16 @@ struct UnitRec {
 };
 
 __device__ __forceinline__ UnitRec unit_rec(const AttnArgs& a, int u) {
+    u = __builtin_amdgcn_readfirstlane(u);  // one record per wave: scalar loads
     const int4* r = reinterpret_cast<const int4*>(a.units + 16 * u);
     const int4 r0 = r[0], r1 = r[1], r2 = r[2];
     auto ptr = [](int lo, int hi) { return (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32); };
     UnitRec x;
-    x.kc = reinterpret_cast<const int8_t*>(ptr(r0.x, r0.y));
-    x.vc = reinterpret_cast<const int8_t*>(ptr(r0.z, r0.w));
-    x.ks = reinterpret_cast<const uint16_t*>(ptr(r1.x, r1.y));
-    x.vs = reinterpret_cast<const uint16_t*>(ptr(r1.z, r1.w));
-    x.pos = reinterpret_cast<const int32_t*>(ptr(r2.x, r2.y));
+    x.kc = gptr<const int8_t>(ptr(r0.x, r0.y));
+    x.vc = gptr<const int8_t>(ptr(r0.z, r0.w));
+    x.ks = gptr<const uint16_t>(ptr(r1.x, r1.y));
+    x.vs = gptr<const uint16_t>(ptr(r1.z, r1.w));
+    x.pos = gptr<const int32_t>(ptr(r2.x, r2.y));
     x.stride = r2.z;
     x.n = r2.w;
     x.coff = a.units[16 * u + 12];

@@ -52,17 +52,6 @@ struct QuantArgs {
     uint32_t rope_n_pos;
 };
 
-#define NQ_GLOBAL __attribute__((address_space(1)))
-
-// A device address as a pointer the compiler knows to be global memory (it is
-// made in the global address space, then cast to a generic pointer, which
-// address-space inference folds back): accesses through it compile to global
-// rather than flat instructions, and stores count on vmcnt only.
-template <class T>
-__device__ __forceinline__ T* gptr(uint64_t addr) {
-    return (T*)(NQ_GLOBAL T*)addr;
-}
-
 // ------------------------------------------------------------------ E8 ----
 
 // min(|e0|, ..., |e7|) in four min3/min instructions.  Written in asm because

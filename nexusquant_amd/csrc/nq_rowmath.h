@@ -59,6 +59,17 @@ __device__ __forceinline__ void load8f(const float* p, float* out) {
 
 typedef __fp16 half2v __attribute__((ext_vector_type(2)));
 
+#define NQ_GLOBAL __attribute__((address_space(1)))
+
+// A device address as a pointer the compiler knows to be global memory (it is
+// made in the global address space, then cast to a generic pointer, which
+// address-space inference folds back): accesses through it compile to global
+// rather than flat instructions, and stores count on vmcnt only.
+template <class T>
+__device__ __forceinline__ T* gptr(uint64_t addr) {
+    return (T*)(NQ_GLOBAL T*)addr;
+}
+
 // Quad butterfly v <- v + c * partner(v) with the partner read through DPP in
 // the same v_fmac_f32 instruction.  The DPP read of a VGPR needs two wait
 // states after the VALU write that produced it; s_nop 1 provides them for the
