@@ -197,6 +197,8 @@ def aux_workload(name, steps, warmup):
         out.update(decode_workload(name, steps, warmup))
     elif name == "rans":
         out.update(rans_workload(steps, warmup))
+    elif name == "e8mm":
+        out.update(e8mm_workload(steps, warmup))
     elif name == "merge":
         ks, vs = _aux_cache(torch, gen, dev, 32, 4, 8, 8192, 128, 10000.0, True)
         comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.25, sliding_window=32,
@@ -214,6 +216,57 @@ def aux_workload(name, steps, warmup):
     else:
         raise SystemExit(f"unknown workload {name}")
     print(json.dumps(out), flush=True)
+
+
+def e8mm_workload(steps, warmup):
+    """Fused E8 dequant + matrix product (e8_dequant_matmul) at a decode shape:
+    one Llama-3-70B layer's keys as standalone E8 codes (8 kv heads x 131072
+    tokens = 1048576 rows of 128 int8 codes, fp32 scales) against the 8 query
+    heads of a group (Q_cols 8).  Bytes are the codes, scales, query and the
+    fp32 output; HBM bound.  The CPU leg times the oracle (torch CPU, fp32
+    decode then float64 product) on 65536 rows."""
+    import torch
+    from nexusquant_amd.kernels import e8_dequant_matmul
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(13)
+    k_rows, h, qc = 8 * 131072, 128, 8
+    codes = torch.randint(-8, 9, (k_rows, h), device=dev, generator=gen, dtype=torch.int8)
+    scales = torch.rand(k_rows, device=dev, generator=gen) * 0.1 + 1e-3
+    query = torch.randn(h, qc, device=dev, generator=gen)
+    out = e8_dequant_matmul(codes, scales, query)
+    ms = _timed(torch, lambda: e8_dequant_matmul(codes, scales, query), steps, warmup) * 1e3
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_ev = max(steps, 5)
+    ev0.record(stream)
+    for _ in range(n_ev):
+        e8_dequant_matmul(codes, scales, query)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ev_ms = ev0.elapsed_time(ev1) / n_ev
+    nbytes = k_rows * h + 4 * k_rows + 4 * h * qc + 4 * k_rows * qc
+    gbs = nbytes / (ev_ms * 1e-3) / 1e9
+    from oracle import torch_ref
+    n_s = 65536
+    c_s, s_s, q_s = codes[:n_s].cpu(), scales[:n_s].cpu(), query.cpu()
+    ref = torch_ref.e8_dequant_matmul(c_s, s_s, q_s)
+    mag = (c_s.double().abs() * s_s.double()[:, None]) @ q_s.double().abs()
+    assert bool(((out[:n_s].cpu().double() - ref).abs() <= 2.0 ** -18 * mag).all())  # fp32 summation bound
+    t0 = time.perf_counter()
+    reps = 0
+    while time.perf_counter() - t0 < 2.0:
+        torch_ref.e8_dequant_matmul(c_s, s_s, q_s)
+        reps += 1
+    cpu_s = (time.perf_counter() - t0) / reps
+    return dict(config={"workload": f"e8_dequant_matmul: int8 codes [{k_rows}, {h}] (8 kv heads x 131072 tokens), "
+                        f"query [{h}, {qc}]"},
+                ms_per_step=round(ms, 4), value=round(ms, 4), ms_per_call_events=round(ev_ms, 4),
+                bytes_per_call=nbytes,
+                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                cpu_baseline={"value": round(n_s * h / cpu_s / 1e9, 4), "unit": "G codes/s",
+                              "cores": torch.get_num_threads(), "kind": "port",
+                              "sample": f"oracle (torch CPU) on {n_s} rows"})
 
 
 def rans_workload(steps, warmup):
@@ -334,7 +387,7 @@ def main():
     ap.add_argument("--workload", default="c2",
                     help="c2 (headline, default), a secondary config: c3, c4, c5a, c5b, aux (all four), "
                          "decode70b / decode7b (paged decode attention from compressed pages), rans (GPU "
-                         "entropy stage), merge (merge eviction), "
+                         "entropy stage), merge (merge eviction), e8mm (fused E8 dequant + matrix product), "
                          "or copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.workload != "c2":

@@ -416,6 +416,21 @@ int32_t nq_paged_attention_chunk_tokens(void);
 int64_t nq_paged_attention_workspace(int32_t n_chunks, int32_t q_heads, int32_t head_dim);
 int nq_paged_attention(const nq_attn_desc* desc, void* stream);
 
+/*
+ * Fused dequantize + matrix product over the standalone E8 code format:
+ * out[k, j] = sum_{h < h} (codes[k, h] * scales[k]) * query[h, j] for
+ * codes int8 [k_rows, h_pad] (row stride h_pad, 8-byte aligned; columns
+ * h .. h_pad-1 are padding and ignored), scales fp32 [k_rows], query fp32
+ * [h, q_cols] row-major and out fp32 [k_rows, q_cols].  Requires
+ * 0 < h <= h_pad <= 256 and h_pad % 8 == 0.  Computed on bf16 MFMAs with the
+ * query split into three bf16 parts: every product is exact, sums are fp32.
+ *
+ * Replaces: e8_dequant_matmul          nexusquant/kernels/e8_triton.py:613-660
+ *           e8_dequant_matmul_kernel   nexusquant/kernels/e8_triton.py:373-444
+ */
+int nq_e8_dequant_matmul(const int8_t* codes, const float* scales, const float* query, float* out, int64_t k_rows,
+                         int32_t h_pad, int32_t h, int32_t q_cols, void* stream);
+
 /* Library version and the last error message of the calling thread. */
 int nq_abi_version(void);
 const char* nq_last_error(void);

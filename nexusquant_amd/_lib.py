@@ -119,6 +119,7 @@ SIGNATURES = {
     "nq_paged_attention": ([ctypes.POINTER(AttnDesc), _P], ctypes.c_int),
     "nq_nibble_pack": ([_P, _I64, _I32, _P, _P], ctypes.c_int),
     "nq_nibble_unpack": ([_P, _I64, _I32, _I32, _P, _P], ctypes.c_int),
+    "nq_e8_dequant_matmul": ([_P, _P, _P, _P, _I64, _I32, _I32, _I32, _P], ctypes.c_int),
 }
 
 _lock = threading.Lock()

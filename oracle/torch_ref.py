@@ -29,6 +29,9 @@ Pinning (see tests/test_oracle_*.py):
   vllm_* (page caller)    golden fixtures written by the reference's
                           integrations/vllm_backend.py (compress / decompress /
                           logits / nibble packing / paged forward)
+  e8_dequant_matmul       brute-force loops on tiny inputs, identity query
+                          (= codes * scales exactly), linearity in the query
+                          (the reference's tests do not cover it)
 """
 
 from __future__ import annotations
@@ -794,3 +797,14 @@ def unpack_codes_nibble(packed: torch.Tensor, original_d: int) -> torch.Tensor:
     inter = torch.stack([p & 0xF, (p >> 4) & 0xF], dim=-1)
     shape = list(inter.shape)[:-2] + [-1]
     return (inter.reshape(shape)[..., :original_d] - 8).to(torch.int8)
+
+
+def e8_dequant_matmul(codes: torch.Tensor, scales: torch.Tensor, query: torch.Tensor) -> torch.Tensor:
+    """Fused decode + matrix product of the standalone E8 format
+    (e8_triton.py:373-444, 613-660): vals = fp32(codes[:, :H]) * scales[:, None]
+    rounded to fp32 as the reference forms them, then vals @ query accumulated in
+    float64 (the exact value the GPU's fp32 sums approximate).  codes int8 [K, H_pad],
+    query [H, Q_cols] -> float64 [K, Q_cols]."""
+    h = query.shape[0]
+    vals = codes[:, :h].to(torch.float32) * scales.to(torch.float32)[:, None]
+    return vals.to(torch.float64) @ query.to(torch.float32).to(torch.float64)
