@@ -157,6 +157,8 @@ def rans_decode(stream: RansStream, device=None) -> torch.Tensor:
         words = stream.words.to(dev)
         if words.numel() == 0:
             words = torch.zeros(1, dtype=torch.int16, device=dev)
+        if words.data_ptr() % 8:  # the kernel reads 4 words at a time
+            words = words.clone()
         offsets = stream.offsets.to(dev)
         freq_d = torch.from_numpy(stream.freq.view(np.int16).copy()).to(dev)
         with torch.cuda.device(dev):
