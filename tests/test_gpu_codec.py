@@ -80,3 +80,32 @@ def test_nqc1_container_roundtrip_and_ratio():
             assert torch.equal(out["codes"][2 * li + r].reshape(want.shape), want)
             assert np.array_equal(out["scales"][2 * li + r].reshape(-1),
                                   layers[li][r].scales.cpu().numpy().reshape(-1))
+
+
+def test_c2_shaped_layer_properties_over_every_row():
+    """One Llama-3-70B layer at full length (bf16 [1, 8, 131072, 128], K3 keys and K2
+    values): checks that hold for every row, independent of size.  The codes dequantize
+    to the fused reconstruction bit for bit; every int8 code 2p is within +-L; scales
+    are finite and non-negative; token deltas and the rANS stream round-trip exactly."""
+    from nexusquant_amd.codec import codes_int8, delta_decode, dequantize
+    from nexusquant_amd.entropy import rans_decode, rans_encode
+    from nexusquant_amd.ops import quantize_tensors
+    print("[gpu] C2-shaped layer, whole-tensor properties", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    for key, L, scale in ((True, 8, 1.0), (False, 4, 0.5)):
+        x = (torch.randn(1, 8, 131072, 128, device=DEV, generator=g) * scale).to(torch.bfloat16)
+        rec, cd = quantize_tensors([x], is_key=key, levels=L, rope_base=500000.0, codes=True)
+        rec, cd = rec[0], cd[0]
+        back = dequantize([cd], rope_base=500000.0)[0]
+        torch.cuda.synchronize()
+        same = (back.view(torch.int16) == rec.view(torch.int16)) | ((back == 0) & (rec == 0))
+        assert bool(same.all()), "dequantized codes differ from the fused reconstruction"
+        c = codes_int8([cd])[0]
+        assert int(c.abs().max()) <= L
+        assert bool(torch.isfinite(cd.scales).all() & (cd.scales >= 0).all())
+        d = codes_int8([cd], delta=True)[0]
+        assert torch.equal(delta_decode([d])[0].reshape(c.shape), c)
+        st = rans_encode(c, L)
+        assert torch.equal(rans_decode(st), c)
+        del x, rec, cd, back, c, d, st
+        torch.cuda.empty_cache()
