@@ -433,6 +433,22 @@ int nq_paged_attention(const nq_attn_desc* desc, void* stream);
 int nq_e8_dequant_matmul(const int8_t* codes, const float* scales, const float* query, float* out, int64_t k_rows,
                          int32_t h_pad, int32_t h, int32_t q_cols, void* stream);
 
+/*
+ * The relaxed-E8 rule on its own: nq_e8_nearest_point maps n_groups fp32
+ * 8-groups x to their lattice points (no clamp); nq_e8_quantize_perhead maps
+ * each of `rows` fp32 rows of length d to q * scale with scale = max(amax,
+ * 1e-8) / (levels / 2) and q the rule applied to the zero-padded 8-groups of
+ * x / scale, clamped to +-levels/2.  Integer candidate rint(x) with the first
+ * smallest-gap coordinate stepped toward x on an odd sum; half candidate
+ * rint(x - 0.5) + 0.5, chosen when its squared distance is smaller.
+ * nq_e8_nearest_point needs 16-byte aligned x and out.
+ *
+ * Replaces: E8Lattice.nearest_point / quantize_perhead   e8_lattice.py:27-69, 97-124
+ *           e8_nearest_point / e8_quantize_perhead      nexusquant/kernels/e8_triton.py:455-522
+ */
+int nq_e8_nearest_point(const float* x, float* out, int64_t n_groups, void* stream);
+int nq_e8_quantize_perhead(const float* x, float* out, int64_t rows, int32_t d, int32_t levels, void* stream);
+
 /* Library version and the last error message of the calling thread. */
 int nq_abi_version(void);
 const char* nq_last_error(void);

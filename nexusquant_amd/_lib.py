@@ -120,6 +120,8 @@ SIGNATURES = {
     "nq_nibble_pack": ([_P, _I64, _I32, _P, _P], ctypes.c_int),
     "nq_nibble_unpack": ([_P, _I64, _I32, _I32, _P, _P], ctypes.c_int),
     "nq_e8_dequant_matmul": ([_P, _P, _P, _P, _I64, _I32, _I32, _I32, _P], ctypes.c_int),
+    "nq_e8_nearest_point": ([_P, _P, _I64, _P], ctypes.c_int),
+    "nq_e8_quantize_perhead": ([_P, _P, _I64, _I32, _I32, _P], ctypes.c_int),
 }
 
 _lock = threading.Lock()

@@ -8,10 +8,13 @@ codes ``[K, H_pad]`` with one fp32 scale per row), on the library entry point
 (the query is split into three bf16 parts on the matrix cores); the
 reference's ``tl.dot`` on fp32 operands may round them to TF32 on its GPUs.
 
-The module's other exports are covered elsewhere: ``e8_nearest_point`` and
-``e8_quantize_perhead`` are the E8 rule and per-head quantization fused into
-the quantizer (``nq_quantize``).  ``e8_encode`` / ``e8_decode`` are not
-provided.
+``e8_nearest_point`` and ``e8_quantize_perhead`` (e8_triton.py:455-522, drop-ins
+for E8Lattice.nearest_point / quantize_perhead, e8_lattice.py:27-69, 97-124) run
+the reference's E8 rule on ``nq_e8_nearest_point`` / ``nq_e8_quantize_perhead``
+in fp32 and return the input's dtype, as the reference's GPU versions do.  The
+per-head path follows E8Lattice.quantize_perhead exactly (the reference's Triton
+version goes through its int8 encoder, which truncates half-integer points).
+``e8_encode`` / ``e8_decode`` are not provided.
 """
 
 from __future__ import annotations
@@ -59,3 +62,40 @@ def e8_dequant_matmul(codes: torch.Tensor, scales: torch.Tensor, query: torch.Te
                 k_rows, h_pad, h, q_cols, ctypes.c_void_p(_lib.current_stream_handle(dev)))
         _lib.check(st, "nq_e8_dequant_matmul")
     return out
+
+
+def _call(lib, name, dev, *args):
+    with torch.cuda.device(dev):
+        st = getattr(lib, name)(*args, ctypes.c_void_p(_lib.current_stream_handle(dev)))
+    _lib.check(st, name)
+
+
+def e8_nearest_point(x: torch.Tensor) -> torch.Tensor:
+    """Nearest relaxed-E8 point of every 8-group: (..., 8) -> same shape and dtype."""
+    assert x.shape[-1] == 8, "last dim must be 8"
+    lib = _lib.load()
+    _lib.require_device(x, "x")
+    shape = x.shape
+    flat = x.contiguous().view(-1, 8).float()
+    if flat.data_ptr() % 16:
+        flat = flat.clone()
+    out = torch.empty_like(flat)
+    if flat.shape[0]:
+        _call(lib, "nq_e8_nearest_point", x.device, ctypes.c_void_p(flat.data_ptr()),
+              ctypes.c_void_p(out.data_ptr()), flat.shape[0])
+    return out.view(shape).to(x.dtype)
+
+
+def e8_quantize_perhead(x: torch.Tensor, levels: int = 4) -> torch.Tensor:
+    """Per-row scale amax / (levels / 2), E8 rule on the padded 8-groups, clamp,
+    rescale: (..., head_dim) -> same shape and dtype (computed in fp32)."""
+    lib = _lib.load()
+    _lib.require_device(x, "x")
+    shape = x.shape
+    d = shape[-1]
+    flat = x.reshape(-1, d).contiguous().float()
+    out = torch.empty_like(flat)
+    if flat.numel():
+        _call(lib, "nq_e8_quantize_perhead", x.device, ctypes.c_void_p(flat.data_ptr()),
+              ctypes.c_void_p(out.data_ptr()), flat.shape[0], d, int(levels))
+    return out.reshape(shape).to(x.dtype)
