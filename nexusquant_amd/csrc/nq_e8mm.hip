@@ -34,21 +34,30 @@ struct DmmArgs {
 constexpr int kTiles = 1;          // 16-row tiles per wave and round (2 and 4 measured no faster)
 constexpr uint32_t kMaxBlocks = 1024;  // row blocks per column tile: each wave streams ~16 tiles
 
-template <int KS>
+// K slot s of lane group kq in K step ks is column h(ks, kq, s): with V16,
+// 64 (ks / 2) + 16 kq + 8 (ks % 2) + s, so a lane's two K steps of a pair read
+// 16 consecutive code bytes in one load (H_pad a multiple of 16, an even
+// number of steps); else 32 ks + 8 kq + s, 8 bytes per step.
+template <bool V16>
+__device__ __forceinline__ int kcol(int ks, int kq, int s) {
+    return V16 ? 64 * (ks >> 1) + 16 * kq + 8 * (ks & 1) + s : 32 * ks + 8 * kq + s;
+}
+
+template <int KS, bool V16>
 __global__ __launch_bounds__(256) void e8_dequant_matmul_kernel(DmmArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, kq = lane >> 4;
     const int col = (int)blockIdx.y * 16 + n;
     const bool col_ok = col < a.q_cols;
 
-    // B operands: lane l holds query rows 32 ks + 8 kq .. + 7 of column col,
+    // B operands: lane l holds query rows kcol(ks, kq, 0 .. 7) of column col,
     // as three bf16 parts (rows >= H and columns >= Q_cols are zero)
     bf16x8v qb[KS][3];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const int h = 32 * ks + 8 * kq + s;
+            const int h = kcol<V16>(ks, kq, s);
             const float x = (h < a.h && col_ok) ? a.query[(size_t)h * a.q_cols + col] : 0.0f;
             const __bf16 p0 = (__bf16)x;
             const float r1 = x - (float)p0;
@@ -64,7 +73,7 @@ __global__ __launch_bounds__(256) void e8_dequant_matmul_kernel(DmmArgs a) {
     uint2 keep[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-        const int h0 = 32 * ks + 8 * kq;
+        const int h0 = kcol<V16>(ks, kq, 0);
         uint32_t m[2] = {0u, 0u};
 #pragma unroll
         for (int b = 0; b < 8; ++b)
@@ -81,11 +90,22 @@ __global__ __launch_bounds__(256) void e8_dequant_matmul_kernel(DmmArgs a) {
         for (int u = 0; u < kTiles; ++u) {
             const int64_t row = (int64_t)(t0 + u) * 16 + n;  // A row of this lane
             const bool row_ok = row < a.k_rows;
+            if constexpr (V16) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const int h0 = 32 * ks + 8 * kq;
-                w[u][ks] = make_uint2(0u, 0u);
-                if (row_ok && h0 < a.h_pad) w[u][ks] = *reinterpret_cast<const uint2*>(a.codes + row * a.h_pad + h0);
+                for (int ks = 0; ks < KS; ks += 2) {
+                    const int h0 = kcol<true>(ks, kq, 0);  // 16 bytes: steps ks and ks + 1
+                    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+                    if (row_ok && h0 < a.h_pad) v = *reinterpret_cast<const uint4*>(a.codes + row * a.h_pad + h0);
+                    w[u][ks] = make_uint2(v.x, v.y);
+                    if (ks + 1 < KS) w[u][ks + 1] = make_uint2(v.z, v.w);
+                }
+            } else {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int h0 = kcol<false>(ks, kq, 0);
+                    w[u][ks] = make_uint2(0u, 0u);
+                    if (row_ok && h0 < a.h_pad) w[u][ks] = *reinterpret_cast<const uint2*>(a.codes + row * a.h_pad + h0);
+                }
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -121,6 +141,17 @@ __global__ __launch_bounds__(256) void e8_dequant_matmul_kernel(DmmArgs a) {
     }
 }
 
+template <int KS>
+static void launch_e8mm(bool v16, dim3 grid, hipStream_t s, const DmmArgs& a) {
+    if constexpr (KS % 2 == 0) {
+        if (v16) {
+            hipLaunchKernelGGL((e8_dequant_matmul_kernel<KS, true>), grid, dim3(256), 0, s, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((e8_dequant_matmul_kernel<KS, false>), grid, dim3(256), 0, s, a);
+}
+
 }  // namespace nq
 
 extern "C" int nq_e8_dequant_matmul(const int8_t* codes, const float* scales, const float* query, float* out,
@@ -154,17 +185,21 @@ extern "C" int nq_e8_dequant_matmul(const int8_t* codes, const float* scales, co
     const uint32_t cap = kMaxBlocks / col_tiles > 0 ? kMaxBlocks / col_tiles : 1u;
     if (row_blocks > cap) row_blocks = cap;
     const dim3 grid(row_blocks, col_tiles);
-    const int ks = (h + 31) / 32;
+    int ks = (h + 31) / 32;
+    // 16-byte code loads when every row starts 16-byte aligned; their K steps
+    // come in pairs, so the count rounds up to even (columns >= H are masked)
+    const bool v16 = h_pad % 16 == 0 && ((uintptr_t)codes & 15) == 0;
+    if (v16) ks = (ks + 1) & ~1;
     hipStream_t s = (hipStream_t)stream;
     switch (ks) {
-        case 1: hipLaunchKernelGGL(e8_dequant_matmul_kernel<1>, grid, dim3(256), 0, s, a); break;
-        case 2: hipLaunchKernelGGL(e8_dequant_matmul_kernel<2>, grid, dim3(256), 0, s, a); break;
-        case 3: hipLaunchKernelGGL(e8_dequant_matmul_kernel<3>, grid, dim3(256), 0, s, a); break;
-        case 4: hipLaunchKernelGGL(e8_dequant_matmul_kernel<4>, grid, dim3(256), 0, s, a); break;
-        case 5: hipLaunchKernelGGL(e8_dequant_matmul_kernel<5>, grid, dim3(256), 0, s, a); break;
-        case 6: hipLaunchKernelGGL(e8_dequant_matmul_kernel<6>, grid, dim3(256), 0, s, a); break;
-        case 7: hipLaunchKernelGGL(e8_dequant_matmul_kernel<7>, grid, dim3(256), 0, s, a); break;
-        default: hipLaunchKernelGGL(e8_dequant_matmul_kernel<8>, grid, dim3(256), 0, s, a); break;
+        case 1: launch_e8mm<1>(false, grid, s, a); break;
+        case 2: launch_e8mm<2>(v16, grid, s, a); break;
+        case 3: launch_e8mm<3>(false, grid, s, a); break;
+        case 4: launch_e8mm<4>(v16, grid, s, a); break;
+        case 5: launch_e8mm<5>(false, grid, s, a); break;
+        case 6: launch_e8mm<6>(v16, grid, s, a); break;
+        case 7: launch_e8mm<7>(false, grid, s, a); break;
+        default: launch_e8mm<8>(v16, grid, s, a); break;
     }
     NQ_CHECK_HIP(hipGetLastError());
     return NQ_OK;
