@@ -390,15 +390,16 @@ def main():
                          "entropy stage), merge (merge eviction), e8mm (fused E8 dequant + matrix product), "
                          "or copy (HBM counter calibration)")
     args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the compression path is data-parallel per layer "
+              "and head (each GPU would run the same kernels on its own layers or heads, with no "
+              "communication for quant_only), and this build runs on single-GPU boxes.",
+              file=sys.stderr)
+        sys.exit(2)
     if args.workload != "c2":
         for w in (["c3", "c4", "c5a", "c5b"] if args.workload == "aux" else [args.workload]):
             aux_workload(w, args.steps, args.warmup)
         return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the compression path is data-parallel per layer "
-              "and head, and this build runs on single-GPU boxes (see DESIGN.md, sharding).",
-              file=sys.stderr)
-        sys.exit(2)
 
     import torch
     from nexusquant_amd import ops
