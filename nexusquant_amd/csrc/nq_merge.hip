@@ -21,6 +21,8 @@ namespace nq {
 constexpr int kMT = 64;     // tile rows (evicted) and columns (kept)
 constexpr int kMPad = 4;    // LDS row padding (floats)
 
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+
 template <int DT>
 __device__ __forceinline__ float load_elem(const void* p, size_t i) {
     if constexpr (DT == NQ_F32) return static_cast<const float*>(p)[i];
@@ -181,7 +183,8 @@ __global__ __launch_bounds__(1024) void merge_evicted_kernel(const uint8_t* keep
 }
 
 // 3. best kept token per evicted token over one split of the kept range:
-//    block (row, evicted tile, split); thread (ty, tx) owns rows 4ty.., cols 4tx..
+//    block (row, evicted tile, split), 64 x 64 tiles staged in LDS; wave w takes
+//    the 32 x 32 quarter (w / 2, w % 2) on the fp32 32x32x2 MFMA.
 struct AssignArgs {
     const float* unit;      // [b, s, d]
     const int32_t* ev_idx;  // [b, s]
@@ -206,21 +209,22 @@ __global__ __launch_bounds__(256) void merge_assign_kernel(AssignArgs a) {
     const int k_begin = split * a.split_len;
     const int k_end = k_begin + a.split_len < nk ? k_begin + a.split_len : nk;
     if (e0 >= ne || k_begin >= k_end) return;  // whole block
-    const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int we = wave >> 1, wk = wave & 1;  // this wave: evicted rows 32 we .., kept columns 32 wk .. of a tile
+    const int c = lane & 31, g = lane >> 5;
     const float* U = a.unit + (size_t)bi * a.s * D;
-    float bv[4];
-    int bidx[4];
+    // running first maximum per row over this wave's columns: lane (c, g), value v
+    // holds row 8 (v / 4) + 4 g + v % 4 of the wave's 32 (all 32 lanes of a g agree)
+    float bv[16];
+    int bidx[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        bv[i] = -__builtin_inff();
-        bidx[i] = k_begin;
+    for (int v = 0; v < 16; ++v) {
+        bv[v] = -__builtin_inff();
+        bidx[v] = k_begin;
     }
     for (int k0 = k_begin; k0 < k_end; k0 += kMT) {
-        float acc[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+        f32x16v acc = {};
         for (int dc = 0; dc < D; dc += DC) {
             __syncthreads();
             // rows past ne / k_end repeat the last valid row; their results are dropped
@@ -236,60 +240,60 @@ __global__ __launch_bounds__(256) void merge_assign_kernel(AssignArgs a) {
                     *reinterpret_cast<const float4*>(U + (size_t)pk * D + dc + 4 * c4);
             }
             __syncthreads();
-            for (int kk = 0; kk < DC; kk += 4) {
-                float4 ev[4], kv[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) ev[i] = *reinterpret_cast<const float4*>(&s_e[4 * ty + i][kk]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) kv[j] = *reinterpret_cast<const float4*>(&s_k[4 * tx + j][kk]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        acc[i][j] = __builtin_fmaf(ev[i].x, kv[j].x, acc[i][j]);
-                        acc[i][j] = __builtin_fmaf(ev[i].y, kv[j].y, acc[i][j]);
-                        acc[i][j] = __builtin_fmaf(ev[i].z, kv[j].z, acc[i][j]);
-                        acc[i][j] = __builtin_fmaf(ev[i].w, kv[j].w, acc[i][j]);
-                    }
-            }
+            // fp32 MFMA 32x32x2: A[i][k] = evicted row 32 we + i, B[k][j] = kept row 32 wk + j
+            const float* ea = &s_e[32 * we + c][g];
+            const float* kb = &s_k[32 * wk + c][g];
+#pragma unroll 8
+            for (int kk = 0; kk < DC; kk += 2)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ea[kk], kb[kk], acc, 0, 0, 0);
         }
-        // best of this tile per row: own 4 columns, then the 16 lanes of the row group
+        // best of this tile per row over the wave's 32 columns (first index on ties)
+        const int col = k0 + 32 * wk + c;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float v = -__builtin_inff();
-            int idx = 0x7fffffff;
+        for (int v = 0; v < 16; ++v) {
+            float x = col < k_end ? acc[v] : -__builtin_inff();
+            int idx = col < k_end ? col : 0x7fffffff;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int k = k0 + 4 * tx + j;
-                if (k < k_end && acc[i][j] > v) {
-                    v = acc[i][j];
-                    idx = k;
-                }
-            }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                const float ov = __shfl_xor(v, o, 64);
+            for (int o = 1; o < 32; o <<= 1) {
+                const float ox = __shfl_xor(x, o, 64);
                 const int oi = __shfl_xor(idx, o, 64);
-                if (ov > v || (ov == v && oi < idx)) {
-                    v = ov;
+                if (ox > x || (ox == x && oi < idx)) {
+                    x = ox;
                     idx = oi;
                 }
             }
-            if (v > bv[i]) {  // strict: an earlier tile keeps ties
-                bv[i] = v;
-                bidx[i] = idx;
+            if (x > bv[v]) {  // strict: an earlier tile keeps ties
+                bv[v] = x;
+                bidx[v] = idx;
             }
         }
     }
-    if (tx == 0) {
+    // the two column halves of each row: larger value, then the lower index
+    __shared__ float s_bv[2][kMT];
+    __shared__ int s_bi[2][kMT];
+    if (c == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = e0 + 4 * ty + i;
-            if (e < ne) {
-                const size_t o = ((size_t)bi * a.s + e) * a.n_split + split;
-                a.best_val[o] = bv[i];
-                a.best_idx[o] = bidx[i];
+        for (int v = 0; v < 16; ++v) {
+            const int r = 32 * we + 8 * (v >> 2) + 4 * g + (v & 3);
+            s_bv[wk][r] = bv[v];
+            s_bi[wk][r] = bidx[v];
+        }
+    }
+    __syncthreads();
+    if (tid < kMT) {
+        const int e = e0 + tid;
+        if (e < ne) {
+            float x = s_bv[0][tid];
+            int idx = s_bi[0][tid];
+            const float x1 = s_bv[1][tid];
+            const int i1 = s_bi[1][tid];
+            if (x1 > x || (x1 == x && i1 < idx)) {
+                x = x1;
+                idx = i1;
             }
+            const size_t o = ((size_t)bi * a.s + e) * a.n_split + split;
+            a.best_val[o] = x;
+            a.best_idx[o] = idx;
         }
     }
 }
