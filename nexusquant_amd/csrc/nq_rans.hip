@@ -70,34 +70,50 @@ struct RansArgs {
 // right end is 8-byte aligned
 __host__ __device__ __forceinline__ int64_t rans_stride(int chunk) { return ((int64_t)chunk + 2 + 3) & ~(int64_t)3; }
 
-// x / d for x < d * 2^20, d in [1, 4096]: the fp32 quotient is within 1 of the
-// true one, and one remainder test corrects it
-__device__ __forceinline__ uint32_t rans_div(uint32_t x, uint32_t d, float rcp, uint32_t& r) {
-    uint32_t q = (uint32_t)((float)x * rcp);
-    int32_t rem = (int32_t)(x - q * d);
-    if (rem < 0) {
-        --q;
-        rem += (int32_t)d;
-    } else if (rem >= (int32_t)d) {
-        ++q;
-        rem -= (int32_t)d;
-    }
-    r = (uint32_t)rem;
-    return q;
+// One lane per chunk, one wave per block (so the chunks spread over every CU).
+// A chunk is a chain of dependent state updates, so its time is the chain's
+// latency per symbol: nothing but the update itself may sit on it.
+//  - The codes of a whole chunk whose length is a multiple of 128 are read
+//    128 at a time (eight 16-byte loads per lane), one group ahead, from the
+//    chunk's end backwards; other chunks read 16 at a time.
+//  - For every 16 codes, all 16 table entries (f, cf, 1/f, and the renorm
+//    bound f * 2^20 - 1) are looked up before the first of them is coded, so
+//    no LDS latency lies on the chain.
+//  - Emitted words collect in a 64-bit buffer and leave in 8-byte stores;
+//    nothing inside a group of 128 waits on memory.
+// Per-symbol encoder constants.  rcp is 1/f rounded up in fp64: for x < f 2^20
+// it gives q = trunc(x * rcp) = floor(x / f) exactly (x * rcp exceeds x / f by
+// at most 2^-32, less than the 1/f gap to the next integer, and the rounded
+// product stays below it), so the update q M + (x - q f) + cf is
+// q (M - f) + x + cf with a 24-bit multiply and no correction.
+struct __attribute__((aligned(16))) RansEnc {
+    uint32_t xmax, mmf, cf, pad;  // renorm bound f 2^20 - 1, M - f, cumulative frequency
+    double rcp;
+    double pad2;
+};
+
+__device__ __forceinline__ double rcp_up(uint32_t f) {
+    double r = 1.0 / (double)f;
+    if (__builtin_fma(r, (double)f, -1.0) < 0.0) r = __longlong_as_double(__double_as_longlong(r) + 1);
+    return r;
 }
 
-// One lane per chunk, one wave per block (so the chunks spread over every CU).
-// Codes are read 16 at a time from the chunk's end backwards; emitted words
-// collect in a 64-bit buffer and leave in 8-byte stores.
 __global__ __launch_bounds__(64) void rans_encode_kernel(RansArgs a) {
-    __shared__ uint32_t fc[kRansMaxAlpha];  // f | cf << 16
-    __shared__ float rcp[kRansMaxAlpha];
+    __shared__ RansEnc tab[kRansMaxAlpha];
     if (threadIdx.x == 0) {
         uint32_t acc = 0;
         for (int s = 0; s < a.alphabet; ++s) {
             const uint32_t f = a.freq[s];
-            fc[s] = f | (acc << 16);
-            rcp[s] = f ? 1.0f / (float)f : 0.0f;
+            RansEnc e;
+            // state >= f * 2^20 as a 32-bit test: f * 2^20 - 1 wraps to 2^32 - 1
+            // at f = 4096 (never renormalise); f = 0 (not valid input) gives 0
+            e.xmax = f ? (f << 20) - 1u : 0u;
+            e.mmf = kRansM - f;
+            e.cf = acc;
+            e.pad = 0;
+            e.rcp = f ? rcp_up(f) : 0.0;
+            e.pad2 = 0.0;
+            tab[s] = e;
             acc += f;
         }
     }
@@ -109,64 +125,123 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(RansArgs a) {
     uint16_t* const end = a.scratch + (ch + 1) * rans_stride(a.chunk);
     uint16_t* out = end;  // next 4-word group goes just below
     uint64_t buf = 0;
-    int nbuf = 0;
-    uint32_t n_emit = 0;
-    auto emit = [&](uint32_t wd) {
-        buf = (buf << 16) | wd;
-        ++n_emit;
-        if (++nbuf == 4) {
+    uint32_t nbuf = 0;
+    uint32_t state = kRansL;
+    // rans_symbol without a branch: byte k of the word, arithmetically shifted
+    // right by 1 when there are no half-integer points, plus L or L / 2
+    const int sym_shift = a.has_half ? 24 : 25;
+    const int sym_off = a.has_half ? a.L : a.L / 2;
+    auto lookup = [&](uint32_t word, int k) -> RansEnc {
+        int s = ((int)(word << (24 - 8 * k)) >> sym_shift) + sym_off;
+        s = min(max(s, 0), a.alphabet - 1);  // codes outside [-L, L] are not valid input
+        return tab[s];
+    };
+    auto code_one = [&](const RansEnc& e) {
+        // at most one word: state >> 16 < 2^16 <= f << 20
+        const bool ren = state > e.xmax;
+        const uint32_t wd = state & 0xffffu;
+        state = ren ? state >> 16 : state;
+        const uint32_t q = (uint32_t)((double)state * e.rcp);  // floor(state / f), q < 2^20
+        state = __umul24(q, e.mmf) + state + e.cf;             // q (M - f) < 2^32
+        // off the chain: the word joins the buffer, a full buffer leaves
+        buf = ren ? (buf << 16) | wd : buf;
+        nbuf += ren ? 1u : 0u;
+        if (nbuf == 4) {
             out -= 4;
             *reinterpret_cast<uint64_t*>(out) = buf;
             nbuf = 0;
         }
     };
-    uint32_t state = kRansL;
-    auto code_one = [&](int8_t c) {
-        int s = rans_symbol(c, a.L, a.has_half);
-        s = s < 0 ? 0 : (s >= a.alphabet ? a.alphabet - 1 : s);  // codes outside [-L, L] are not valid input
-        const uint32_t e = fc[s];
-        const uint32_t fs = e & 0xffffu, cs = e >> 16;
-        if ((uint64_t)state >= ((uint64_t)fs << 20)) {  // at most one word: state >> 16 < 2^16 <= fs << 20
-            emit(state & 0xffffu);
-            state >>= 16;
-        }
-        uint32_t r;
-        const uint32_t q = rans_div(state, fs, rcp[s], r);
-        state = q * kRansM + r + cs;
-    };
-    // 16-byte blocks [b, b + 16) from the one holding c1 - 1 down to the one holding c0
-    int64_t b = ((c1 - 1) / 16) * 16;
-    auto load_block = [&](int64_t bb) {
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (bb + 16 <= a.n) {
-            v = *reinterpret_cast<const uint4*>(a.codes + bb);
-        } else {  // the array's last, partial block
-            uint8_t t[16] = {};
-            for (int k = 0; k < 16 && bb + k < a.n; ++k) t[k] = (uint8_t)a.codes[bb + k];
-            v = *reinterpret_cast<const uint4*>(t);
-        }
-        return v;
-    };
-    uint4 cur = load_block(b);
-    for (; b + 16 > c0; b -= 16) {
-        const uint4 nxt = b - 16 >= 0 && b - 16 + 16 > c0 ? load_block(b - 16) : make_uint4(0u, 0u, 0u, 0u);
-        const uint32_t wv[4] = {cur.x, cur.y, cur.z, cur.w};
-        const int k_hi = (int)((c1 - 1 < b + 15 ? c1 - 1 : b + 15) - b);
-        const int k_lo = (int)((c0 > b ? c0 : b) - b);
-        if (k_hi == 15 && k_lo == 0) {
+    // the 16 codes of one 16-byte block, highest first
+    auto code16 = [&](uint4 v) {
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+        RansEnc e[16];
 #pragma unroll
-            for (int k = 15; k >= 0; --k) code_one((int8_t)(wv[k >> 2] >> (8 * (k & 3))));
-        } else {
-            for (int k = k_hi; k >= k_lo; --k) code_one((int8_t)(wv[k >> 2] >> (8 * (k & 3))));
+        for (int k = 0; k < 16; ++k) e[k] = lookup(wv[k >> 2], k & 3);
+#pragma unroll
+        for (int k = 15; k >= 0; --k) code_one(e[k]);
+    };
+    if (a.chunk % 128 == 0 && c1 - c0 == a.chunk) {
+        const uint4* p = reinterpret_cast<const uint4*>(a.codes + c0);
+        int sb = a.chunk / 128 - 1;
+        uint4 cur[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            cur[j] = p[8 * sb + j];
+            // keeps the first group's loads apart from the loop's, so they are not
+            // merged into one load at the loop top
+            asm("" : "+v"(cur[j].x), "+v"(cur[j].y), "+v"(cur[j].z), "+v"(cur[j].w));
         }
-        cur = nxt;
+        // the table entries of the next 16 codes are looked up between the
+        // current 16 codes' chain steps, where they fill its dependency stalls
+        RansEnc e[16];
+        {
+            const uint32_t wv[4] = {cur[7].x, cur[7].y, cur[7].z, cur[7].w};
+#pragma unroll
+            for (int k = 0; k < 16; ++k) e[k] = lookup(wv[k >> 2], k & 3);
+        }
+        for (; sb >= 0; --sb) {
+            const int nb = sb > 0 ? sb - 1 : 0;  // the last pass reloads group 0 (in bounds, unused)
+            uint4 nxt[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) nxt[j] = p[8 * nb + j];
+#pragma unroll
+            for (int j = 7; j >= 0; --j) {
+                const uint4 nv = j > 0 ? cur[j - 1] : nxt[7];
+                const uint32_t nw[4] = {nv.x, nv.y, nv.z, nv.w};
+                RansEnc en[16];
+#pragma unroll
+                for (int k = 15; k >= 0; --k) {
+                    code_one(e[k]);
+                    en[k] = lookup(nw[k >> 2], k & 3);
+                }
+#pragma unroll
+                for (int k = 0; k < 16; ++k) e[k] = en[k];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
+        }
+    } else {
+        // 16-byte blocks [b, b + 16) from the one holding c1 - 1 down to the one holding c0
+        auto load_block = [&](int64_t bb) {
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (bb + 16 <= a.n) {
+                v = *reinterpret_cast<const uint4*>(a.codes + bb);
+            } else {  // the array's last, partial block
+                uint8_t t[16] = {};
+                for (int k = 0; k < 16 && bb + k < a.n; ++k) t[k] = (uint8_t)a.codes[bb + k];
+                v = *reinterpret_cast<const uint4*>(t);
+            }
+            return v;
+        };
+        int64_t b = ((c1 - 1) / 16) * 16;
+        uint4 cur = load_block(b);
+        for (; b + 16 > c0; b -= 16) {
+            const uint4 nxt = b - 16 >= 0 && b - 16 + 16 > c0 ? load_block(b - 16) : make_uint4(0u, 0u, 0u, 0u);
+            const int k_hi = (int)((c1 - 1 < b + 15 ? c1 - 1 : b + 15) - b);
+            const int k_lo = (int)((c0 > b ? c0 : b) - b);
+            if (k_hi == 15 && k_lo == 0) {
+                code16(cur);
+            } else {
+                const uint32_t wv[4] = {cur.x, cur.y, cur.z, cur.w};
+                for (int k = k_hi; k >= k_lo; --k) code_one(lookup(wv[k >> 2], k & 3));
+            }
+            cur = nxt;
+        }
     }
-    emit(state & 0xffffu);
-    emit(state >> 16);
+    // the final state, high word last (the decoder reads it first)
+    for (int k = 0; k < 2; ++k) {
+        buf = (buf << 16) | (k ? state >> 16 : state & 0xffffu);
+        if (++nbuf == 4) {
+            out -= 4;
+            *reinterpret_cast<uint64_t*>(out) = buf;
+            nbuf = 0;
+        }
+    }
     // the last 0..3 words, just below the stored groups: the earliest emitted
     // (the buffer's highest) at the highest address
-    for (int k = 0; k < nbuf; ++k) out[-1 - k] = (uint16_t)(buf >> (16 * (nbuf - 1 - k)));
-    a.n_words[ch] = n_emit;
+    for (uint32_t k = 0; k < nbuf; ++k) out[-1 - (int)k] = (uint16_t)(buf >> (16 * (nbuf - 1 - k)));
+    a.n_words[ch] = (uint32_t)(end - out) + nbuf;
 }
 
 // copy each chunk's right-aligned words to its compacted offset; one wave per chunk
@@ -182,15 +257,31 @@ __global__ __launch_bounds__(256) void rans_compact_kernel(const uint16_t* scrat
     for (uint32_t i = lane; i < nw; i += 64) dst[i] = src[i];
 }
 
-// One lane per chunk, one wave per block.  A 4096-entry LDS table maps a slot
-// to code byte | (slot - cf[s]) << 8 | (f[s] - 1) << 20 for its symbol s.  A
-// symbol needs at most one word (the state is >= 16 before renormalisation);
-// words are read 4 at a time (aligned 8-byte loads inside the stream, single
-// words at its very end), and decoded codes leave 16 at a time when the
-// chunk's start is 16-aligned.
+// One lane per chunk, one wave per block.  Two 4096-entry LDS tables map a
+// slot to f[s] | (slot - cf[s]) << 13 and to the code byte of its symbol s.  A
+// symbol needs at most one word (the state is >= 16 before renormalisation).
+// The chain per symbol is one table read and a multiply-add; everything else
+// is kept off it:
+//  - each lane's stream words pass through a private 64-word ring in LDS.  At
+//    the start of every 16 symbols a lane writes the 16 words it loaded one
+//    step earlier and, if fewer than 32 unread words remain, loads the next
+//    16, so no load is waited on inside a step and the ring always holds the
+//    (at most 16) words a step reads;
+//  - the word a renormalisation would take is read from the ring alongside
+//    the table entry, before it is known to be needed;
+//  - 16 decoded codes leave in one 16-byte store, issued a step late so that
+//    the next wait on loads does not also wait for it.
+constexpr int kRingStride = 34;  // dwords per lane: 64 words + 4 bytes, 8-byte aligned rows
+// the ring is written in 8-byte groups and read in 16-bit words: both through
+// may_alias types, so the compiler keeps every read after the writes it follows
+typedef uint16_t __attribute__((may_alias)) ring_word_t;
+typedef uint64_t __attribute__((may_alias)) ring_group_t;
+
 __global__ __launch_bounds__(64) void rans_decode_kernel(RansArgs a) {
     __shared__ uint32_t tab[kRansM];
+    __shared__ uint8_t code_of[kRansM];
     __shared__ uint16_t cf[kRansMaxAlpha + 1];
+    __shared__ __attribute__((aligned(8))) uint32_t ring_all[64 * kRingStride];
     if (threadIdx.x == 0) {
         uint32_t acc = 0;
         for (int s = 0; s < a.alphabet; ++s) {
@@ -202,9 +293,12 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(RansArgs a) {
     __syncthreads();
     for (int s = 0; s < a.alphabet; ++s) {
         const uint32_t lo = cf[s], hi = cf[s + 1] < kRansM ? cf[s + 1] : kRansM;
-        const uint32_t code = (uint8_t)rans_code(s, a.L, a.has_half);
-        const uint32_t fm1 = (hi > lo ? hi - lo : 1u) - 1u;
-        for (uint32_t k = lo + threadIdx.x; k < hi; k += 64) tab[k] = code | ((k - lo) << 8) | (fm1 << 20);
+        const uint8_t code = (uint8_t)rans_code(s, a.L, a.has_half);
+        const uint32_t f = hi > lo ? hi - lo : 1u;  // f <= 4096: 13 bits
+        for (uint32_t k = lo + threadIdx.x; k < hi; k += 64) {
+            tab[k] = f | ((k - lo) << 13);
+            code_of[k] = code;
+        }
     }
     __syncthreads();
     const int64_t ch = (int64_t)blockIdx.x * 64 + threadIdx.x;
@@ -214,47 +308,82 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(RansArgs a) {
     const uint64_t w0 = a.offset[ch];
     const uint32_t len = (uint32_t)(a.offset[ch + 1] - w0);
     const uint64_t total = a.offset[a.n_chunks];
-    // sequential word reader: gbuf holds the next gleft words of the aligned
-    // 4-word group starting at word g (groups past the stream's end read as 0)
-    auto load_group = [&](uint64_t g) -> uint64_t {
+    // words are numbered from g0, the 4-aligned word at or below the chunk's
+    // first; 4-word group k holds words 4k .. 4k + 3 and sits in ring slots
+    // 4 (k % 16) ..
+    const uint64_t g0 = w0 & ~(uint64_t)3;
+    uint32_t* const ring = ring_all + threadIdx.x * kRingStride;
+    const ring_word_t* const ring16 = reinterpret_cast<const ring_word_t*>(ring);
+    auto load_group = [&](uint32_t k) -> uint64_t {  // groups past the stream's end read as 0
+        const uint64_t g = g0 + 4ull * k;
         if (g + 4 <= total) return *reinterpret_cast<const uint64_t*>(a.words + g);
         uint64_t v = 0;
-        for (uint64_t k = 0; g + k < total; ++k) v |= (uint64_t)a.words[g + k] << (16 * k);
+        for (uint64_t j = 0; g + j < total; ++j) v |= (uint64_t)a.words[g + j] << (16 * j);
         return v;
     };
-    uint64_t g = w0 & ~(uint64_t)3;
-    uint64_t gbuf = load_group(g) >> (16 * (uint32_t)(w0 & 3));
-    uint32_t gleft = 4u - (uint32_t)(w0 & 3);
-    auto next_word = [&]() -> uint32_t {
-        if (gleft == 0) {
-            g += 4;
-            gbuf = load_group(g);
-            gleft = 4;
-        }
-        const uint32_t v = (uint32_t)gbuf & 0xffffu;
-        gbuf >>= 16;
-        --gleft;
-        return v;
-    };
-    uint32_t pos = 2;
+    auto put_group = [&](uint32_t k, uint64_t v) { *reinterpret_cast<ring_group_t*>(ring + 2 * (k & 15u)) = v; };
+    uint32_t written = 8;  // groups in the ring: the first 8, all loads issued before the first write
+    {
+        uint64_t first[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) first[k] = load_group(k);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) put_group(k, first[k]);
+    }
+    uint32_t rpos = (uint32_t)(w0 & 3);   // next word to read
+    const uint32_t rend = rpos + len;     // one past the chunk's last word
     uint32_t state = kRansL;
     if (len >= 2) {
-        const uint32_t hi = next_word();
-        state = (hi << 16) | next_word();
+        state = ((uint32_t)ring16[rpos] << 16) | ring16[rpos + 1];
+        rpos += 2;
     }
+    uint32_t nw = ring16[rpos & 63u];  // the word a renormalisation takes next
+    // renormalise below lim: 2^16 while the chunk has words left, else never
+    uint32_t lim = rpos < rend ? kRansL : 0u;
+    // opaque to the compiler, which would otherwise split state < lim back into
+    // two tests joined by a scalar AND on the chain
+    auto set_lim = [&]() {
+        lim = rpos < rend ? kRansL : 0u;
+        asm("" : "+v"(lim));
+    };
     auto step = [&]() -> uint32_t {
-        const uint32_t e = tab[state & (kRansM - 1u)];
-        state = ((e >> 20) + 1u) * (state >> 12) + ((e >> 8) & 0xfffu);
-        if (state < kRansL && pos < len) {
-            state = (state << 16) | next_word();
-            ++pos;
+        const uint32_t slot = state & (kRansM - 1u);
+        const uint32_t e = tab[slot];
+        const uint32_t code = code_of[slot];
+        state = __umul24(e & 0x1fffu, state >> 12) + (e >> 13);  // f (state >> 12) + slot - cf
+        const bool need = state < lim;
+        state = need ? (state << 16) | nw : state;
+        rpos += need ? 1u : 0u;
+        set_lim();
+        nw = ring16[rpos & 63u];
+        return code;
+    };
+    uint64_t pf[4];        // groups loaded for the next step
+    bool inflight = false;
+    auto refill = [&]() {
+        if (inflight) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) put_group(written + j, pf[j]);
+            written += 4;
+            inflight = false;
+            nw = ring16[rpos & 63u];  // its slot may have just been written
         }
-        return e & 0xffu;
+    };
+    auto prefetch = [&]() {
+        if (4 * written - rpos < 32) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pf[j] = load_group(written + j);
+            inflight = true;
+        }
     };
     int8_t* out = a.out_codes + c0;
     uint32_t i = 0;
     if ((((uintptr_t)out) & 15) == 0) {
+        uint4 prev = make_uint4(0u, 0u, 0u, 0u);
         for (; i + 16 <= n_sym; i += 16) {
+            refill();
+            if (i) *reinterpret_cast<uint4*>(out + i - 16) = prev;
+            prefetch();
             uint32_t ob[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -264,13 +393,25 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(RansArgs a) {
                 v |= step() << 24;
                 ob[q] = v;
             }
-            *reinterpret_cast<uint4*>(out + i) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
+            prev = make_uint4(ob[0], ob[1], ob[2], ob[3]);
         }
+        if (i) *reinterpret_cast<uint4*>(out + i - 16) = prev;
     }
-    for (; i < n_sym; ++i) out[i] = (int8_t)step();
+    // the rest one code at a time; every 16 codes the ring is topped up to at
+    // least 16 unread words first
+    for (; i < n_sym; ++i) {
+        if ((i & 15u) == 0) {
+            refill();
+            if (4 * written - rpos < 16) {
+                prefetch();
+                refill();
+            }
+        }
+        out[i] = (int8_t)step();
+    }
 }
 
-// exclusive scan of n_words into offset[0..n_chunks]: one block; per round
+// exclusive scan of n_words into offset[0..n_chunks]: one block; per pass
 // every thread sums 32 consecutive counts, one block-wide scan of the 1024
 // sums, then every thread writes its 32 offsets
 __global__ __launch_bounds__(1024) void rans_scan_kernel(const uint32_t* n_words, int64_t n_chunks, uint64_t* offset) {

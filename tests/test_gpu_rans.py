@@ -28,7 +28,7 @@ def test_single_chunk_equals_reference_words(golden, tag):
 
 
 @pytest.mark.parametrize("levels,n,chunk", [(8, 1_000_003, 4096), (4, 262_144, 1024), (16, 70_000, 4096),
-                                            (2, 4096, 4096), (8, 1, 4096)])
+                                            (2, 4096, 4096), (8, 1, 4096), (4, 50_001, 1000), (8, 40_000, 200)])
 def test_chunked_roundtrip_and_chunk_words(levels, n, chunk):
     from nexusquant_amd.entropy import pack_nqr1, rans_decode, rans_encode, shannon_bits, unpack_nqr1
     from nexusquant_amd.ops import quantize_tensors
@@ -56,3 +56,30 @@ def test_chunked_roundtrip_and_chunk_words(levels, n, chunk):
     st2, sc = unpack_nqr1(blob, shape=codes.shape, device=DEV)
     assert torch.equal(rans_decode(st2), codes)
     assert torch.equal(sc, cd[0].scales.cpu().reshape(-1))
+
+
+@pytest.mark.parametrize("case", ["constant", "rare", "runs"])
+def test_skewed_streams_roundtrip_and_chunk_words(case):
+    """Streams with long stretches of no renormalisation (one symbol at
+    probability 1, or nearly): the decoder's word ring stays full and the
+    encoder emits little but the final states."""
+    from nexusquant_amd.entropy import rans_decode, rans_encode
+    print(f"[gpu] rans skewed {case}", flush=True)
+    rng = np.random.default_rng(5)
+    n, chunk, levels = 300_000, 4096, 4
+    c = np.zeros(n, np.int8)
+    if case == "rare":
+        hit = rng.random(n) < 0.003
+        c[hit] = rng.choice(np.array([-4, -2, 2, 4], np.int8), hit.sum())
+    elif case == "runs":
+        for s0 in range(0, n, 20_000):  # dense bursts between long constant runs
+            c[s0:s0 + 3000] = rng.choice(np.array([-4, -2, 0, 2, 4], np.int8), 3000)
+    codes = torch.from_numpy(c).to(DEV)
+    st = rans_encode(codes, levels, chunk=chunk)
+    assert torch.equal(rans_decode(st), codes)
+    sym = c.astype(np.int32) // 2 + levels // 2
+    offs = st.offsets.cpu().numpy()
+    words = st.words.cpu().numpy().view(np.uint16)
+    for k in sorted({0, 1, 5, len(offs) - 2}):
+        want = R.rans_encode(sym[k * chunk:(k + 1) * chunk], st.freq)
+        assert np.array_equal(words[offs[k]:offs[k + 1]], np.array(want, np.uint16))
