@@ -30,11 +30,20 @@ __device__ __forceinline__ int hist_bin(int8_t c, int L) {
     return b < 0 ? 0 : (b > 2 * L ? 2 * L : b);  // codes outside [-L, L] are not valid input
 }
 
-// histogram of c + L over [0, 2L] (the host folds it when no code is odd)
+// histogram of c + L over [0, 2L] (the host folds it when no code is odd).
+// Lattice codes are peaked around 0, so a wave's 64 lanes mostly hit a few
+// bins: each of 16 lane groups (lane % 16) counts into its own copy of the
+// bins, so at most 4 lanes of a wave meet on one address, and the copies are
+// 65 words apart so that equal bins of different copies sit in different banks.
+// (One copy per lane measured the same.)
+constexpr int kHistCopies = 16;
+constexpr int kHistStride = kRansMaxAlpha + 1;
+
 __global__ __launch_bounds__(256) void rans_hist_kernel(const int8_t* codes, int64_t n, int L, uint32_t* hist) {
-    __shared__ uint32_t h[kRansMaxAlpha];
-    if (threadIdx.x < kRansMaxAlpha) h[threadIdx.x] = 0;
+    __shared__ uint32_t h_all[kHistCopies * kHistStride];
+    for (int i = threadIdx.x; i < kHistCopies * kHistStride; i += 256) h_all[i] = 0;
     __syncthreads();
+    uint32_t* const h = h_all + (threadIdx.x & (kHistCopies - 1)) * kHistStride;
     const int64_t stride = (int64_t)gridDim.x * 256 * 16;
     for (int64_t base = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16; base < n; base += stride) {
         if (base + 16 <= n) {
@@ -49,7 +58,12 @@ __global__ __launch_bounds__(256) void rans_hist_kernel(const int8_t* codes, int
         }
     }
     __syncthreads();
-    if (threadIdx.x <= 2 * L && h[threadIdx.x]) atomicAdd(&hist[threadIdx.x], h[threadIdx.x]);
+    if (threadIdx.x <= 2 * L) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int c = 0; c < kHistCopies; ++c) t += h_all[c * kHistStride + threadIdx.x];
+        if (t) atomicAdd(&hist[threadIdx.x], t);
+    }
 }
 
 struct RansArgs {
