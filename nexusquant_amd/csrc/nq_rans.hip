@@ -17,10 +17,6 @@ constexpr uint32_t kRansM = 1u << 12;
 constexpr uint32_t kRansL = 1u << 16;
 constexpr int kRansMaxAlpha = 64;
 
-__device__ __forceinline__ int rans_symbol(int8_t c, int L, int has_half) {
-    return has_half ? (int)c + L : ((int)c >> 1) + L / 2;
-}
-
 __device__ __forceinline__ int8_t rans_code(int s, int L, int has_half) {
     return (int8_t)(has_half ? s - L : 2 * (s - L / 2));
 }
@@ -141,8 +137,9 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(RansArgs a) {
     uint64_t buf = 0;
     uint32_t nbuf = 0;
     uint32_t state = kRansL;
-    // rans_symbol without a branch: byte k of the word, arithmetically shifted
-    // right by 1 when there are no half-integer points, plus L or L / 2
+    // the symbol of code byte k without a branch: the byte arithmetically
+    // shifted right by 1 when there are no half-integer points (c / 2, c even),
+    // plus L or L / 2
     const int sym_shift = a.has_half ? 24 : 25;
     const int sym_off = a.has_half ? a.L : a.L / 2;
     auto lookup = [&](uint32_t word, int k) -> RansEnc {
