@@ -453,6 +453,13 @@ int nq_e8_quantize_perhead(const float* x, float* out, int64_t rows, int32_t d, 
 int nq_abi_version(void);
 const char* nq_last_error(void);
 
+/*
+ * Hash of the sources and compiler flags the library was built from (16 hex
+ * digits).  Build provenance, no counterpart in the reference: the Python
+ * loader compares it with the sources next to it and refuses a stale build.
+ */
+const char* nq_source_hash(void);
+
 #ifdef __cplusplus
 }
 #endif

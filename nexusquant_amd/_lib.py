@@ -10,7 +10,7 @@ import ctypes
 import os
 import threading
 
-from .build import LIB_PATH
+from .build import LIB_PATH, source_hash
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
 NQ_KEEP_ZERO, NQ_KEEP_WRITE_KEPT, NQ_KEEP_WRITE_EVICTED = 0, 1, 2
@@ -94,6 +94,7 @@ _I32, _I64, _F32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
     "nq_abi_version": ([], ctypes.c_int),
     "nq_last_error": ([], ctypes.c_char_p),
+    "nq_source_hash": ([], ctypes.c_char_p),
     "nq_quantize": ([ctypes.POINTER(QuantDesc), _P], ctypes.c_int),
     "nq_score_keykey_workspace": ([_I32, _I32, _I32], _I64),
     "nq_score_keykey": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
@@ -152,6 +153,12 @@ def load():
                 raise NexusQuantError(
                     f"{LIB_PATH} has ABI version {lib.nq_abi_version()}, the bindings expect "
                     f"{ABI_VERSION}; rebuild with `python -m nexusquant_amd.build`")
+            built = lib.nq_source_hash().decode()
+            want = source_hash()
+            if built != want:
+                raise NexusQuantError(
+                    f"{LIB_PATH} was built from other sources (hash {built}, sources {want}); "
+                    "rebuild with `python -m nexusquant_amd.build`")
             _lib = lib
     return _lib
 

@@ -39,6 +39,24 @@ def sources():
     return sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")))
 
 
+def source_hash() -> str:
+    """sha256 (hex, 16 digits) of everything the library is built from: the
+    kernel sources and headers, the public header and the compiler flags.
+    The build embeds it (nq_source_hash()); _lib.load() recomputes it and
+    refuses a library built from other sources."""
+    import hashlib
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")) + glob.glob(os.path.join(HERE, "csrc", "*.h"))
+                   + glob.glob(os.path.join(ROOT, "include", "*.h")))
+    for path in files:
+        h.update(os.path.relpath(path, ROOT).encode() + b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+        h.update(b"\0")
+    h.update(" ".join(HIPCC_FLAGS).encode())
+    return h.hexdigest()[:16]
+
+
 def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -55,7 +73,7 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB_PATH + ".tmp"
     inc = ["-I", os.path.join(ROOT, "include")]
-    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"] + [f'-DNQ_SOURCE_HASH="{source_hash()}"']
     jobs = jobs or min(len(sources()), os.cpu_count() or 1, 16)
     with tempfile.TemporaryDirectory(prefix="nqamd_build_") as objdir:
         objs = [os.path.join(objdir, os.path.basename(src) + ".o") for src in sources()]

@@ -16,6 +16,12 @@ void set_error(const char* fmt, ...) {
 
 }  // namespace nq
 
+#ifndef NQ_SOURCE_HASH
+#error "build with -DNQ_SOURCE_HASH=<hash of the sources> (python -m nexusquant_amd.build)"
+#endif
+
 extern "C" int nq_abi_version(void) { return NQ_ABI_VERSION; }
+
+extern "C" const char* nq_source_hash(void) { return NQ_SOURCE_HASH; }
 
 extern "C" const char* nq_last_error(void) { return nq::g_last_error; }

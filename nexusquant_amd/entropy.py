@@ -148,9 +148,58 @@ def rans_encode(codes: torch.Tensor, levels: int, chunk: int = DEFAULT_CHUNK) ->
                       chunk=chunk, shape=tuple(codes.shape))
 
 
+def check_stream_header(levels: int, has_half: bool, alphabet: int, n: int, chunk: int, n_chunks: int) -> None:
+    """Raise ValueError unless a stream header's counts agree with each other."""
+    if levels not in (2, 4, 8, 16):
+        raise ValueError(f"stream levels must be 2, 4, 8 or 16, got {levels}")
+    want_alpha = 2 * levels + 1 if has_half else levels + 1
+    if alphabet != want_alpha:
+        raise ValueError(f"alphabet {alphabet} does not match levels {levels} "
+                         f"({'with' if has_half else 'without'} half-integer points: {want_alpha})")
+    if chunk < 1 or chunk > (1 << 30):
+        raise ValueError(f"chunk must be in [1, 2^30], got {chunk}")
+    if n < 0:
+        raise ValueError(f"negative symbol count {n}")
+    if n_chunks != (n + chunk - 1) // chunk:
+        raise ValueError(f"{n_chunks} chunks for {n} symbols of chunk {chunk}; expected {(n + chunk - 1) // chunk}")
+
+
+def check_stream_layout(levels: int, has_half: bool, alphabet: int, n: int, chunk: int, n_chunks: int,
+                        freq: np.ndarray, offsets: np.ndarray, n_words: int) -> None:
+    """Raise ValueError unless a stream's header, frequency table and chunk
+    offsets are consistent with each other and with the n_words words present.
+
+    nq_rans_decode recomputes the chunk count as ceil(n / chunk) and reads
+    offsets[k] .. offsets[k + 1] of every chunk, and its slot tables are only
+    complete when the frequencies sum to 4096, so all of this is checked on
+    the host before anything reaches the device."""
+    check_stream_header(levels, has_half, alphabet, n, chunk, n_chunks)
+    freq = np.asarray(freq)
+    if freq.size != alphabet or int(freq.astype(np.int64).sum()) != M:
+        raise ValueError(f"frequency table must hold {alphabet} entries summing to {M}")
+    offsets = np.asarray(offsets, dtype=np.int64)
+    if offsets.size != n_chunks + 1 or (offsets.size and offsets[0] != 0):
+        raise ValueError("chunk offsets must hold n_chunks + 1 entries starting at 0")
+    if offsets.size > 1:
+        per = np.diff(offsets)
+        if np.any(per < 0):
+            raise ValueError("chunk offsets must be non-decreasing")
+        lens = np.full(n_chunks, chunk, dtype=np.int64)
+        lens[-1] = n - chunk * (n_chunks - 1)
+        if np.any(per > lens + 2):  # a chunk holds its final state plus at most one word per symbol
+            raise ValueError("a chunk claims more words than its symbols can produce")
+    if offsets.size and int(offsets[-1]) != n_words:
+        raise ValueError(f"chunk offsets end at word {int(offsets[-1])} but the stream holds {n_words} words")
+
+
 def rans_decode(stream: RansStream, device=None) -> torch.Tensor:
     """int8 codes of a RansStream, in its original shape."""
     lib = _lib.load()
+    check_stream_layout(stream.levels, stream.has_half, stream.alphabet, stream.n, stream.chunk,
+                        stream.offsets.numel() - 1, stream.freq, stream.offsets.cpu().numpy(),
+                        stream.words.numel())
+    if int(np.prod(stream.shape)) != stream.n:
+        raise ValueError(f"stream shape {stream.shape} does not hold {stream.n} symbols")
     dev = stream.words.device if device is None else torch.device(device)
     out = torch.empty(stream.n, dtype=torch.int8, device=dev)
     if stream.n:
@@ -184,24 +233,46 @@ def pack_nqr1(stream: RansStream, scales: Optional[torch.Tensor] = None) -> byte
 
 
 def unpack_nqr1(blob: bytes, shape=None, device="cuda"):
-    """(RansStream on `device`, fp32 scales or None) from NQR1 bytes."""
-    if blob[:4] != _MAGIC:
+    """(RansStream on `device`, fp32 scales or None) from NQR1 bytes.
+
+    Every length, count and offset is checked against the blob before any
+    array is built (ValueError on a truncated or inconsistent container)."""
+    head = 4 + struct.calcsize("<HBBHHQII")
+    if len(blob) < head or blob[:4] != _MAGIC:
         raise ValueError("not an NQR1 stream")
     version, levels, has_half, alphabet, _, n, chunk, n_chunks = struct.unpack_from("<HBBHHQII", blob, 4)
     if version != 1:
         raise ValueError(f"NQR1 version {version} unsupported")
-    at = 4 + struct.calcsize("<HBBHHQII")
+    check_stream_header(levels, bool(has_half), alphabet, n, chunk, n_chunks)
+    at = head
+
+    def need(nbytes, what):
+        if nbytes < 0 or at + nbytes > len(blob):
+            raise ValueError(f"truncated NQR1 stream: {what} needs {nbytes} bytes at offset {at}, "
+                             f"{len(blob)} bytes in the blob")
+
+    need(2 * alphabet, "frequency table")
     freq = np.frombuffer(blob, dtype="<u2", count=alphabet, offset=at).astype(np.uint16)
     at += 2 * alphabet + ((-2 * alphabet) % 4)
+    need(8 * (n_chunks + 1), "chunk offsets")
     offsets = np.frombuffer(blob, dtype="<u8", count=n_chunks + 1, offset=at).astype(np.int64)
     at += 8 * (n_chunks + 1)
     n_words = int(offsets[-1])
+    need(2 * n_words, "words")
+    check_stream_layout(levels, bool(has_half), alphabet, n, chunk, n_chunks, freq, offsets, n_words)
+    if shape is not None and int(np.prod(shape)) != n:
+        raise ValueError(f"shape {tuple(shape)} does not hold the stream's {n} symbols")
     words = np.frombuffer(blob, dtype="<u2", count=n_words, offset=at).view(np.int16)
     at += 2 * n_words
     scales = None
     if at < len(blob):
+        need(8, "scale count")
         (ns,) = struct.unpack_from("<Q", blob, at)
-        scales = torch.from_numpy(np.frombuffer(blob, dtype="<f4", count=ns, offset=at + 8).copy())
+        at += 8
+        need(4 * ns, "scales")
+        if at + 4 * ns != len(blob):
+            raise ValueError(f"{len(blob) - at - 4 * ns} trailing bytes after the NQR1 scales")
+        scales = torch.from_numpy(np.frombuffer(blob, dtype="<f4", count=ns, offset=at).copy())
     dev = torch.device(device)
     stream = RansStream(words=torch.from_numpy(words.copy()).to(dev), offsets=torch.from_numpy(offsets.copy()).to(dev),
                         freq=freq, levels=levels, has_half=bool(has_half), n=n, chunk=chunk,

@@ -71,6 +71,17 @@ def real_importance(model, input_ids: torch.Tensor) -> torch.Tensor:
         window = kwargs.get("sliding_window", getattr(module, "sliding_window", None))
         if window is not None and window < query.shape[2]:
             raise NotImplementedError("the real scorer kernel implements full causal attention only")
+        # Logit soft-capping (Gemma-2: tanh(x / cap) * cap) and attention sinks
+        # (gpt-oss: an extra softmax column per head) change the probabilities
+        # the reference column-sums; the kernel computes plain causal softmax.
+        if kwargs.get("softcap") is not None:
+            raise NotImplementedError(
+                "the real scorer kernel does not implement attention logit soft-capping "
+                f"(softcap={kwargs['softcap']}); use scorer='key-key' for this model")
+        if kwargs.get("s_aux") is not None or kwargs.get("sinks") is not None:
+            raise NotImplementedError(
+                "the real scorer kernel does not implement attention sinks (s_aux); "
+                "use scorer='key-key' for this model")
         if prev == "eager" or prev is None:
             base = _model_eager(module)
         else:

@@ -59,3 +59,23 @@ def test_abi_version_and_error_calls_need_no_gpu():
     lib = _lib.load()
     assert lib.nq_abi_version() == _lib.ABI_VERSION == 4
     assert isinstance(lib.nq_last_error(), bytes)
+
+
+def test_library_was_built_from_these_sources():
+    # the loader refuses a stale library; this names the mismatch directly
+    from nexusquant_amd.build import source_hash
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.nq_source_hash.restype = ctypes.c_char_p
+    assert lib.nq_source_hash().decode() == source_hash(), "stale libnqamd.so: rebuild"
+
+
+def test_loader_refuses_a_stale_library(monkeypatch):
+    # a library whose embedded hash differs from the sources must not load
+    from nexusquant_amd import build as nqbuild
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "source_hash", lambda: "0" * 16)
+    with pytest.raises(_lib.NexusQuantError, match="other sources"):
+        _lib.load()
+    monkeypatch.setattr(_lib, "source_hash", nqbuild.source_hash)
+    monkeypatch.setattr(_lib, "_lib", None)
+    assert _lib.load().nq_abi_version() == _lib.ABI_VERSION

@@ -57,3 +57,72 @@ def test_nqr1_container_roundtrip_on_host():
     assert torch.equal(t.words, s.words) and torch.equal(t.offsets, s.offsets)
     assert np.array_equal(t.freq, s.freq) and (t.levels, t.has_half, t.n, t.chunk) == (2, False, 8000, 4096)
     assert torch.equal(sc, torch.arange(5, dtype=torch.float32))
+
+
+def _good_blob():
+    from nexusquant_amd.entropy import RansStream, pack_nqr1
+    rng = np.random.default_rng(4)
+    s = RansStream(words=torch.from_numpy(rng.integers(-2 ** 15, 2 ** 15, 900).astype(np.int16)),
+                   offsets=torch.tensor([0, 500, 900], dtype=torch.int64),
+                   freq=np.array([1000, 3000, 96], np.uint16), levels=2, has_half=False, n=8000, chunk=4096,
+                   shape=(8000,))
+    return s, pack_nqr1(s, scales=torch.ones(3))
+
+
+def _patch(blob, fmt, offset, *vals):
+    import struct
+    b = bytearray(blob)
+    struct.pack_into(fmt, b, offset, *vals)
+    return bytes(b)
+
+
+@pytest.mark.parametrize("what", ["n_chunks", "n_symbols", "chunk0", "alphabet", "freq_sum", "offset0",
+                                  "offsets_order", "offset_end", "truncated", "scales_tail",
+                                  "shape"])
+def test_nqr1_rejects_inconsistent_containers(what):
+    # every header field the decoder trusts is checked on the host, so a
+    # corrupted or truncated container raises instead of reaching the device
+    from nexusquant_amd.entropy import unpack_nqr1
+    _, blob = _good_blob()
+    # magic, then '<HBBHHQII' (24 bytes): alphabet at 8, n at 12, chunk at 20, n_chunks at 24
+    head = 28
+    freq_at = head
+    off_at = head + 8                # 3 freqs (6 bytes) padded to 8
+    shape = None
+    if what == "n_chunks":
+        blob = _patch(blob, "<I", 24, 1)
+    elif what == "n_symbols":
+        blob = _patch(blob, "<Q", 12, 20000)
+    elif what == "chunk0":
+        blob = _patch(blob, "<I", 20, 0)
+    elif what == "alphabet":
+        blob = _patch(blob, "<H", 8, 5)
+    elif what == "freq_sum":
+        blob = _patch(blob, "<H", freq_at, 999)
+    elif what == "offset0":
+        blob = _patch(blob, "<Q", off_at, 1)
+    elif what == "offsets_order":
+        blob = _patch(blob, "<Q", off_at + 8, 950)
+    elif what == "offset_end":
+        blob = _patch(blob, "<Q", off_at + 16, 899)
+    elif what == "truncated":
+        blob = blob[:off_at + 24 + 100]
+    elif what == "scales_tail":
+        blob = blob + b"\0\0"
+    elif what == "shape":
+        shape = (7999,)
+    with pytest.raises(ValueError):
+        unpack_nqr1(blob, shape=shape, device="cpu")
+
+
+def test_nqr1_rejects_chunk_with_too_many_words():
+    from nexusquant_amd.entropy import RansStream, pack_nqr1, unpack_nqr1
+    s = RansStream(words=torch.zeros(20, dtype=torch.int16), offsets=torch.tensor([0, 12, 20], dtype=torch.int64),
+                   freq=np.array([1000, 3000, 96], np.uint16), levels=2, has_half=False, n=15, chunk=8,
+                   shape=(15,))
+    with pytest.raises(ValueError, match="more words"):
+        unpack_nqr1(pack_nqr1(s), device="cpu")   # chunk 0: 8 symbols, at most 10 words
+    s.offsets = torch.tensor([0, 10, 19], dtype=torch.int64)
+    s.words = torch.zeros(19, dtype=torch.int16)
+    t, _ = unpack_nqr1(pack_nqr1(s), device="cpu")
+    assert t.n == 15 and t.offsets.tolist() == [0, 10, 19]

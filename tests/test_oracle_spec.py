@@ -162,15 +162,35 @@ def _row_agree_rel_l2(got, ref, row_ok):
     return float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30))
 
 
-@pytest.mark.parametrize("tag", ["b1e4", "b5e5"])
+# Reference fixtures of the quant-only path (tests/golden, written by the reference):
+# tag -> (fixture, key levels, value levels, RoPE base or None to read it, output arrays)
+REF_FIXTURES = {
+    "b1e4": ("quant_only_b1e4", 8, 4, None, ("k_k3v2", "v_k3v2")),
+    "b5e5": ("quant_only_b5e5", 8, 4, None, ("k_k3v2", "v_k3v2")),
+    # NexusQuantEvict(bits=2, eviction_rate=0) at head_dim 256: the K2V2 of Gemma-2-2b (C5b)
+    "d256": ("quant_only_d256", 4, 4, 10000.0, ("k_out", "v_out")),
+    # bf16 inputs (stored as their exact fp32 values), K3V2 at base 5e5
+    "bf16": ("quant_only_bf16", 8, 4, 500000.0, ("k_out", "v_out")),
+}
+
+
+def _allowed_flips(n_groups):
+    """North-star code agreement: >= 99.99 % of 8-groups; a fixture with fewer
+    than 10^4 groups may still hold one near-tie flip."""
+    return max(1, int(1e-4 * n_groups))
+
+
+@pytest.mark.parametrize("tag", sorted(REF_FIXTURES))
 def test_spec_within_tolerance_of_reference_fixture(golden, tag):
-    g = golden(f"quant_only_{tag}")
-    base = float(g["base"])
+    name, kl, vl, base, (k_name, v_name) = REF_FIXTURES[tag]
+    g = golden(name)
+    if base is None:
+        base = float(g["base"])
     for li in range(g["k_in"].shape[0]):
         k = g["k_in"][li].astype(np.float32)
         v = g["v_in"][li].astype(np.float32)
-        ok, ov = _spec_layer(k, v, base, 8, 4)
-        for o, ref, L, is_key in ((ok, g["k_k3v2"][li], 8, True), (ov, g["v_k3v2"][li], 4, False)):
+        ok, ov = _spec_layer(k, v, base, kl, vl)
+        for o, ref, L, is_key in ((ok, g[k_name][li], kl, True), (ov, g[v_name][li], vl, False)):
             d = ref.shape[-1]
             ref2 = ref.reshape(-1, d)
             # reference lattice points for the code comparison
@@ -182,10 +202,100 @@ def test_spec_within_tolerance_of_reference_fixture(golden, tag):
             rot = torch.einsum('nd,de->ne', x, T.hadamard_matrix(d))
             p_ref, _ = T.e8_quantize_perhead_parts(rot, L)
             mism = (p_ref.numpy().reshape(-1, 8) != o["p"].reshape(-1, 8)).any(1)
-            assert mism.mean() <= 1e-4
+            assert mism.sum() <= _allowed_flips(mism.size)
             assert np.all(o["margin"].reshape(-1)[mism] < 1e-5)
             row_ok = ~mism.reshape(ref2.shape[0], -1).any(1)
             assert _row_agree_rel_l2(o["recon"], ref2, row_ok) <= 1e-3
+
+
+# ---------------------------------------------------------------------------
+# head_dim 96 (Phi-3-mini, C5a).  The reference raises in hadamard_matrix(96)
+# (hadamard.py:35-36), so this build defines the path: inverse RoPE at d = 96,
+# zero-pad to 128, the reference's 128-point quantizer, inverse transform,
+# keep the first 96 coordinates, forward RoPE at d = 96.  Pinned two ways:
+# (1) by composing the reference's own operators on that definition, and
+# (2) by invariants that tie the d = 96 path to the d = 128 one.
+# ---------------------------------------------------------------------------
+
+def _reference_ops_padded(x, L, is_key, base):
+    """The reference's operators at head_dim 96 padded to 128.
+
+    x: [h, s, 96] fp32 (post-RoPE keys or values).  Returns (lattice points
+    [h*s, 128], fp16 reconstruction [h*s, 96]).  inverse_rope / forward_rope
+    follow rope_utils.py:75-122, 203-249 at d = 96; the transform is the
+    einsum with hadamard_matrix(128) (pipeline.py:250, 253); the quantizer is
+    E8Lattice.quantize_perhead (e8_lattice.py:97-124)."""
+    import torch.nn.functional as F
+    h, s, d = x.shape
+    D = 128
+    if is_key:
+        x = T.inverse_rope(x, base=base)
+    rot = torch.einsum('hsd,de->hse', F.pad(x, (0, D - d)), T.hadamard_matrix(D)).reshape(-1, D)
+    p, scale = T.e8_quantize_perhead_parts(rot, L)
+    back = torch.einsum('nd,ed->ne', p * scale, T.hadamard_matrix(D))[:, :d].reshape(h, s, d)
+    if is_key:
+        back = T.forward_rope(back, base=base)
+    return p.numpy(), back.half().numpy().reshape(-1, d)
+
+
+def _phi3_rows(h, s, seed, base):
+    g = torch.Generator().manual_seed(seed)
+    kp = torch.randn(h, s, 96, generator=g)
+    for hi in range(h):
+        kp[hi, :, torch.randperm(96, generator=g)[:4]] *= 8.0
+    k = T.forward_rope(kp, base=base)
+    v = torch.randn(h, s, 96, generator=g) * 0.5
+    return k, v
+
+
+@pytest.mark.parametrize("L", [4, 8])
+def test_head_dim_96_spec_reduces_to_reference_ops(L):
+    base = 10000.0
+    h, s = 8, 512
+    k, v = _phi3_rows(h, s, seed=96 + L, base=base)
+    cs, sn = T.rope_cos_sin(torch.arange(s, dtype=torch.float32), 96, base)
+    cos = np.tile(cs.numpy(), (h, 1))
+    sin = np.tile(sn.numpy(), (h, 1))
+    for x, is_key in ((k, True), (v, False)):
+        kw = dict(cos_in=cos, sin_in=sin, cos_out=cos, sin_out=sin) if is_key else {}
+        o = S.quant_rows(x.numpy().reshape(-1, 96), L, margins=True, **kw)
+        p_ref, rec_ref = _reference_ops_padded(x, L, is_key, base)
+        assert o["p"].shape == p_ref.shape == (h * s, 128)
+        mism = (p_ref.reshape(-1, 8) != o["p"].reshape(-1, 8)).any(1)
+        assert mism.sum() <= _allowed_flips(mism.size)
+        assert np.all(o["margin"].reshape(-1)[mism] < 1e-5)
+        row_ok = ~mism.reshape(h * s, -1).any(1)
+        assert _row_agree_rel_l2(o["recon"], rec_ref, row_ok) <= 1e-3
+
+
+def test_head_dim_96_values_equal_the_zero_padded_128_path():
+    # values carry no RoPE: the d = 96 path is the d = 128 path on the
+    # zero-padded row, first 96 outputs, bit for bit (codes and scales too)
+    _, v = _phi3_rows(4, 300, seed=7, base=10000.0)
+    x96 = v.numpy().reshape(-1, 96)
+    x128 = np.zeros((x96.shape[0], 128), np.float32)
+    x128[:, :96] = x96
+    for L in (2, 4, 8, 16):
+        a = S.quant_rows(x96, L)
+        b = S.quant_rows(x128, L)
+        assert np.array_equal(a["p"], b["p"]) and np.array_equal(a["scale"], b["scale"])
+        assert np.array_equal(a["sym"], b["sym"]) and np.array_equal(a["coset"], b["coset"])
+        assert np.array_equal(a["recon"].view(np.uint16), b["recon"][:, :96].view(np.uint16))
+
+
+def test_head_dim_96_keys_at_identity_rotation_equal_values():
+    # with cos = 1, sin = 0 (position 0) both rotations are exact identities,
+    # so the key path must equal the value path bit for bit: this isolates the
+    # padding / transform / quantizer part of the d = 96 key path
+    k, _ = _phi3_rows(2, 200, seed=8, base=10000.0)
+    x = k.numpy().reshape(-1, 96)
+    one = np.ones((x.shape[0], 48), np.float32)
+    zero = np.zeros((x.shape[0], 48), np.float32)
+    for L in (4, 8):
+        a = S.quant_rows(x, L, cos_in=one, sin_in=zero, cos_out=one, sin_out=zero)
+        b = S.quant_rows(x, L)
+        assert np.array_equal(a["p"], b["p"]) and np.array_equal(a["scale"], b["scale"])
+        assert np.array_equal(a["recon"].view(np.uint16), b["recon"].view(np.uint16))
 
 
 def test_symbol_packing_roundtrip():
