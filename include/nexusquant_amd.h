@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define NQ_ABI_VERSION 4
+#define NQ_ABI_VERSION 5
 
 /* status codes */
 #define NQ_OK 0
@@ -106,14 +106,15 @@ int nq_quantize(const nq_quant_desc* desc, void* stream);
 /*
  * Key-key importance (SnapKV-style proxy): keys [batch, heads, seq, head_dim]
  * (dtype NQ_F16/NQ_BF16/NQ_F32, head_dim 64/96/128/256); queries are the last
- * min(obs_window, seq) <= 32 keys; importance[batch, seq] = mean over heads of
- * the per-key sum over queries of softmax(q . k * scale) over all keys.
- * scale is the reference's fp32 d**-0.5.  workspace: device buffer of at least
- * nq_score_keykey_workspace(batch, heads, seq) bytes (caller owned).
+ * obs = min(obs_window, seq) keys; importance[batch, seq] = mean over heads of
+ * the per-key sum over queries of softmax(q . k * scale) over all keys, in
+ * fp32.  scale is the reference's fp32 d**-0.5.  workspace: device buffer of
+ * at least nq_score_keykey_workspace(batch, heads, seq, obs_window) bytes
+ * (caller owned; per-split row statistics and per-head column sums).
  *
  * Replaces: NexusQuantEvict._score_importance          pipeline.py:756-782
  */
-int64_t nq_score_keykey_workspace(int32_t batch, int32_t heads, int32_t seq);
+int64_t nq_score_keykey_workspace(int32_t batch, int32_t heads, int32_t seq, int32_t obs_window);
 int nq_score_keykey(const void* keys, int32_t dtype, int32_t batch, int32_t heads, int32_t seq,
                     int32_t head_dim, int32_t obs_window, float scale, float* importance, void* workspace,
                     int64_t workspace_bytes, void* stream);

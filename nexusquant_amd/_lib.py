@@ -14,7 +14,7 @@ from .build import LIB_PATH, source_hash
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
 NQ_KEEP_ZERO, NQ_KEEP_WRITE_KEPT, NQ_KEEP_WRITE_EVICTED = 0, 1, 2
-ABI_VERSION = 4  # NQ_ABI_VERSION of the header these bindings mirror
+ABI_VERSION = 5  # NQ_ABI_VERSION of the header these bindings mirror
 _P = ctypes.c_void_p
 
 
@@ -96,7 +96,7 @@ SIGNATURES = {
     "nq_last_error": ([], ctypes.c_char_p),
     "nq_source_hash": ([], ctypes.c_char_p),
     "nq_quantize": ([ctypes.POINTER(QuantDesc), _P], ctypes.c_int),
-    "nq_score_keykey_workspace": ([_I32, _I32, _I32], _I64),
+    "nq_score_keykey_workspace": ([_I32, _I32, _I32, _I32], _I64),
     "nq_score_keykey": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
     "nq_keep_mask": ([_P, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P], ctypes.c_int),
     "nq_gather_rows": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),

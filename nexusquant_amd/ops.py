@@ -292,7 +292,9 @@ def score_keykey(keys: torch.Tensor, obs_window: int = 32) -> torch.Tensor:
     imp = torch.empty(b, s, dtype=torch.float32, device=dev)
     if s == 0:
         return imp
-    ws_bytes = lib.nq_score_keykey_workspace(b, h, s)
+    if int(obs_window) <= 0:
+        raise ValueError(f"obs_window must be positive, got {obs_window}")
+    ws_bytes = lib.nq_score_keykey_workspace(b, h, s, int(obs_window))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     scale = float(d) ** -0.5
     with torch.cuda.device(dev):

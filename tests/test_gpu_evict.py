@@ -64,6 +64,19 @@ def test_keykey_scorer_matches_oracle(dtype, d, s):
         assert _keep_sets_match(imp.numpy(), ref.numpy(), km, kr)
 
 
+@pytest.mark.parametrize("obs,dtype,d,s", [(1, torch.float16, 128, 300), (7, torch.bfloat16, 128, 500),
+                                           (48, torch.float16, 128, 777), (100, torch.float32, 64, 450),
+                                           (64, torch.float16, 256, 64), (40, torch.bfloat16, 96, 39)])
+def test_keykey_scorer_any_observation_window(obs, dtype, d, s):
+    # queries are the last min(obs, s) keys, in blocks of 32 (pipeline.py:772-776)
+    from nexusquant_amd.ops import score_keykey
+    print(f"[gpu] keykey obs={obs} {dtype} d={d} s={s}", flush=True)
+    k = _keys(2, 3, s, d, dtype, seed=obs + s)
+    imp = score_keykey(k.to(DEV), obs).cpu()
+    ref = T.score_keykey(k.float(), obs)
+    assert torch.allclose(imp, ref, rtol=1e-4, atol=1e-8), (imp - ref).abs().max()
+
+
 def test_keykey_scorer_matches_reference_fixture(golden):
     from nexusquant_amd.ops import score_keykey
     g = golden("evict_mask_b4")
