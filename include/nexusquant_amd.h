@@ -120,6 +120,25 @@ int nq_score_keykey(const void* keys, int32_t dtype, int32_t batch, int32_t head
                     int64_t workspace_bytes, void* stream);
 
 /*
+ * nq_score_keykey without a workspace argument: the partial row statistics
+ * live in a static device array of the library, NQ_KEYKEY_SCRATCH_BYTES per
+ * GPU (held from library load until the process ends), so the call allocates
+ * nothing -- no hipMalloc, no hipFree, no allocating library call.  Shapes
+ * whose nq_score_keykey_workspace(batch, heads, seq, obs_window) exceeds the
+ * scratch return NQ_EINVAL before any launch (8 MiB covers e.g. 64 heads x
+ * 131072 tokens with 64 observation queries).  The stream must belong to the
+ * current device.  Every call on a GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other streams, other threads) race.
+ *
+ * No counterpart in the reference: this entry point is for callers that
+ * cannot allocate -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.
+ */
+#define NQ_KEYKEY_SCRATCH_BYTES (8 << 20)
+int nq_score_keykey_noalloc(const void* keys, int32_t dtype, int32_t batch, int32_t heads, int32_t seq,
+                            int32_t head_dim, int32_t obs_window, float scale, float* importance, void* stream);
+
+/*
  * Real-attention importance of one layer, accumulated: importance[b, j] +=
  * mean over q_heads of sum_{i >= j} p[b, h, i, j], with
  * p = round(softmax_fp32(round(round(q . k) * scaling))) under the causal

@@ -98,6 +98,7 @@ SIGNATURES = {
     "nq_quantize": ([ctypes.POINTER(QuantDesc), _P], ctypes.c_int),
     "nq_score_keykey_workspace": ([_I32, _I32, _I32, _I32], _I64),
     "nq_score_keykey": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
+    "nq_score_keykey_noalloc": ([_P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P], ctypes.c_int),
     "nq_keep_mask": ([_P, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P], ctypes.c_int),
     "nq_gather_rows": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "nq_dequantize": ([ctypes.POINTER(CodesDesc), _P], ctypes.c_int),

@@ -29,6 +29,8 @@
 // lanes c and c + 32 read one 32-byte run; a unit is one MFMA step for f16 /
 // bf16 (the hardware's own k order) and four steps for f32.  Both operands use
 // the same order, so the products cover every coordinate once.
+#include <mutex>
+
 #include "nq_common.h"
 
 namespace nq {
@@ -392,6 +394,75 @@ int score_keykey_ws(const void* keys, int32_t dtype, int32_t batch, int32_t head
 }
 
 }  // namespace nq
+
+// ---------------------------------------------------------------------------
+// No-allocation variant: the workspace is this file-scope device array, one
+// copy per GPU for the life of the process.  Host code never passes `scratch`
+// itself to a kernel (in host code the name is a stand-in, not a device
+// address): each device's address comes from hipGetSymbolAddress, taken once
+// per device with that device current, and only that pointer is used.
+// Nothing in it needs to start at zero: kk_stats writes every partial that
+// kk_colsum then reads, in the same call.  Calls that overlap on one GPU
+// share the array and race.
+// ---------------------------------------------------------------------------
+namespace nq {
+
+static __device__ __align__(256) char scratch[NQ_KEYKEY_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// the device address of `scratch` on the current device (looked up once per device)
+static int current_scratch(void** out, const char* who) {
+    int dev = -1;
+    NQ_CHECK_HIP(hipGetDevice(&dev));
+    NQ_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "%s: device %d beyond the %d this library tracks", who, dev,
+                 kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error("%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev, hipGetErrorString(e));
+            return NQ_EHIP;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return NQ_OK;
+}
+
+}  // namespace nq
+
+extern "C" int nq_score_keykey_noalloc(const void* keys, int32_t dtype, int32_t batch, int32_t heads, int32_t seq,
+                                       int32_t head_dim, int32_t obs_window, float scale, float* importance,
+                                       void* stream) {
+    using namespace nq;
+    static const char* who = "nq_score_keykey_noalloc";
+    NQ_CHECK_ARG(batch > 0 && heads > 0 && seq >= 0 && obs_window > 0, "%s: bad shape", who);
+    if (seq == 0) return NQ_OK;
+    const int64_t need = nq_score_keykey_workspace(batch, heads, seq, obs_window);
+    NQ_CHECK_ARG(need <= NQ_KEYKEY_SCRATCH_BYTES,
+                 "%s: batch %d x heads %d x seq %d (obs %d) needs %lld bytes of scratch, above the static "
+                 "%d; use nq_score_keykey with a workspace",
+                 who, batch, heads, seq, obs_window, (long long)need, NQ_KEYKEY_SCRATCH_BYTES);
+    int cur = -1;
+    NQ_CHECK_HIP(hipGetDevice(&cur));
+    if (stream) {
+        hipDevice_t sdev = -1;
+        NQ_CHECK_HIP(hipStreamGetDevice((hipStream_t)stream, &sdev));
+        NQ_CHECK_ARG((int)sdev == cur, "%s: the stream belongs to device %d, the current device is %d", who,
+                     (int)sdev, cur);
+    }
+    void* ws = nullptr;
+    const int st = current_scratch(&ws, who);
+    if (st != NQ_OK) return st;
+    return score_keykey_ws(keys, dtype, batch, heads, seq, head_dim, obs_window, scale, importance, ws,
+                           NQ_KEYKEY_SCRATCH_BYTES, stream, who);
+}
 
 extern "C" int64_t nq_score_keykey_workspace(int32_t batch, int32_t heads, int32_t seq, int32_t obs_window) {
     if (batch <= 0 || heads <= 0 || seq <= 0 || obs_window <= 0) return 0;

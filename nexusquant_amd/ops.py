@@ -305,6 +305,33 @@ def score_keykey(keys: torch.Tensor, obs_window: int = 32) -> torch.Tensor:
     return imp
 
 
+def score_keykey_noalloc(keys: torch.Tensor, obs_window: int = 32,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """score_keykey through nq_score_keykey_noalloc: the library's static
+    per-GPU scratch instead of a workspace, so the launch allocates nothing
+    (pass `out`, fp32 [batch, seq], to allocate nothing here either).  keys
+    must be contiguous and 16-byte aligned.  Calls that overlap on one GPU
+    share the scratch and race."""
+    lib = _lib.load()
+    _lib.require_device(keys, "keys")
+    if keys.dim() != 4 or not keys.is_contiguous() or keys.data_ptr() % 16:
+        raise ValueError("keys must be a contiguous, 16-byte aligned [batch, heads, seq, head_dim] tensor")
+    b, h, s, d = keys.shape
+    if out is None:
+        out = torch.empty(b, s, dtype=torch.float32, device=keys.device)
+    elif (tuple(out.shape) != (b, s) or out.dtype != torch.float32 or not out.is_contiguous()
+          or out.device != keys.device):
+        raise ValueError(f"out must be a contiguous fp32 [{b}, {s}] tensor on {keys.device}")
+    if s == 0:
+        return out
+    with torch.cuda.device(keys.device):
+        st = lib.nq_score_keykey_noalloc(_addr(keys), _lib.dtype_code(keys.dtype), b, h, s, d, int(obs_window),
+                                         ctypes.c_float(float(d) ** -0.5), _addr(out),
+                                         ctypes.c_void_p(_lib.current_stream_handle(keys.device)))
+    _lib.check(st, "nq_score_keykey_noalloc")
+    return out
+
+
 def keep_plan(seq: int, rate: float, sliding_window: int) -> Tuple[int, int]:
     """(prefix, k) of the keep mask, in Python double as pipeline.py:924-925, 944-946."""
     prefix = max(seq - sliding_window, 0)

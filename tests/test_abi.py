@@ -79,3 +79,18 @@ def test_loader_refuses_a_stale_library(monkeypatch):
     monkeypatch.setattr(_lib, "source_hash", nqbuild.source_hash)
     monkeypatch.setattr(_lib, "_lib", None)
     assert _lib.load().nq_abi_version() == _lib.ABI_VERSION
+
+
+def test_noalloc_keykey_rejects_shapes_beyond_its_scratch_without_a_gpu():
+    # the size check runs on the host before any HIP call or pointer use, so
+    # dummy pointers are never dereferenced
+    lib = _lib.load()
+    b, h, s, obs = 1, 64, 131072, 96          # 12 MiB of row statistics > 8 MiB
+    assert lib.nq_score_keykey_workspace(b, h, s, obs) > (8 << 20)
+    assert lib.nq_score_keykey_workspace(1, 64, 131072, 64) == (8 << 20)
+    dummy = ctypes.c_void_p(256)
+    st = lib.nq_score_keykey_noalloc(dummy, _lib.NQ_F16, b, h, s, 128, obs, ctypes.c_float(128 ** -0.5),
+                                     dummy, None)
+    assert st == -1 and b"scratch" in lib.nq_last_error()
+    st = lib.nq_score_keykey_noalloc(dummy, _lib.NQ_F16, 0, h, s, 128, obs, ctypes.c_float(1.0), dummy, None)
+    assert st == -1
