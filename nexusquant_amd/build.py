@@ -28,6 +28,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source flags.  The scorers read every MFMA result with VALU instructions;
+# accumulators in VGPRs save one v_accvgpr_read per element.
+SOURCE_FLAGS = {
+    "nq_score.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "nq_keykey.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and os.path.exists(cand):
@@ -54,6 +62,8 @@ def source_hash() -> str:
             h.update(f.read())
         h.update(b"\0")
     h.update(" ".join(HIPCC_FLAGS).encode())
+    for name in sorted(SOURCE_FLAGS):
+        h.update((name + ":" + " ".join(SOURCE_FLAGS[name])).encode())
     return h.hexdigest()[:16]
 
 
@@ -78,7 +88,8 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
     with tempfile.TemporaryDirectory(prefix="nqamd_build_") as objdir:
         objs = [os.path.join(objdir, os.path.basename(src) + ".o") for src in sources()]
         with ThreadPoolExecutor(max_workers=jobs) as pool:
-            list(pool.map(lambda so: _run([hipcc(), *compile_flags, *inc, "-c", so[0], "-o", so[1]], verbose),
+            list(pool.map(lambda so: _run([hipcc(), *compile_flags, *SOURCE_FLAGS.get(os.path.basename(so[0]), []),
+                                           *inc, "-c", so[0], "-o", so[1]], verbose),
                           zip(sources(), objs)))
         _run([hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB_PATH)

@@ -184,10 +184,13 @@ __global__ __launch_bounds__(64) void real_sweep(RealArgs a) {
 // operand reads of 16 consecutive lanes hit 64 distinct banks).
 //
 // real_rowstats: a workgroup owns 128 query rows (wave w: rows 32w..32w+31 of
-// the block) of one query head; its queries are the MFMA A operand.  It streams
-// the key tiles 0..(last row)/32 twice: first the row maximum of the raw
-// logits (the rounding chain round_T(round_T(.) * scaling) is monotone, so it
-// is applied once to the maximum), then the row sums of exp(x - max).  Writes
+// the block) of one query head, held in registers as the MFMA B operand, and
+// streams the key tiles 0..(last row)/32 once, keys as the A operand: a lane
+// then holds one query's logits against 16 keys of the tile.  Each lane keeps
+// the running maximum m of its raw logits (the rounding chain
+// round_T(round_T(.) * scaling) is monotone, so it is applied to the maximum
+// alone) and the sum z of exp(x - max) relative to it, rescaling z when m
+// grows; lanes c and c + 32 (the same query) are combined at the end.  Writes
 // -max * log2(e) and 1 / sum per row.
 // real_colsum: a workgroup owns 128 keys (wave w: keys 32w..32w+31) as the B
 // operand and streams the query tiles from its first key on; it accumulates
@@ -257,25 +260,59 @@ constexpr int kWaitVm0 = 0x0f70;
 // loads, in the padded layout tile_store writes (row r at r * ROWB).  The stage
 // is UPR = ROWB / 16 windows of 64 16-byte slots; window w goes to wave w mod 4,
 // and lane l of it fills slot 64 w + l: row (64 w + l) / UPR, unit
-// (64 w + l) mod UPR, the pad unit (D / 8) masked off.  Rows past seq are
-// clamped.  Nothing passes through registers, so a stage in flight costs no
-// VGPRs; the caller waits (vmcnt) and then synchronises the workgroup.
+// (64 w + l) mod UPR, the pad unit (D / 8) masked off.  Nothing passes through
+// registers, so a stage in flight costs no VGPRs; the caller waits (vmcnt) and
+// then synchronises the workgroup.
+//
+// The lane's slots do not depend on the stage, so DmaPlan computes them once:
+// the byte offset of each slot within a stage (row * 2D + 16 unit) and its
+// row.  A full stage (row0 + 64 <= seq) then issues each load from the
+// wave-uniform stage base plus that fixed offset; the last, partial stage
+// clamps rows past seq to the last row.
 template <int D>
-__device__ __forceinline__ void tile_dma(const uint16_t* base, int row0, int seq, char* buf) {
-    constexpr int UPR = RealTile<D>::ROWB / 16;
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int lane = threadIdx.x & 63;
+struct DmaPlan {
+    static constexpr int UPR = RealTile<D>::ROWB / 16;
+    static constexpr int NW = (UPR + 3) / 4;  // windows per wave (the last may be empty)
+    uint32_t off[NW];
+    int row[NW];   // -1: pad slot or no window
+    __device__ __forceinline__ DmaPlan() {
+        const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int k = 0; k < (UPR + 3) / 4; ++k) {
-        const int w = 4 * k + wave;
-        if (w < UPR) {
+        for (int k = 0; k < NW; ++k) {
+            const int w = 4 * k + wave;
             const int slot = 64 * w + lane;
             const int r = slot / UPR, u = slot - r * UPR;
-            if (u < D / 8) {
-                int row = row0 + r;
-                row = row < seq ? row : seq - 1;
-                __builtin_amdgcn_global_load_lds((global_void_t*)(base + (size_t)row * D + 8 * u),
-                                                 (lds_void_t*)(buf + 1024 * w), 16, 0, 0);
+            const bool ok = w < UPR && u < D / 8;
+            row[k] = ok ? r : -1;
+            off[k] = ok ? (uint32_t)(r * D * 2 + 16 * u) : 0u;
+        }
+    }
+};
+
+template <int D>
+__device__ __forceinline__ void tile_dma(const DmaPlan<D>& plan, const uint16_t* base, int row0, int seq, char* buf) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const char* stage = reinterpret_cast<const char*>(base) + (size_t)row0 * D * 2;  // wave-uniform
+    if (row0 + 64 <= seq) {
+        // uniform base + 32-bit lane offset: the scalar-base form of the load, no VALU
+#pragma unroll
+        for (int k = 0; k < DmaPlan<D>::NW; ++k) {
+            const int w = 4 * k + wave;
+            if (w < DmaPlan<D>::UPR && plan.row[k] >= 0)
+                __builtin_amdgcn_global_load_lds((global_void_t*)(stage + plan.off[k]), (lds_void_t*)(buf + 1024 * w),
+                                                 16, 0, 0);
+        }
+    } else {
+        const char* last = reinterpret_cast<const char*>(base) + (size_t)(seq - 1) * D * 2;
+#pragma unroll
+        for (int k = 0; k < DmaPlan<D>::NW; ++k) {
+            const int w = 4 * k + wave;
+            if (w < DmaPlan<D>::UPR && plan.row[k] >= 0) {
+                // rows past seq read the last row (same unit)
+                const char* src = row0 + plan.row[k] < seq ? stage + plan.off[k]
+                                                           : last + (plan.off[k] - (uint32_t)plan.row[k] * D * 2);
+                __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)(buf + 1024 * w), 16, 0, 0);
             }
         }
     }
@@ -325,11 +362,14 @@ __device__ __forceinline__ float eager_logit(float acc, float scaling) {
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 typedef __fp16 f16x2v __attribute__((ext_vector_type(2)));
 
-// two fp32 -> packed fp16, round to nearest even (one v_cvt_pk_f16_f32)
+// two fp32 -> packed fp16, round to nearest even: one v_cvt_pk_f16_f32,
+// emitted by the compiler (not inline asm: the operands are often MFMA results
+// held in VGPRs, and only compiler-visible reads get the MFMA-to-VALU wait states)
 __device__ __forceinline__ f16x2v cvt_pk_f16(float lo, float hi) {
-    uint32_t r;
-    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
-    return __builtin_bit_cast(f16x2v, r);
+    typedef float f32x2v __attribute__((ext_vector_type(2)));
+    typedef _Float16 h16x2v __attribute__((ext_vector_type(2)));
+    const f32x2v v = {lo, hi};
+    return __builtin_bit_cast(f16x2v, __builtin_convertvector(v, h16x2v));
 }
 
 // exp2 arguments of two logits: round_T(round_T(acc) * scaling) * log2(e) + nm,
@@ -354,81 +394,57 @@ __device__ __forceinline__ void exp_args2(float a0, float a1, float scaling, flo
     }
 }
 
-// round_T of two fp32 values, added to acc in fp32
+// round_T of two fp32 values, packed (low = first)
 template <int DT>
-__device__ __forceinline__ float add_rounded2(float acc, float p0, float p1, bool v0, bool v1) {
+__device__ __forceinline__ uint32_t round_pair(float p0, float p1) {
     if constexpr (DT == NQ_F16) {
-        const f16x2v h = cvt_pk_f16(p0, p1);
-        acc = v0 ? acc + (float)h.x : acc;
-        return v1 ? acc + (float)h.y : acc;
+        return __builtin_bit_cast(uint32_t, cvt_pk_f16(p0, p1));
     } else {
         const bf16x2v h = {(__bf16)p0, (__bf16)p1};
-        acc = v0 ? acc + (float)h.x : acc;
-        return v1 ? acc + (float)h.y : acc;
+        return __builtin_bit_cast(uint32_t, h);
     }
 }
 
-// One pass over the 64-key LDS stages of a query block, two LDS buffers: the
-// next stage's direct-to-LDS loads are issued before the current stage is
-// computed, and each thread waits for its own part before the one barrier per
-// stage.  The buffers are separate arrays used in fixed roles (the loop is
-// unrolled by two), so the compiler can see that the reads of the current
-// buffer do not depend on the loads into the other one.
-template <int DT, int D, int PASS>
-__device__ __forceinline__ void rowstats_sweep(const RealArgs& a, const uint16_t* kbase, char* lds0, char* lds1,
-                                               const uint4 (&qa)[RealTile<D>::KS], int n_it, bool live,
-                                               int q0, int lane, float (&m)[16], float (&z)[16]) {
-    const int g = lane >> 5, c = lane & 31;
-    const int my_diag = q0 / 32;  // this wave's diagonal 32-key block
-    tile_dma<D>(kbase, 0, a.seq, lds0);
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    __syncthreads();
-    auto stage = [&](int it, const char* cur, char* nxt) {
-        if (it + 1 < n_it) tile_dma<D>(kbase, (it + 1) * 64, a.seq, nxt);
-        if (live) {
+// Online row statistics of one lane (one query): fold the valid logits of a
+// tile (raw dot products acc[j], j in [0, 16) x NT tiles) into (mt, m, nm, z):
+// mt the largest raw logit so far; m <= mt the reference the sum is kept
+// against, nm = -round_T(round_T(m) * scaling) * log2(e); z = sum of
+// exp2(x * log2(e) + nm) over the logits folded in.  The reference moves (and
+// z is rescaled) only when a logit exceeds it by more than span, the raw
+// logit distance whose exp2 argument is 32: every term stays below 2^32, the
+// sum far from overflow, and most tiles skip the rescale.  The row's true
+// maximum is applied once at the end.
+template <int DT, int NT, bool MASKED>
+__device__ __forceinline__ void row_fold(const f32x16 (&acc)[NT], float scaling, float span, int diag_key, int g,
+                                         float& mt, float& m, float& nm, float& z) {
+    float tm = -__builtin_inff();
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int kt = 2 * it + h;
-                if (kt > my_diag) continue;
-                const f32x16 acc = logits_regs_lds<DT, D>(qa, cur + h * 32 * RealTile<D>::ROWB, c, g);
-                if (kt < my_diag) {  // every key of the block precedes every row of the wave
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-                    for (int j = 0; j < 16; j += 2) {
-                        if constexpr (PASS == 0) {
-                            m[j] = __builtin_fmaxf(m[j], acc[j]);
-                            m[j + 1] = __builtin_fmaxf(m[j + 1], acc[j + 1]);
-                        } else {
-                            float x0, x1;
-                            exp_args2<DT>(acc[j], acc[j + 1], a.scaling, m[j], m[j + 1], x0, x1);
-                            z[j] += __builtin_amdgcn_exp2f(x0);
-                            z[j + 1] += __builtin_amdgcn_exp2f(x1);
-                        }
-                    }
-                } else {
-                    const int key = kt * 32 + c;
+        for (int j = 0; j < 16; ++j)
+            tm = fmaxf(tm, (!MASKED || acc_row(j, 32 * g) <= diag_key) ? acc[t][j] : -__builtin_inff());
+    mt = fmaxf(mt, tm);
+    if (tm > m + span) {  // per lane: move the reference to this tile's maximum, rescale the sum
+        const float nm_new = -(eager_logit<DT>(tm, scaling) * kLog2e);
+        z = m == -__builtin_inff() ? 0.0f : z * __builtin_amdgcn_exp2f(nm_new - nm);
+        m = tm;
+        nm = nm_new;
+    }
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        const int i = q0 + acc_row(j, lane);
-                        const bool valid = key <= i && i < a.seq;
-                        if constexpr (PASS == 0) {
-                            m[j] = valid ? __builtin_fmaxf(m[j], acc[j]) : m[j];
-                        } else {
-                            const float e = __builtin_amdgcn_exp2f(
-                                __builtin_fmaf(eager_logit<DT>(acc[j], a.scaling), kLog2e, m[j]));
-                            z[j] += valid ? e : 0.0f;
-                        }
-                    }
-                }
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) {
+            float x0, x1;
+            exp_args2<DT>(acc[t][j], acc[t][j + 1], scaling, nm, nm, x0, x1);
+            const float e0 = __builtin_amdgcn_exp2f(x0), e1 = __builtin_amdgcn_exp2f(x1);
+            if constexpr (MASKED) {
+                z += acc_row(j, 32 * g) <= diag_key ? e0 : 0.0f;
+                z += acc_row(j + 1, 32 * g) <= diag_key ? e1 : 0.0f;
+            } else {
+                z += e0;
+                z += e1;
             }
         }
-        __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this thread's part of the next stage has landed
-        __syncthreads();
-    };
-#pragma unroll 1
-    for (int it = 0; it < n_it; it += 2) {
-        stage(it, lds0, lds1);
-        if (it + 1 < n_it) stage(it + 1, lds1, lds0);
-    }
 }
 
 template <int DT, int D>
@@ -454,33 +470,102 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     const uint16_t* kbase = static_cast<const uint16_t*>(a.k) + ((size_t)b * a.hkv + hk) * a.seq * D;
     const int q0 = qb * 128 + wave * 32;             // this wave's first query row
     const bool live = q0 < a.seq;                    // wave-uniform
+    const int my_diag = q0 / 32;                     // the key tile on this wave's diagonal
     const int last_key = min(qb * 128 + 127, a.seq - 1);
     const int n_it = last_key / 64 + 1;              // 64-key stages
     uint4 qa[RealTile<D>::KS];
     row_operand<D>(qbase, q0 + c, a.seq, g, qa);
-
-    float m[16], z[16];
+    // this lane: query q0 + c, keys tile * 32 + acc_row(j, g)
+    float mt = -__builtin_inff(), m = -__builtin_inff(), nm = 0.0f, z = 0.0f;
+    // raw logit distance with exp2 argument 32 (|round_T| error is far below it)
+    const float span = 32.0f / (a.scaling * kLog2e);
+    const DmaPlan<D> plan;
+    tile_dma<D>(plan, kbase, 0, a.seq, lds0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    auto stage = [&](int it, const char* cur, char* nxt) {
+        if (it + 1 < n_it) tile_dma<D>(plan, kbase, (it + 1) * 64, a.seq, nxt);
+        if (live) {
+            const int kt0 = 2 * it;
+            if (kt0 + 1 < my_diag) {  // both tiles wholly before this wave's queries: no mask
+                f32x16 acc[2];
+                acc[0] = logits_lds_regs<DT, D>(cur, qa, c, g);
+                acc[1] = logits_lds_regs<DT, D>(cur + 32 * RealTile<D>::ROWB, qa, c, g);
+                row_fold<DT, 2, false>(acc, a.scaling, span, 0, g, mt, m, nm, z);
+            } else {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        m[j] = -__builtin_inff();
-        z[j] = 0.0f;
+                for (int h = 0; h < 2; ++h) {
+                    const int kt = kt0 + h;
+                    if (kt > my_diag) break;
+                    f32x16 acc[1];
+                    acc[0] = logits_lds_regs<DT, D>(cur + h * 32 * RealTile<D>::ROWB, qa, c, g);
+                    if (kt < my_diag) row_fold<DT, 1, false>(acc, a.scaling, span, 0, g, mt, m, nm, z);
+                    else row_fold<DT, 1, true>(acc, a.scaling, span, c, g, mt, m, nm, z);  // key <= query
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this thread's part of the next stage has landed
+        __syncthreads();
+    };
+#pragma unroll 1
+    for (int it = 0; it < n_it; it += 2) {
+        stage(it, lds0, lds1);
+        if (it + 1 < n_it) stage(it + 1, lds1, lds0);
     }
-    rowstats_sweep<DT, D, 0>(a, kbase, lds0, lds1, qa, n_it, live, q0, lane, m, z);
-    // row max of the raw logits -> max of the eager logits -> -max * log2(e)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) m[j] = -(eager_logit<DT>(reduce32_max(m[j]), a.scaling) * kLog2e);
-    rowstats_sweep<DT, D, 1>(a, kbase, lds0, lds1, qa, n_it, live, q0, lane, m, z);
     if (!live) return;
-    const size_t stat = (size_t)bhq * a.seq;
+    // lanes c and c + 32 hold the same query over disjoint keys: the row
+    // maximum, and both sums moved from their references to it
+    const float M = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float nmM = -(eager_logit<DT>(M, a.scaling) * kLog2e);
+    float zs = m == -__builtin_inff() ? 0.0f : z * __builtin_amdgcn_exp2f(nmM - nm);
+    const float m_o = __shfl_xor(m, 32, 64), nm_o = __shfl_xor(nm, 32, 64), z_o = __shfl_xor(z, 32, 64);
+    zs += m_o == -__builtin_inff() ? 0.0f : z_o * __builtin_amdgcn_exp2f(nmM - nm_o);
+    const int i = q0 + c;
+    if (g == 0 && i < a.seq) {
+        const size_t stat = (size_t)bhq * a.seq;
+        a.row_max[stat + i] = nmM;
+        a.row_sum[stat + i] = 1.0f / zs;
+    }
+}
+
+// Column sums of one 32 x 32 tile of a lane's key column (queries = rows
+// acc_row(j, g)): p = round_T(exp2(x * log2(e) + nm[row]) * rz[row]) with x the
+// eager logit, then colacc += P^T . ones on the matrix cores.  The lane's 16
+// rounded values of key c are exactly row c of an A operand (8 per MFMA, in
+// any k order since B is all ones), so two 32x32x16 MFMAs add them in fp32;
+// every lane of the result then holds the running sums of 16 keys.  MASKED:
+// rows r with r < key_off (row before the key) or r >= row_end (past seq)
+// contribute 0.
+template <int DT, bool MASKED>
+__device__ __forceinline__ void col_fold(const f32x16& acc, const float* nm_rows, const float* rz_rows, float scaling,
+                                         int key_off, int row_end, int g, f32x16& colacc) {
+    uint32_t pk[8];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const float zs = reduce32_sum(z[j]);
-        const int i = q0 + acc_row(j, lane);
-        if (c == 0 && i < a.seq) {
-            a.row_max[stat + i] = m[j];
-            a.row_sum[stat + i] = 1.0f / zs;
+    for (int jq = 0; jq < 4; ++jq) {
+        const int r0 = 8 * jq + 4 * g;  // rows r0 .. r0 + 3 of the 32-row block
+        const float4 nm4 = *reinterpret_cast<const float4*>(&nm_rows[r0]);
+        const float4 rz4 = *reinterpret_cast<const float4*>(&rz_rows[r0]);
+        const float nm[4] = {nm4.x, nm4.y, nm4.z, nm4.w};
+        const float rz[4] = {rz4.x, rz4.y, rz4.z, rz4.w};
+#pragma unroll
+        for (int u = 0; u < 4; u += 2) {
+            const int j = 4 * jq + u;
+            float x0, x1;
+            exp_args2<DT>(acc[j], acc[j + 1], scaling, nm[u], nm[u + 1], x0, x1);
+            float p0 = __builtin_amdgcn_exp2f(x0) * rz[u];
+            float p1 = __builtin_amdgcn_exp2f(x1) * rz[u + 1];
+            if constexpr (MASKED) {
+                const int r = r0 + u;
+                p0 = key_off <= r && r < row_end ? p0 : 0.0f;
+                p1 = key_off <= r + 1 && r + 1 < row_end ? p1 : 0.0f;
+            }
+            pk[j / 2] = round_pair<DT>(p0, p1);
         }
     }
+    constexpr uint32_t one2 = DT == NQ_F16 ? 0x3C003C00u : 0x3F803F80u;  // (1.0, 1.0) in the model type
+    const uint4 ones = make_uint4(one2, one2, one2, one2);
+    colacc = mfma16<DT>(make_uint4(pk[0], pk[1], pk[2], pk[3]), ones, colacc);
+    colacc = mfma16<DT>(make_uint4(pk[4], pk[5], pk[6], pk[7]), ones, colacc);
 }
 
 template <int DT, int D>
@@ -509,12 +594,13 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
     const bool live = k0 < a.seq;
     uint4 kr[RealTile<D>::KS];
     row_operand<D>(kbase, key, a.seq, g, kr);
-    float col = 0.0f;
+    f32x16 colacc = {};  // row r = key k0 + r: its column sum (every column holds it)
     // One stage: 64 query rows by direct-to-LDS loads, and (wave 0) their row
     // statistics, one dword per lane.  Two buffers in fixed roles as in
-    // rowstats_sweep; each thread waits for its own loads before the barrier.
+    // real_rowstats; each thread waits for its own loads before the barrier.
+    const DmaPlan<D> plan;
     auto load_stage = [&](int it, char* buf, float* nm, float* rz) {
-        tile_dma<D>(qbase, it * 64, a.seq, buf);
+        tile_dma<D>(plan, qbase, it * 64, a.seq, buf);
         if (wave == 0) {
             const int i = min(it * 64 + lane, a.seq - 1);
             __builtin_amdgcn_global_load_lds((global_void_t*)(a.row_max + stat + i), (lds_void_t*)nm, 4, 0, 0);
@@ -528,36 +614,26 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
                      float* nrz) {
         if (it + 1 < n_it) load_stage(it + 1, nxt, nnm, nrz);
         if (live) {
+            const int qt0 = 2 * it;
+            if (qt0 > my_first && qt0 * 32 + 64 <= a.seq) {
+                // both blocks interior (all rows after all keys, all rows < seq):
+                // one basic block, so the second tile's MFMAs run under the
+                // first tile's VALU work
+                const f32x16 acc0 = logits_lds_regs<DT, D>(cur, kr, c, g);
+                const f32x16 acc1 = logits_lds_regs<DT, D>(cur + 32 * RealTile<D>::ROWB, kr, c, g);
+                col_fold<DT, false>(acc0, cnm, crz, a.scaling, 0, 0, g, colacc);
+                col_fold<DT, false>(acc1, cnm + 32, crz + 32, a.scaling, 0, 0, g, colacc);
+            } else {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int qt = 2 * it + h;
-                if (qt < my_first) continue;
-                const f32x16 acc = logits_lds_regs<DT, D>(cur + h * 32 * RealTile<D>::ROWB, kr, c, g);
-                // interior blocks (all rows after all keys, all rows < seq) skip the masks
-                const bool interior = qt > my_first && qt * 32 + 32 <= a.seq;
-#pragma unroll
-                for (int jq = 0; jq < 4; ++jq) {
-                    const int r0 = 8 * jq + 4 * g;  // rows r0 .. r0 + 3 of the 32-row block
-                    const float4 nm4 = *reinterpret_cast<const float4*>(&cnm[32 * h + r0]);
-                    const float4 rz4 = *reinterpret_cast<const float4*>(&crz[32 * h + r0]);
-                    const float nm[4] = {nm4.x, nm4.y, nm4.z, nm4.w};
-                    const float rz[4] = {rz4.x, rz4.y, rz4.z, rz4.w};
-#pragma unroll
-                    for (int u = 0; u < 4; u += 2) {
-                        const int j = 4 * jq + u;
-                        const int i = qt * 32 + r0 + u;
-                        float x0, x1;
-                        exp_args2<DT>(acc[j], acc[j + 1], a.scaling, nm[u], nm[u + 1], x0, x1);
-                        const float p0 = __builtin_amdgcn_exp2f(x0) * rz[u];
-                        const float p1 = __builtin_amdgcn_exp2f(x1) * rz[u + 1];
-                        if (interior) {
-                            col = add_rounded2<DT>(col, p0, p1, true, true);
-                        } else {
-                            const bool v0 = (qt > my_first || key <= i) && i < a.seq;
-                            const bool v1 = (qt > my_first || key <= i + 1) && i + 1 < a.seq;
-                            col = add_rounded2<DT>(col, p0, p1, v0, v1);
-                        }
-                    }
+                for (int h = 0; h < 2; ++h) {
+                    const int qt = qt0 + h;
+                    if (qt < my_first) continue;
+                    const f32x16 acc = logits_lds_regs<DT, D>(cur + h * 32 * RealTile<D>::ROWB, kr, c, g);
+                    if (qt > my_first && qt * 32 + 32 <= a.seq)
+                        col_fold<DT, false>(acc, cnm + 32 * h, crz + 32 * h, a.scaling, 0, 0, g, colacc);
+                    else
+                        col_fold<DT, true>(acc, cnm + 32 * h, crz + 32 * h, a.scaling, key - qt * 32,
+                                           a.seq - qt * 32, g, colacc);
                 }
             }
         }
@@ -569,8 +645,14 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
         stage(it, lds0, st_nm0, st_rz0, lds1, st_nm1, st_rz1);
         if (it + 1 < n_it) stage(it + 1, lds1, st_nm1, st_rz1, lds0, st_nm0, st_rz0);
     }
-    col += __shfl_xor(col, 32, 64);
-    if (g == 0 && key < a.seq) a.colsum[stat + key] = col;
+    // lanes 0 and 32 hold the sums of keys k0 + acc_row(j, g), j = 0..15
+    if (c == 0 && live) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int kk = k0 + acc_row(j, lane);
+            if (kk < a.seq) a.colsum[stat + kk] = colacc[j];
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void head_mean_accumulate(const float* colsum, float* importance, int hq,
