@@ -119,8 +119,9 @@ def _timed(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
-def aux_workload(name, steps, warmup):
-    """Secondary configs (BASELINE.json configs[2..4]); one JSON line each."""
+def aux_workload(name, steps, warmup, emit=True):
+    """Secondary configs (BASELINE.json configs[2..4]); one JSON line each
+    (emit=False: return the record instead of printing it)."""
     import torch
     import nexusquant_amd as nq
     from nexusquant_amd.scoring import score_real_accumulate
@@ -147,13 +148,27 @@ def aux_workload(name, steps, warmup):
         comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.25, sliding_window=32,
                                   obs_window=32, rope_base=10000.0)
         score_ms = _timed(torch, lambda: comp._score_importance(ks[0]), steps, warmup) * 1e3
+        # device time of the scorer alone: the no-allocation entry point with a
+        # preallocated output keeps the host out of the way
+        from nexusquant_amd.ops import score_keykey_noalloc
+        imp_out = torch.empty(4, 8192, device=dev)
+        for _ in range(3):
+            score_keykey_noalloc(ks[0], 32, out=imp_out)
+        e_a, e_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e_a.record()
+        for _ in range(50):
+            score_keykey_noalloc(ks[0], 32, out=imp_out)
+        e_b.record()
+        torch.cuda.synchronize()
+        kk_dev_ms = e_a.elapsed_time(e_b) / 50
         step_ms = _timed(torch, lambda: comp.compress(Cache(ks, vs)), steps, warmup) * 1e3
         elems = 2 * 32 * 4 * 8 * 8192 * 128
         out.update(config={"workload": "light eviction, key-key scorer: Mistral-7B shape, 32 layers x K,V fp16 "
                            "[4, 8, 8192, 128], 25% eviction, BOS + last 32 kept, K3V2 on survivors"},
                    ms_per_step=round(step_ms, 3), value=round(step_ms, 3),
                    keykey_score_ms=round(score_ms, 4),
-                   keykey_score_gbs=round(4 * 8 * 8192 * 128 * 2 / (score_ms * 1e-3) / 1e9, 1),
+                   keykey_device_ms=round(kk_dev_ms, 4),
+                   keykey_score_gbs=round(4 * 8 * 8192 * 128 * 2 / (kk_dev_ms * 1e-3) / 1e9, 1),
                    gbs_fp16_compressed=round(2 * elems / (step_ms * 1e-3) / 1e9, 1))
     elif name == "c4":
         s, hq, hkv, d, layers = 8192, 32, 8, 128, 32
@@ -180,7 +195,7 @@ def aux_workload(name, steps, warmup):
                    roofline={"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                              "algorithmic_flops": flops,
-                             "note": "two causal QK^T passes per layer (the kernel runs three sweeps)"})
+                             "note": "two causal QK^T passes per layer, as the kernels run them"})
     elif name in ("c5a", "c5b"):
         if name == "c5a":
             layers, h, d, rate, desc = 32, 32, 96, 0.60, "Phi-3-mini shape, 32 layers x K,V fp16 [1, 32, 16384, 96]"
@@ -215,7 +230,9 @@ def aux_workload(name, steps, warmup):
                    merge_value_gbs=round(2 * v_bytes / (merge_ms * 1e-3) / 1e9, 1))
     else:
         raise SystemExit(f"unknown workload {name}")
-    print(json.dumps(out), flush=True)
+    if emit:
+        print(json.dumps(out), flush=True)
+    return out
 
 
 def e8mm_workload(steps, warmup):
@@ -223,24 +240,36 @@ def e8mm_workload(steps, warmup):
     one Llama-3-70B layer's keys as standalone E8 codes (8 kv heads x 131072
     tokens = 1048576 rows of 128 int8 codes, fp32 scales) against the 8 query
     heads of a group (Q_cols 8).  Bytes are the codes, scales, query and the
-    fp32 output; HBM bound.  The CPU leg times the oracle (torch CPU, fp32
-    decode then float64 product) on 65536 rows."""
+    fp32 output; HBM bound.  Calls rotate over 4 layers' code buffers (688 MB
+    of codes, scales and outputs, above the 256 MB last-level cache), so each
+    call reads its codes from HBM.  The CPU leg times the oracle (torch CPU,
+    fp32 decode then float64 product) on 65536 rows."""
     import torch
     from nexusquant_amd.kernels import e8_dequant_matmul
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(13)
-    k_rows, h, qc = 8 * 131072, 128, 8
-    codes = torch.randint(-8, 9, (k_rows, h), device=dev, generator=gen, dtype=torch.int8)
-    scales = torch.rand(k_rows, device=dev, generator=gen) * 0.1 + 1e-3
+    k_rows, h, qc, n_sets = 8 * 131072, 128, 8, 4
+    sets = []
+    for _ in range(n_sets):
+        codes = torch.randint(-8, 9, (k_rows, h), device=dev, generator=gen, dtype=torch.int8)
+        scales = torch.rand(k_rows, device=dev, generator=gen) * 0.1 + 1e-3
+        sets.append((codes, scales))
     query = torch.randn(h, qc, device=dev, generator=gen)
+    codes, scales = sets[0]
     out = e8_dequant_matmul(codes, scales, query)
-    ms = _timed(torch, lambda: e8_dequant_matmul(codes, scales, query), steps, warmup) * 1e3
+    it = [0]
+
+    def call():
+        c, sc = sets[it[0] % n_sets]
+        it[0] += 1
+        return e8_dequant_matmul(c, sc, query)
+    ms = _timed(torch, call, steps, warmup) * 1e3
     stream = torch.cuda.current_stream(dev)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n_ev = max(steps, 5)
+    n_ev = max(steps, 8)
     ev0.record(stream)
     for _ in range(n_ev):
-        e8_dequant_matmul(codes, scales, query)
+        call()
     ev1.record(stream)
     torch.cuda.synchronize()
     ev_ms = ev0.elapsed_time(ev1) / n_ev
@@ -259,9 +288,9 @@ def e8mm_workload(steps, warmup):
         reps += 1
     cpu_s = (time.perf_counter() - t0) / reps
     return dict(config={"workload": f"e8_dequant_matmul: int8 codes [{k_rows}, {h}] (8 kv heads x 131072 tokens), "
-                        f"query [{h}, {qc}]"},
+                        f"query [{h}, {qc}]; calls rotate over {n_sets} code buffers"},
                 ms_per_step=round(ms, 4), value=round(ms, 4), ms_per_call_events=round(ev_ms, 4),
-                bytes_per_call=nbytes,
+                bytes_per_call=nbytes, working_set_bytes=n_sets * nbytes,
                 roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
                 cpu_baseline={"value": round(n_s * h / cpu_s / 1e9, 4), "unit": "G codes/s",
@@ -378,12 +407,98 @@ def decode_workload(name, steps, warmup):
                 fp16_equivalent_gbs=round(fp16_bytes / (ev_ms * 1e-3) / 1e9, 1))
 
 
+def entropy_stage(ck, cv, torch):
+    """The delta + zstd stage after the C2 step: the GPU delta kernel
+    (nq_codes_to_int8 with token deltas) over all 80 layers' K and V codes,
+    then host zstd, timed separately: level 3 on the full int8 delta stream,
+    one zstd frame per layer (K then V, the accounting layout) compressed by a
+    pool of host threads, and level 22 (the reference default) on a subsample."""
+    from concurrent.futures import ThreadPoolExecutor
+    import numpy as np
+    from nexusquant_amd.codec import Zstd, codes_int8
+    dev = ck[0].scales.device
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    codes_int8(ck[:1], delta=True)  # warm: tables, address ring
+    torch.cuda.synchronize()
+    e0.record(stream)
+    dk = codes_int8(ck, delta=True)
+    dv = codes_int8(cv, delta=True)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    delta_ms = e0.elapsed_time(e1)
+    n_out = sum(t.numel() for t in dk + dv)
+    n_in = sum(c.syms.numel() + c.cosets.numel() + 4 * c.scales.numel() for c in list(ck) + list(cv))
+    z = Zstd.get()
+    threads = len(os.sched_getaffinity(0))
+    # level 3 on the whole stream: copy a layer to the host, compress its K+V
+    # frame on a worker while the next layer is copied
+    t0 = time.perf_counter()
+    comp_bytes = 0
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        futs = []
+        for a, c in zip(dk, dv):
+            chunk = np.concatenate([a.reshape(-1).cpu().numpy(), c.reshape(-1).cpu().numpy()])
+            futs.append(pool.submit(lambda buf: len(z.compress(buf, 3)), chunk))
+            if len(futs) >= 2 * threads:
+                comp_bytes += futs.pop(0).result()
+        comp_bytes += sum(f.result() for f in futs)
+    fast_s = time.perf_counter() - t0
+    # level 22 on a bounded subsample: the first 8 MiB of layer 0's key deltas
+    sample = dk[0].reshape(-1)[:8 << 20].cpu().numpy()
+    t0 = time.perf_counter()
+    c22 = len(z.compress(sample, 22))
+    l22_s = time.perf_counter() - t0
+    c3_sample = len(z.compress(sample, 3))
+    fp16_bytes = 2 * sum(c.scales.numel() * c.head_dim for c in list(ck) + list(cv))
+    del dk, dv
+    v = z.version()
+    return {
+        "gpu_delta": {"ms": round(delta_ms, 3), "bytes_read": n_in, "bytes_written": n_out,
+                      "gbs": round((n_in + n_out) / (delta_ms * 1e-3) / 1e9, 1),
+                      "kernel": "int8_codes_kernel (delta) over 80 layers x K, V packed codes"},
+        "zstd_fast_full_stream": {"level": 3, "stream_bytes": n_out, "compressed_bytes": comp_bytes,
+                                  "seconds": round(fast_s, 2), "gbs": round(n_out / fast_s / 1e9, 2),
+                                  "host_threads": threads, "frames": len(ck),
+                                  "ratio_vs_int8": round(n_out / comp_bytes, 3),
+                                  "ratio_vs_fp16_kv": round(fp16_bytes / comp_bytes, 3),
+                                  "note": "includes the device-to-host copies; one frame per layer"},
+        "zstd_22_subsample": {"level": 22, "sample_bytes": int(sample.size), "compressed_bytes": c22,
+                              "seconds": round(l22_s, 2), "mbs": round(sample.size / l22_s / 1e6, 2),
+                              "ratio_vs_int8": round(sample.size / c22, 3),
+                              "level3_ratio_same_sample": round(sample.size / c3_sample, 3),
+                              "sample": "first 8 MiB of layer 0's key delta stream", "host_threads": 1},
+        "libzstd": f"{v // 10000}.{v // 100 % 100}.{v % 100}",
+    }
+
+
+def aux_summary(steps=2, warmup=1):
+    """C3, C4, C5a, C5b step times (no CPU leg) for the headline record."""
+    out = {}
+    for name in ("c3", "c4", "c5a", "c5b"):
+        r = aux_workload(name, steps, warmup, emit=False)
+        out[f"{name}_ms_per_step"] = r["ms_per_step"]
+        for k in ("keykey_score_ms", "keykey_device_ms", "keykey_score_gbs", "real_score_ms", "evict_quant_ms",
+                  "gbs_fp16_compressed"):
+            if k in r:
+                out[f"{name}_{k}"] = r[k]
+        if name == "c4":
+            out["c4_real_scorer_roofline"] = r["roofline"]
+        import torch
+        torch.cuda.empty_cache()
+    out["note"] = (f"{steps} timed steps after {warmup} warmup each; workloads and units as "
+                   "bench.py --workload aux prints them")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the delta + zstd stage and the C3-C5 step times after the headline")
     ap.add_argument("--workload", default="c2",
                     help="c2 (headline, default), a secondary config: c3, c4, c5a, c5b, aux (all four), "
                          "decode70b / decode7b (paged decode attention from compressed pages), rans (GPU "
@@ -503,6 +618,15 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(keys, values, torch)
+    if not args.no_extras:
+        rk, ck, rv, cv = step()
+        del rk, rv
+        result["entropy_stage"] = entropy_stage(ck, cv, torch)
+        del ck, cv, keys, values
+        gc.unfreeze()
+        gc.collect()
+        torch.cuda.empty_cache()
+        result["aux"] = aux_summary()
     print(json.dumps(result), flush=True)
 
 
