@@ -455,23 +455,11 @@ def resolve_layer_levels(layer: int, n_layers: int, key_levels: int, value_level
 # Eviction pipelines
 # ---------------------------------------------------------------------------
 
-def evict_mask_compress(cache, key_levels: int, value_levels: int, rate: float,
-                        sliding_window: int = 32, obs_window: int = 32, rope_base: float = 10000.0,
-                        rope_scaling: Optional[dict] = None, importance: Optional[torch.Tensor] = None,
-                        skip_layers: Sequence[int] = (), protected_positions=None,
-                        layer_bit_profile: str = "uniform"):
-    """Hard-eviction mask path of NexusQuantEvict.compress (pipeline.py:1050-1244).
-
-    Returns (cache, mask [b, s] float).  `importance` overrides the key-key
-    scorer (used for the real-attention scorer).
-    """
+def _apply_keep_mask(cache, keep: torch.Tensor, key_levels: int, value_levels: int, rope_base: float,
+                     rope_scaling: Optional[dict], skip_layers, layer_bit_profile: str) -> None:
+    """Per-layer hard-eviction loop (pipeline.py:1190-1242): zero evicted rows,
+    quantize (skip layers: fp16 cast only), zero them again."""
     n = num_layers(cache)
-    k0, _ = get_layer_kv(cache, 0)
-    b, _, seq, _ = k0.shape
-    if importance is None:
-        importance = score_keykey(k0.float(), obs_window)
-    keep = build_keep_mask(importance, seq, rate, sliding_window, protected_positions)
-    mask_out = keep.float()
     for li in range(n):
         k, v = get_layer_kv(cache, li)
         k = k.float()
@@ -490,7 +478,98 @@ def evict_mask_compress(cache, key_levels: int, value_levels: int, rate: float,
         k_out = k_out * m4.half()
         v_out = v_out * m4.half()
         set_layer_kv(cache, li, k_out, v_out)
-    return cache, mask_out
+
+
+def evict_mask_compress(cache, key_levels: int, value_levels: int, rate: float,
+                        sliding_window: int = 32, obs_window: int = 32, rope_base: float = 10000.0,
+                        rope_scaling: Optional[dict] = None, importance: Optional[torch.Tensor] = None,
+                        skip_layers: Sequence[int] = (), protected_positions=None,
+                        layer_bit_profile: str = "uniform"):
+    """Hard-eviction mask path of NexusQuantEvict.compress (pipeline.py:1050-1244).
+
+    Returns (cache, mask [b, s] float).  `importance` overrides the key-key
+    scorer (used for the real-attention scorer).
+    """
+    k0, _ = get_layer_kv(cache, 0)
+    b, _, seq, _ = k0.shape
+    if importance is None:
+        importance = score_keykey(k0.float(), obs_window)
+    keep = build_keep_mask(importance, seq, rate, sliding_window, protected_positions)
+    _apply_keep_mask(cache, keep, key_levels, value_levels, rope_base, rope_scaling, skip_layers, layer_bit_profile)
+    return cache, keep.float()
+
+
+def auto_detect_boundary(cache) -> int:
+    """Boundary protection probe (pipeline.py:863-893): 2 when the mean |key| of
+    the first and last layers is more than twice the middle layer's, else 0;
+    0 below 6 layers."""
+    n = num_layers(cache)
+    if n < 6:
+        return 0
+    k_first, _ = get_layer_kv(cache, 0)
+    k_last, _ = get_layer_kv(cache, n - 1)
+    k_mid, _ = get_layer_kv(cache, n // 2)
+    mag_boundary = (k_first.float().abs().mean() + k_last.float().abs().mean()) / 2
+    mag_middle = k_mid.float().abs().mean()
+    return 2 if (mag_boundary / (mag_middle + 1e-8)).item() > 2.0 else 0
+
+
+def swa_layers_from_config(model_config) -> set:
+    """Sliding-window layers of a hybrid model (pipeline.py:670-710): a
+    sliding_window_pattern (every layer except each pattern-th), else
+    layer_types naming local layers, else the last num_kv_shared_layers."""
+    cfg = getattr(model_config, "text_config", model_config)
+    swa = set()
+    n = getattr(cfg, "num_hidden_layers", 32)
+    pattern = getattr(cfg, "sliding_window_pattern", None)
+    if pattern is not None:
+        for i in range(n):
+            if (i + 1) % pattern != 0:
+                swa.add(i)
+    types = getattr(cfg, "layer_types", None)
+    if types is not None and not swa:
+        for i, lt in enumerate(types):
+            if lt in ("sliding_window", "local", "swa", "sliding_attention"):
+                swa.add(i)
+    shared = getattr(cfg, "num_kv_shared_layers", 0)
+    if shared > 0 and not swa:
+        for i in range(n - shared, n):
+            swa.add(i)
+    return swa
+
+
+def evict_compress(cache, key_levels: int, value_levels: int, eviction_rate, sliding_window: int = 32,
+                   obs_window: int = 32, rope_base: float = 10000.0, rope_scaling: Optional[dict] = None,
+                   protected_layers=(), protect_boundary=0, min_context_for_compression: int = 0,
+                   adaptive_context: bool = False, distance_graduated: bool = False, swa_layers=None,
+                   protected_positions=None, layer_bit_profile: str = "uniform"):
+    """NexusQuantEvict.compress, hard-eviction mask mode, with every option
+    (pipeline.py:1050-1127 then :1190-1244): the scoring layer is the first
+    non-SWA layer when swa_layers is given ("global_only"), the rate is "auto"
+    (entropy) or fixed, scaled by adaptive_context; the keep mask may carry the
+    distance ramp; boundary protection is an int or "auto"; SWA layers are
+    skipped; a prefix shorter than min_context_for_compression passes through.
+
+    Returns (cache, mask [b, s] float, resolved rate, skipped layer set)."""
+    n = num_layers(cache)
+    score_layer = 0
+    if swa_layers:
+        score_layer = next((li for li in range(n) if li not in swa_layers), 0)
+    k_score, _ = get_layer_kv(cache, score_layer)
+    b, _, seq, _ = k_score.shape
+    importance = score_keykey(k_score.float(), obs_window)
+    rate = auto_eviction_rate(importance, seq) if eviction_rate == "auto" else float(eviction_rate)
+    if adaptive_context:
+        rate = adaptive_context_rate(rate, seq)
+    keep = build_keep_mask(importance, seq, rate, sliding_window, protected_positions, distance_graduated)
+    n_protect = auto_detect_boundary(cache) if protect_boundary == "auto" else int(protect_boundary)
+    skip = boundary_skip_layers(n, n_protect, protected_layers)
+    if swa_layers:
+        skip |= set(swa_layers)
+    if min_context_for_compression > 0 and seq < min_context_for_compression:
+        return cache, torch.ones(b, seq), rate, skip
+    _apply_keep_mask(cache, keep, key_levels, value_levels, rope_base, rope_scaling, skip, layer_bit_profile)
+    return cache, keep.float(), rate, skip
 
 
 def merge_centroids(value_layers: Sequence[torch.Tensor], bi: int) -> Optional[torch.Tensor]:

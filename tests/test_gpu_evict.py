@@ -8,6 +8,8 @@ import torch
 
 from oracle import torch_ref as T
 
+from gpu_helpers import assert_close_rows as _assert_close_rows, keep_sets_match as _keep_sets_match
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
@@ -24,24 +26,6 @@ def _keys(b, h, s, d, dtype, seed, sink=True):
     if sink:
         k[:, :, 0, :] *= 4
     return k.to(dtype)
-
-
-def _keep_sets_match(imp_gpu, imp_ref, keep_gpu, keep_ref, tol=1e-6, window=32):
-    """Keep sets identical except positions whose reference score lies within tol
-    of the k-th largest prefix score (a tie the two scorers may break differently)."""
-    diff = keep_gpu != keep_ref
-    for bi in range(keep_gpu.shape[0]):
-        idx = np.nonzero(diff[bi])[0]
-        if idx.size == 0:
-            continue
-        s = keep_ref.shape[1]
-        prefix = max(s - window, 0)
-        scores = np.sort(imp_ref[bi][1:prefix])[::-1]
-        k = int(keep_ref[bi][1:prefix].sum())
-        kth = scores[k - 1] if k > 0 else np.inf
-        if np.any(np.abs(imp_ref[bi][idx] - kth) > tol):
-            return False
-    return True
 
 
 @pytest.mark.parametrize("dtype,d,s", [(torch.float16, 128, 1000), (torch.bfloat16, 128, 777),
@@ -178,18 +162,6 @@ def test_keep_mask_ties_keep_lowest_positions_and_protected():
     # row 1: the ten high scores, then the lowest tied positions
     assert keep[1, 100:110].all()
     assert int(n_kept[0]) == int(keep[0].sum()) and int(n_kept[1]) == int(keep[1].sum())
-
-
-def _assert_close_rows(got, ref, max_flip_frac=1e-4):
-    got = got.float().cpu().numpy().reshape(-1, got.shape[-1])
-    ref = np.asarray(ref, np.float32).reshape(-1, got.shape[-1])
-    num = np.linalg.norm(got - ref, axis=1)
-    den = np.maximum(np.linalg.norm(ref, axis=1), 1e-30)
-    flipped = (num / den) > 1e-2
-    assert flipped.sum() <= max(1, int(max_flip_frac * got.size / 8)), flipped.sum()
-    ok = ~flipped
-    if ok.any() and np.linalg.norm(ref[ok]) > 0:
-        assert np.linalg.norm(got[ok] - ref[ok]) / np.linalg.norm(ref[ok]) <= 1e-3
 
 
 def test_mask_eviction_matches_reference_fixture(golden):
