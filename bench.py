@@ -214,6 +214,16 @@ def aux_workload(name, steps, warmup, emit=True):
         out.update(rans_workload(steps, warmup))
     elif name == "e8mm":
         out.update(e8mm_workload(steps, warmup))
+    elif name == "temporal":
+        from nexusquant_amd.ops import quantize_tensors
+        k, _ = synth_layer(gen, dev, torch)
+        _, cd = quantize_tensors([k], is_key=True, levels=8, rope_base=BASE, codes=True, recon=False)
+        del k
+        r = temporal_codec_stage(cd[0], torch, reps=max(steps, 1))
+        enc, dec = r["gpu_delta_encode"], r["gpu_delta_decode"]
+        out.update(config={"workload": "temporal_codec container of one C2 layer's key codes: " + r["stream"]},
+                   ms_per_step=dec["ms"], value=dec["ms"], temporal_codec=r,
+                   note="ms_per_step / value: GPU delta decode of the stream (HIP events)")
     elif name == "merge":
         ks, vs = _aux_cache(torch, gen, dev, 32, 4, 8, 8192, 128, 10000.0, True)
         comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.25, sliding_window=32,
@@ -452,8 +462,10 @@ def entropy_stage(ck, cv, torch):
     c3_sample = len(z.compress(sample, 3))
     fp16_bytes = 2 * sum(c.scales.numel() * c.head_dim for c in list(ck) + list(cv))
     del dk, dv
+    temporal = temporal_codec_stage(ck[0], torch)
     v = z.version()
     return {
+        "temporal_codec": temporal,
         "gpu_delta": {"ms": round(delta_ms, 3), "bytes_read": n_in, "bytes_written": n_out,
                       "gbs": round((n_in + n_out) / (delta_ms * 1e-3) / 1e9, 1),
                       "kernel": "int8_codes_kernel (delta) over 80 layers x K, V packed codes"},
@@ -469,6 +481,76 @@ def entropy_stage(ck, cv, torch):
                               "level3_ratio_same_sample": round(sample.size / c3_sample, 3),
                               "sample": "first 8 MiB of layer 0's key delta stream", "host_threads": 1},
         "libzstd": f"{v // 10000}.{v // 100 % 100}.{v % 100}",
+    }
+
+
+def temporal_codec_stage(code0, torch, reps=20):
+    """temporal_codec.compress_indices / decompress_indices on a real code
+    stream: layer 0's key codes as int8 2p, token-major ([tokens][heads x D],
+    the reference's [n_tokens][n_per] view).  The GPU delta kernels are timed
+    with HIP events on the launch stream (average over `reps` launches,
+    algorithmic bytes = read + write of the stream); the container end to end
+    (delta, device-to-host copy, zlib at the reference default level 22 ->
+    zlib 9) on the first 8 MiB, with the oracle's numpy + zlib on the same
+    sample beside it, and the zstd container (level 3) on the whole stream."""
+    import numpy as np
+    from nexusquant_amd import temporal_codec as TC
+    from nexusquant_amd.codec import codes_int8
+    from oracle import temporal as OT
+    dev = code0.scales.device
+    b, h, s = code0.scales.shape
+    codes = codes_int8([code0])[0]                                   # [b, h, s, D]
+    flat = codes.permute(0, 2, 1, 3).contiguous().reshape(-1)      # [b*s tokens][h*D]
+    n_tokens = b * s
+    n_per = flat.numel() // n_tokens
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    timings = {}
+    enc = TC.temporal_delta_encode(flat, n_tokens)
+    for name, fn, arg in (("encode", TC.temporal_delta_encode, flat), ("decode", TC.temporal_delta_decode, enc)):
+        fn(arg, n_tokens)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            fn(arg, n_tokens)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        timings[name] = {"ms": round(ms, 4), "gbs": round(2 * flat.numel() / (ms * 1e-3) / 1e9, 1)}
+    assert torch.equal(TC.temporal_delta_decode(enc, n_tokens), flat)
+    sample_tokens = min(n_tokens, (8 << 20) // n_per)
+    sample = flat[:sample_tokens * n_per]
+    host_sample = sample.cpu().numpy()
+    t0 = time.perf_counter()
+    blob = TC.compress_indices(sample, sample_tokens)
+    comp_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    back = TC.decompress_indices(blob, device=dev)
+    decomp_s = time.perf_counter() - t0
+    assert torch.equal(back, sample)
+    t0 = time.perf_counter()
+    ref_blob = OT.compress(host_sample, sample_tokens)
+    cpu_s = time.perf_counter() - t0
+    assert ref_blob == blob
+    t0 = time.perf_counter()
+    zblob = TC.compress_indices(flat, n_tokens, level=3, compressor="zstd")
+    z_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    zback = TC.decompress_indices(zblob, device=dev)
+    zd_s = time.perf_counter() - t0
+    assert torch.equal(zback, flat)
+    return {
+        "stream": f"layer 0 key codes, int8 2p, [{n_tokens} tokens][{n_per}]", "bytes": int(flat.numel()),
+        "gpu_delta_encode": {**timings["encode"], "kernel": "delta_encode_kernel<16>"},
+        "gpu_delta_decode": {**timings["decode"],
+                             "kernel": "delta_chunk_totals / delta_chunk_prefix / delta_chunk_scan <16>"},
+        "container_zlib": {"sample_bytes": int(sample.numel()), "level": "22 -> zlib 9",
+                           "compress_s": round(comp_s, 3), "decompress_s": round(decomp_s, 3),
+                           "compress_mbs": round(sample.numel() / comp_s / 1e6, 1),
+                           "ratio_vs_int8": round(sample.numel() / len(blob), 3),
+                           "cpu_oracle_compress_s": round(cpu_s, 3), "bytes_equal_to_oracle": True},
+        "container_zstd3": {"compress_s": round(z_s, 3), "decompress_s": round(zd_s, 3),
+                            "ratio_vs_int8": round(flat.numel() / len(zblob), 3)},
     }
 
 
@@ -502,7 +584,7 @@ def main():
     ap.add_argument("--workload", default="c2",
                     help="c2 (headline, default), a secondary config: c3, c4, c5a, c5b, aux (all four), "
                          "decode70b / decode7b (paged decode attention from compressed pages), rans (GPU "
-                         "entropy stage), merge (merge eviction), e8mm (fused E8 dequant + matrix product), "
+                         "entropy stage), temporal (temporal_codec container), merge (merge eviction), e8mm (fused E8 dequant + matrix product), "
                          "or copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define NQ_ABI_VERSION 5
+#define NQ_ABI_VERSION 6
 
 /* status codes */
 #define NQ_OK 0
@@ -223,13 +223,27 @@ int nq_dequantize(const nq_codes_desc* desc, void* stream);
  *
  * Replaces: _quantize_perhead_with_scales code output  vllm_backend.py:309-314
  *           _compress_with_delta_zstd delta step        compression_accounting.py:56-60
- *           temporal_delta_encode                       temporal_codec.py:30-52
  */
 int nq_codes_to_int8(const nq_codes_desc* desc, int32_t delta, void* stream);
 
 /*
+ * Token deltas of raw int8 rows: out[s, 0, :] = x[s, 0, :] and
+ * out[s, t, :] = x[s, t, :] - x[s, t-1, :] (int8 wrap) for n_tensors tensors
+ * of `streams` x seq x coords int8 (any coords > 0).  Addresses are aligned to
+ * 16 bytes when coords % 16 == 0, to 4 when coords % 4 == 0; out must not
+ * overlap src.  At most 2^32 - 2^22 words of 16, 4 or 1 bytes per tensor.
+ *
+ * Replaces: temporal_delta_encode  temporal_codec.py:30-52
+ */
+int nq_delta_encode(const uint64_t* src, const uint64_t* out, int32_t n_tensors, int32_t streams, int32_t seq,
+                    int32_t coords, void* stream);
+
+/*
  * Inverse of the delta stream: out[s, t, :] = sum_{u <= t} deltas[s, u, :]
- * (int8 wrap) for n_tensors tensors of `streams` x seq x coords int8.
+ * (int8 wrap) for n_tensors tensors of `streams` x seq x coords int8 (any
+ * coords > 0, alignment as for nq_delta_encode).  out may equal deltas (in
+ * place) but must not partially overlap it.  Few columns are scanned in token
+ * chunks (three launches, chunk totals staged in out), many in one launch.
  *
  * Replaces: _decompress_with_delta cumsum  compression_accounting.py:70-77
  *           temporal_delta_decode          temporal_codec.py:55-73

@@ -14,7 +14,7 @@ from .build import LIB_PATH, source_hash
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
 NQ_KEEP_ZERO, NQ_KEEP_WRITE_KEPT, NQ_KEEP_WRITE_EVICTED = 0, 1, 2
-ABI_VERSION = 5  # NQ_ABI_VERSION of the header these bindings mirror
+ABI_VERSION = 6  # NQ_ABI_VERSION of the header these bindings mirror
 _P = ctypes.c_void_p
 
 
@@ -103,6 +103,7 @@ SIGNATURES = {
     "nq_gather_rows": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "nq_dequantize": ([ctypes.POINTER(CodesDesc), _P], ctypes.c_int),
     "nq_codes_to_int8": ([ctypes.POINTER(CodesDesc), _I32, _P], ctypes.c_int),
+    "nq_delta_encode": ([_P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "nq_delta_decode": ([_P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "nq_score_real_workspace": ([_I32, _I32, _I32], _I64),
     "nq_score_real": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),

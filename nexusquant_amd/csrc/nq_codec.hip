@@ -208,22 +208,213 @@ __global__ __launch_bounds__(256) void int8_codes_kernel(CodecArgs a) {
     for (int c = 0; c < C; ++c) *reinterpret_cast<uint2*>(dst + 32 * c + 8 * q) = make_uint2(cur[c][0], cur[c][1]);
 }
 
-// Prefix sum of int8 deltas along tokens (wrapping), four coordinates per thread.
-__global__ __launch_bounds__(256) void delta_decode_kernel(const uint64_t* deltas, const uint64_t* out, uint32_t bh,
-                                                           uint32_t seq, uint32_t words_per_row, uint32_t n_cols) {
-    const uint32_t col = blockIdx.x * 256u + threadIdx.x;  // (stream, word)
-    if (col >= n_cols) return;
-    const uint32_t tensor = blockIdx.y;
-    const uint32_t stream = col / words_per_row;
-    const uint32_t word = col - stream * words_per_row;
-    const uint32_t* in = reinterpret_cast<const uint32_t*>(deltas[tensor]) + (size_t)stream * seq * words_per_row + word;
-    uint32_t* o = reinterpret_cast<uint32_t*>(out[tensor]) + (size_t)stream * seq * words_per_row + word;
-    uint32_t acc = 0;
-    for (uint32_t t = 0; t < seq; ++t) {
-        const uint32_t d = in[(size_t)t * words_per_row];
-        acc = ((acc & 0x7f7f7f7fu) + (d & 0x7f7f7f7fu)) ^ ((acc ^ d) & 0x80808080u);
-        o[(size_t)t * words_per_row] = acc;
+// ---------------------------------------------------------------------------
+// Raw int8 token deltas and their inverse over [stream][token][coord] bytes.
+// A thread owns one W-byte word of a token row (W = 16, 4 or 1 as the row
+// width allows); int8 lanes wrap like numpy's int8 arithmetic.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t add_bytes(uint32_t a, uint32_t b) {
+    return ((a & 0x7f7f7f7fu) + (b & 0x7f7f7f7fu)) ^ ((a ^ b) & 0x80808080u);
+}
+
+template <int W> struct Bytes;
+template <> struct Bytes<1> {
+    using T = uint8_t;
+    static __device__ __forceinline__ T add(T a, T b) { return (T)(a + b); }
+    static __device__ __forceinline__ T sub(T a, T b) { return (T)(a - b); }
+    static __device__ __forceinline__ T zero() { return 0; }
+};
+template <> struct Bytes<4> {
+    using T = uint32_t;
+    static __device__ __forceinline__ T add(T a, T b) { return add_bytes(a, b); }
+    static __device__ __forceinline__ T sub(T a, T b) { return sub_bytes(a, b); }
+    static __device__ __forceinline__ T zero() { return 0u; }
+};
+template <> struct Bytes<16> {
+    using T = uint4;
+    static __device__ __forceinline__ T add(T a, T b) {
+        return make_uint4(add_bytes(a.x, b.x), add_bytes(a.y, b.y), add_bytes(a.z, b.z), add_bytes(a.w, b.w));
     }
+    static __device__ __forceinline__ T sub(T a, T b) {
+        return make_uint4(sub_bytes(a.x, b.x), sub_bytes(a.y, b.y), sub_bytes(a.z, b.z), sub_bytes(a.w, b.w));
+    }
+    static __device__ __forceinline__ T zero() { return make_uint4(0u, 0u, 0u, 0u); }
+};
+
+struct DeltaGeom {
+    uint32_t seq;        // token rows per stream
+    uint32_t row_words;  // W-byte words per token row
+    uint32_t chunk_len;  // token rows per scan chunk (the last chunk may be shorter)
+    uint32_t n_chunks;
+    uint32_t n_threads;  // streams * n_chunks * row_words
+};
+
+// out[s, t] = x[s, t] - x[s, t - 1] for t > 0, x[s, 0] at t = 0.  out must not
+// alias x: the previous row is read by another thread.
+template <int W>
+__global__ __launch_bounds__(256) void delta_encode_kernel(const uint64_t* src, const uint64_t* out, uint32_t n_words,
+                                                           uint32_t row_words, uint32_t seq) {
+    using B = Bytes<W>;
+    using T = typename B::T;
+    const T* __restrict__ x = reinterpret_cast<const T*>(src[blockIdx.y]);
+    T* __restrict__ o = reinterpret_cast<T*>(out[blockIdx.y]);
+    const uint32_t stride = gridDim.x * 256u;
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n_words; i += stride) {
+        T v = x[i];
+        if ((i / row_words) % seq != 0) v = B::sub(v, x[i - row_words]);
+        o[i] = v;
+    }
+}
+
+// Word `word` of the token rows of (stream, chunk).
+__device__ __forceinline__ void delta_column(const DeltaGeom& g, uint32_t i, uint32_t& stream, uint32_t& chunk,
+                                             uint32_t& word) {
+    word = i % g.row_words;
+    const uint32_t sc = i / g.row_words;
+    chunk = sc % g.n_chunks;
+    stream = sc / g.n_chunks;
+}
+
+__device__ __forceinline__ uint32_t chunk_last_row(const DeltaGeom& g, uint32_t chunk) {
+    return min(g.seq, (chunk + 1u) * g.chunk_len) - 1u;
+}
+
+// Pass 1 of a chunked scan: the wrapping sum of each chunk's deltas, stored
+// at the chunk's last row of out.
+template <int W>
+__global__ __launch_bounds__(256) void delta_chunk_totals_kernel(const uint64_t* deltas, const uint64_t* out,
+                                                                 DeltaGeom g) {
+    using B = Bytes<W>;
+    using T = typename B::T;
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= g.n_threads) return;
+    uint32_t stream, chunk, word;
+    delta_column(g, i, stream, chunk, word);
+    const size_t base = (size_t)stream * g.seq * g.row_words + word;
+    const T* in = reinterpret_cast<const T*>(deltas[blockIdx.y]) + base;
+    T* o = reinterpret_cast<T*>(out[blockIdx.y]) + base;
+    const uint32_t t0 = chunk * g.chunk_len, t1 = chunk_last_row(g, chunk) + 1u;
+    constexpr int U = 8;
+    T acc = B::zero();
+    uint32_t t = t0;
+    for (; t + U <= t1; t += U) {
+        T d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) d[u] = in[(size_t)(t + u) * g.row_words];
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = B::add(acc, d[u]);
+    }
+    for (; t < t1; ++t) acc = B::add(acc, in[(size_t)t * g.row_words]);
+    o[(size_t)(t1 - 1u) * g.row_words] = acc;
+}
+
+// Pass 2: running sums of the chunk totals, one workgroup per (stream, word)
+// column: thread j loads the totals of chunks [j*per, (j+1)*per) (per <= 16),
+// the 256 partial sums are scanned in LDS, and each chunk's last row then
+// holds the inclusive prefix through that row.
+template <int W>
+__global__ __launch_bounds__(256) void delta_chunk_prefix_kernel(const uint64_t* out, DeltaGeom g) {
+    using B = Bytes<W>;
+    using T = typename B::T;
+    constexpr int PER = 16;
+    __shared__ T part[256];
+    const uint32_t col = blockIdx.x;
+    const uint32_t word = col % g.row_words, stream = col / g.row_words;
+    T* o = reinterpret_cast<T*>(out[blockIdx.y]) + (size_t)stream * g.seq * g.row_words + word;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t per = (g.n_chunks + 255u) / 256u;
+    const uint32_t k0 = tid * per;
+    T v[PER];
+    T sum = B::zero();
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const uint32_t k = k0 + (uint32_t)u;
+        if ((uint32_t)u < per && k < g.n_chunks) {
+            v[u] = o[(size_t)chunk_last_row(g, k) * g.row_words];
+            sum = B::add(sum, v[u]);
+        }
+    }
+    part[tid] = sum;
+    __syncthreads();
+    for (uint32_t off = 1; off < 256u; off <<= 1) {
+        const T x = tid >= off ? part[tid - off] : B::zero();
+        __syncthreads();
+        part[tid] = B::add(part[tid], x);
+        __syncthreads();
+    }
+    T acc = tid > 0 ? part[tid - 1] : B::zero();
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const uint32_t k = k0 + (uint32_t)u;
+        if ((uint32_t)u < per && k < g.n_chunks) {
+            acc = B::add(acc, v[u]);
+            o[(size_t)chunk_last_row(g, k) * g.row_words] = acc;
+        }
+    }
+}
+
+// Pass 3 (the whole scan when n_chunks == 1): prefix sums of a chunk's rows,
+// starting from the previous chunk's last row.  With several chunks the last
+// row of each chunk already holds its final value (passes 1-2) and is left as
+// it is, so no thread writes a row another thread reads.
+template <int W>
+__global__ __launch_bounds__(256) void delta_chunk_scan_kernel(const uint64_t* deltas, const uint64_t* out,
+                                                               DeltaGeom g) {
+    using B = Bytes<W>;
+    using T = typename B::T;
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= g.n_threads) return;
+    uint32_t stream, chunk, word;
+    delta_column(g, i, stream, chunk, word);
+    const size_t base = (size_t)stream * g.seq * g.row_words + word;
+    const T* in = reinterpret_cast<const T*>(deltas[blockIdx.y]) + base;
+    T* o = reinterpret_cast<T*>(out[blockIdx.y]) + base;
+    const uint32_t t0 = chunk * g.chunk_len;
+    const uint32_t t1 = g.n_chunks > 1 ? chunk_last_row(g, chunk) : g.seq;
+    T acc = chunk > 0 ? o[(size_t)(t0 - 1u) * g.row_words] : B::zero();
+    constexpr int U = 8;
+    uint32_t t = t0;
+    for (; t + U <= t1; t += U) {
+        T d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) d[u] = in[(size_t)(t + u) * g.row_words];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            acc = B::add(acc, d[u]);
+            o[(size_t)(t + u) * g.row_words] = acc;
+        }
+    }
+    for (; t < t1; ++t) {
+        acc = B::add(acc, in[(size_t)t * g.row_words]);
+        o[(size_t)t * g.row_words] = acc;
+    }
+}
+
+// Word width of a row of `coords` bytes.
+static int delta_word_bytes(int32_t coords) { return coords % 16 == 0 ? 16 : coords % 4 == 0 ? 4 : 1; }
+
+template <int W>
+static hipError_t launch_delta_encode(const uint64_t* src, const uint64_t* out, uint32_t n_tensors, uint32_t n_words,
+                                      uint32_t row_words, uint32_t seq, hipStream_t s) {
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>(((uint64_t)n_words + 255) / 256, 8192);
+    hipLaunchKernelGGL(delta_encode_kernel<W>, dim3(blocks, n_tensors), dim3(256), 0, s, src, out, n_words, row_words,
+                       seq);
+    return hipGetLastError();
+}
+
+template <int W>
+static hipError_t launch_delta_decode(const uint64_t* deltas, const uint64_t* out, uint32_t n_tensors,
+                                      uint32_t streams, DeltaGeom g, hipStream_t s) {
+    const uint32_t cols = streams * g.row_words;
+    if (g.n_chunks > 1) {
+        hipLaunchKernelGGL(delta_chunk_totals_kernel<W>, dim3((g.n_threads + 255) / 256, n_tensors), dim3(256), 0, s,
+                           deltas, out, g);
+        hipLaunchKernelGGL(delta_chunk_prefix_kernel<W>, dim3(cols, n_tensors), dim3(256), 0, s, out, g);
+    }
+    hipLaunchKernelGGL(delta_chunk_scan_kernel<W>, dim3((g.n_threads + 255) / 256, n_tensors), dim3(256), 0, s,
+                       deltas, out, g);
+    return hipGetLastError();
 }
 
 template <int D, int L, int DR>
@@ -307,18 +498,58 @@ extern "C" int nq_codes_to_int8(const nq_codes_desc* desc, int32_t delta, void* 
     return nq::run_codec(desc, delta ? 2 : 1, stream);
 }
 
+extern "C" int nq_delta_encode(const uint64_t* src, const uint64_t* out, int32_t n_tensors, int32_t streams,
+                               int32_t seq, int32_t coords, void* stream) {
+    using namespace nq;
+    NQ_CHECK_ARG(src && out, "nq_delta_encode: NULL pointer array");
+    NQ_CHECK_ARG(n_tensors >= 0 && n_tensors <= 65535 && streams >= 0 && seq >= 0 && coords > 0,
+                 "nq_delta_encode: bad shape");
+    if (n_tensors == 0 || streams == 0 || seq == 0) return NQ_OK;
+    const int W = delta_word_bytes(coords);
+    const uint64_t row_words = (uint64_t)coords / W;
+    const uint64_t n_words = (uint64_t)streams * seq * row_words;
+    NQ_CHECK_ARG(n_words < (1ull << 32) - (1ull << 22), "nq_delta_encode: tensor too large (%llu words of %d bytes)",
+                 (unsigned long long)n_words, W);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e;
+    if (W == 16) e = launch_delta_encode<16>(src, out, n_tensors, (uint32_t)n_words, (uint32_t)row_words, seq, s);
+    else if (W == 4) e = launch_delta_encode<4>(src, out, n_tensors, (uint32_t)n_words, (uint32_t)row_words, seq, s);
+    else e = launch_delta_encode<1>(src, out, n_tensors, (uint32_t)n_words, (uint32_t)row_words, seq, s);
+    NQ_CHECK_HIP(e);
+    return NQ_OK;
+}
+
 extern "C" int nq_delta_decode(const uint64_t* deltas, const uint64_t* out, int32_t n_tensors, int32_t streams,
                                int32_t seq, int32_t coords, void* stream) {
     using namespace nq;
     NQ_CHECK_ARG(deltas && out, "nq_delta_decode: NULL pointer array");
-    NQ_CHECK_ARG(n_tensors >= 0 && n_tensors <= 65535 && streams >= 0 && seq >= 0, "nq_delta_decode: bad shape");
-    NQ_CHECK_ARG(coords > 0 && coords % 4 == 0, "nq_delta_decode: coords must be a positive multiple of 4");
+    NQ_CHECK_ARG(n_tensors >= 0 && n_tensors <= 65535 && streams >= 0 && seq >= 0 && coords > 0,
+                 "nq_delta_decode: bad shape");
     if (n_tensors == 0 || streams == 0 || seq == 0) return NQ_OK;
-    const uint64_t cols = (uint64_t)streams * (coords / 4);
+    const int W = delta_word_bytes(coords);
+    DeltaGeom g;
+    g.seq = (uint32_t)seq;
+    g.row_words = (uint32_t)(coords / W);
+    const uint64_t cols = (uint64_t)streams * g.row_words;
     NQ_CHECK_ARG(cols < (1ull << 31), "nq_delta_decode: too many streams");
-    dim3 grid((uint32_t)((cols + 255) / 256), (uint32_t)n_tensors);
-    hipLaunchKernelGGL(delta_decode_kernel, grid, dim3(256), 0, (hipStream_t)stream, deltas, out, (uint32_t)streams,
-                       (uint32_t)seq, (uint32_t)(coords / 4), (uint32_t)cols);
-    NQ_CHECK_HIP(hipGetLastError());
+    // Split the token axis into chunks when the columns alone would leave the
+    // chip idle: about 2^17 threads in flight, chunks of at least 16 rows and
+    // at most 4096 chunks (16 per thread of the prefix workgroup).
+    constexpr uint64_t kTargetThreads = 1u << 17;
+    uint64_t n_chunks = 1;
+    if (cols < kTargetThreads) {
+        n_chunks = std::min<uint64_t>((kTargetThreads + cols - 1) / cols, ((uint64_t)seq + 15) / 16);
+        n_chunks = std::max<uint64_t>(1, std::min<uint64_t>(n_chunks, 4096));
+    }
+    g.chunk_len = (uint32_t)(((uint64_t)seq + n_chunks - 1) / n_chunks);
+    g.n_chunks = (uint32_t)(((uint64_t)seq + g.chunk_len - 1) / g.chunk_len);
+    NQ_CHECK_ARG(cols * g.n_chunks < (1ull << 32) - 256, "nq_delta_decode: too many columns");
+    g.n_threads = (uint32_t)(cols * g.n_chunks);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e;
+    if (W == 16) e = launch_delta_decode<16>(deltas, out, n_tensors, streams, g, s);
+    else if (W == 4) e = launch_delta_decode<4>(deltas, out, n_tensors, streams, g, s);
+    else e = launch_delta_decode<1>(deltas, out, n_tensors, streams, g, s);
+    NQ_CHECK_HIP(e);
     return NQ_OK;
 }

@@ -8,7 +8,8 @@ torch.topk keep masks, and the real-attention scorer through transformers'
 eager attention.  Nothing under /root/reference is copied; only the numbers it
 produces are stored, as small .npz files next to this script.
 
-Usage:  python tests/golden/make_golden.py [/root/reference [evict_soft | vllm_pages | evict_merge | rans]]
+Usage:  python tests/golden/make_golden.py [/root/reference [evict_soft | vllm_pages | evict_merge | rans |
+                                                              temporal_codec]]
 """
 
 from __future__ import annotations
@@ -27,6 +28,8 @@ from nexusquant.pipeline import (NexusQuantEvict, NexusQuantEvictTruncate,  # no
                                  NexusQuantQuantOnly, compress_kv_cache)
 from nexusquant.core.e8_lattice import E8Lattice  # noqa: E402
 from nexusquant.core.rope_utils import inverse_rope, forward_rope  # noqa: E402
+
+from make_golden_cases import temporal_cases  # noqa: E402
 
 
 class ListCache:
@@ -313,6 +316,26 @@ def make_vllm():
     save("vllm_pages", **out)
 
 
+def make_temporal():
+    """compress_indices / decompress_indices bytes and outputs (temporal_codec.py:76-132)."""
+    from nexusquant.core import temporal_codec as tc
+    assert not tc._HAS_ZSTD, "fixture is for the zlib branch"
+    out = {}
+    for name, coords, n_tokens, use_delta, level in temporal_cases():
+        blob = tc.compress_indices(coords, n_tokens, use_delta=use_delta, level=level)
+        out[f"{name}_coords"] = coords
+        out[f"{name}_meta"] = np.array([n_tokens, int(use_delta), level], np.int64)
+        out[f"{name}_blob"] = np.frombuffer(blob, np.uint8)
+        out[f"{name}_decoded"] = tc.decompress_indices(blob)
+        if use_delta:
+            out[f"{name}_delta"] = tc.temporal_delta_encode(coords.astype(np.int8), n_tokens)
+    m = tc.measure_compression(out["delta_coords"], 48, fp16_bytes=48 * 64 * 2, scale_bytes=48 * 8 * 2)
+    keys = sorted(m)
+    out["measure_keys"] = np.array(keys)
+    out["measure_values"] = np.array([float(m[k]) for k in keys])
+    save("temporal_codec", **out)
+
+
 if __name__ == "__main__":
     if sys.argv[2:] == ["evict_soft"]:
         make_soft()
@@ -322,9 +345,12 @@ if __name__ == "__main__":
         make_merge()
     elif sys.argv[2:] == ["rans"]:
         make_rans()
+    elif sys.argv[2:] == ["temporal_codec"]:
+        make_temporal()
     else:
         main()
         make_soft()
         make_vllm()
         make_merge()
         make_rans()
+        make_temporal()
