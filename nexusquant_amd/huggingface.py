@@ -6,7 +6,17 @@ DynamicSlidingWindowLayer.update are patched for the duration of the context;
 on each prefill-sized update of a layer the concatenated keys/values of that
 layer are compressed on the GPU and returned to the attention call.  As in the
 reference, compress() therefore sees one layer at a time, so key-key scoring
-uses each layer's own keys and protect_boundary > 0 protects that single layer.
+uses each layer's own keys and protect_boundary > 0 protects that single layer
+(huggingface.py:736-752).
+
+compat_reference_hook=False selects the full-cache semantics instead: prefill
+updates pass through uncompressed and register their layer; the registered
+layers are then compressed together by one NexusQuantEvict.compress call on the
+whole cache (layer-0 or injected real-attention scores, boundary protection
+across the model's layers, graduated bit profile, automatic boundary), as
+compress_kv_cache does after a prefill.  That happens when the model's forward
+returns, before the next update of a registered layer (a decode step or the
+next prefill chunk) and, for what is still registered, when the context exits.
 """
 
 from __future__ import annotations
@@ -89,6 +99,13 @@ class _SingleLayerCache:
         self.value_cache = [v]
 
 
+class _LayerListCache:
+    """Cache view over transformers cache-layer objects (reads and writes .keys/.values)."""
+
+    def __init__(self, layers):
+        self.layers = layers
+
+
 @contextmanager
 def nexusquant_evict(model, eviction_rate=0.6, quality: str = "balanced", sliding_window: int = 32,
                      obs_window: int = 32, bits: int = 2, key_bits: int = None, value_bits: int = None,
@@ -96,8 +113,13 @@ def nexusquant_evict(model, eviction_rate=0.6, quality: str = "balanced", slidin
                      protected_layers: set = None, protect_boundary=0, min_context_for_compression: int = 0,
                      soft_eviction: bool = False, adaptive_context: bool = False,
                      protected_positions: Optional[torch.Tensor] = None, compress_layers: str = "all",
-                     layer_bit_profile: str = "uniform", verbose: bool = True):
-    """Compress the KV cache with eviction + relaxed-E8 quantization on the first prefill."""
+                     layer_bit_profile: str = "uniform", verbose: bool = True,
+                     compat_reference_hook: bool = True):
+    """Compress the KV cache with eviction + relaxed-E8 quantization on the first prefill.
+
+    compat_reference_hook=True (default) compresses each layer alone inside its
+    update, as the reference does; False compresses the whole cache at once
+    after the prefill (see the module docstring)."""
     if quality in _EVICT_PRESETS:
         preset = _EVICT_PRESETS[quality]
         eviction_rate = preset["eviction_rate"]
@@ -151,8 +173,38 @@ def nexusquant_evict(model, eviction_rate=0.6, quality: str = "balanced", slidin
     original_dl = DynamicLayer.update
     original_dsw = DynamicSlidingWindowLayer.update
 
+    def run_compress(cache):
+        if scorer == "real" and compressor._cached_real_importance is not None:
+            cached = compressor._cached_real_importance
+            compressor._score_importance = lambda k, _imp=cached: _imp
+            try:
+                result = compressor.compress(cache)
+            finally:
+                del compressor._score_importance
+        else:
+            result = compressor.compress(cache)
+        if truncate:
+            compressor.next_position = result[1]
+        else:
+            compressor.last_mask = result[1]
+
+    # full-cache mode: cache-layer objects registered by prefill updates, in order
+    pending = []
+
+    def flush():
+        if not pending:
+            return
+        layers = list(pending)
+        pending.clear()
+        run_compress(_LayerListCache(layers))
+        for lay in layers:
+            lay.keys._nq_compressed = True
+            stats.record(lay.keys, lay.values)
+
     def make_hook(original):
         def hooked_update(self, key_states, value_states, *args, **kwargs):
+            if not compat_reference_hook and any(lay is self for lay in pending):
+                flush()
             keys, values = original(self, key_states, value_states, *args, **kwargs)
             if getattr(keys, "_nq_compressed", False):
                 return keys, values
@@ -162,20 +214,11 @@ def nexusquant_evict(model, eviction_rate=0.6, quality: str = "balanced", slidin
                 return keys, values
             if existing > 0 and incoming < max(existing * 0.1, 8):
                 return keys, values
+            if not compat_reference_hook:
+                pending.append(self)
+                return keys, values
             single = _SingleLayerCache(keys, values)
-            if scorer == "real" and compressor._cached_real_importance is not None:
-                cached = compressor._cached_real_importance
-                compressor._score_importance = lambda k, _imp=cached: _imp
-                try:
-                    result = compressor.compress(single)
-                finally:
-                    del compressor._score_importance
-            else:
-                result = compressor.compress(single)
-            if truncate:
-                compressor.next_position = result[1]
-            else:
-                compressor.last_mask = result[1]
+            run_compress(single)
             new_k, new_v = single.key_cache[0], single.value_cache[0]
             new_k._nq_compressed = True
             self.keys = new_k
@@ -186,6 +229,21 @@ def nexusquant_evict(model, eviction_rate=0.6, quality: str = "balanced", slidin
 
     DynamicLayer.update = make_hook(original_dl)
     DynamicSlidingWindowLayer.update = make_hook(original_dsw)
+    forward_patched = False
+    if not compat_reference_hook:
+        # compress right after each forward of the model (a prefill), before
+        # the caller or generate() sees the cache
+        had_own_forward = "forward" in model.__dict__
+        own_forward = model.__dict__.get("forward")
+        inner_forward = model.forward
+
+        def forward_then_compress(*args, **kwargs):
+            out = inner_forward(*args, **kwargs)
+            flush()
+            return out
+
+        model.forward = forward_then_compress
+        forward_patched = True
     if verbose:
         kb, vb = compressor.key_bits, compressor.value_bits
         bits_label = f"K={kb}-bit/V={vb}-bit E8" if kb != vb else f"{kb}-bit E8"
@@ -193,11 +251,18 @@ def nexusquant_evict(model, eviction_rate=0.6, quality: str = "balanced", slidin
         name = getattr(model.config, "_name_or_path", model.__class__.__name__)
         print(f"NexusQuantEvict (gfx950): activating on {name} (eviction={ev}, {bits_label}, "
               f"sliding_window={sliding_window}, mode={'truncate' if truncate else 'mask'}, "
-              f"scorer={scorer})", flush=True)
+              f"scorer={scorer}, {'per-layer' if compat_reference_hook else 'full-cache'})", flush=True)
     try:
         yield compressor
+        flush()
     finally:
+        pending.clear()
         DynamicLayer.update = original_dl
         DynamicSlidingWindowLayer.update = original_dsw
+        if forward_patched:
+            if had_own_forward:
+                model.forward = own_forward
+            else:
+                del model.forward
         if verbose:
             print(stats.summary(), flush=True)

@@ -542,13 +542,15 @@ def evict_compress(cache, key_levels: int, value_levels: int, eviction_rate, sli
                    obs_window: int = 32, rope_base: float = 10000.0, rope_scaling: Optional[dict] = None,
                    protected_layers=(), protect_boundary=0, min_context_for_compression: int = 0,
                    adaptive_context: bool = False, distance_graduated: bool = False, swa_layers=None,
-                   protected_positions=None, layer_bit_profile: str = "uniform"):
+                   protected_positions=None, layer_bit_profile: str = "uniform", importance=None):
     """NexusQuantEvict.compress, hard-eviction mask mode, with every option
     (pipeline.py:1050-1127 then :1190-1244): the scoring layer is the first
     non-SWA layer when swa_layers is given ("global_only"), the rate is "auto"
     (entropy) or fixed, scaled by adaptive_context; the keep mask may carry the
     distance ramp; boundary protection is an int or "auto"; SWA layers are
     skipped; a prefix shorter than min_context_for_compression passes through.
+    importance [b, s], when given, replaces the key-key scores, as the hook's
+    injected real-attention scores do (huggingface.py:743-749).
 
     Returns (cache, mask [b, s] float, resolved rate, skipped layer set)."""
     n = num_layers(cache)
@@ -557,7 +559,8 @@ def evict_compress(cache, key_levels: int, value_levels: int, eviction_rate, sli
         score_layer = next((li for li in range(n) if li not in swa_layers), 0)
     k_score, _ = get_layer_kv(cache, score_layer)
     b, _, seq, _ = k_score.shape
-    importance = score_keykey(k_score.float(), obs_window)
+    if importance is None:
+        importance = score_keykey(k_score.float(), obs_window)
     rate = auto_eviction_rate(importance, seq) if eviction_rate == "auto" else float(eviction_rate)
     if adaptive_context:
         rate = adaptive_context_rate(rate, seq)

@@ -357,3 +357,71 @@ def test_nexusquant_evict_real_scorer_matches_eager_attentions():
     imp = comp._cached_real_importance
     assert torch.allclose(imp, ref, rtol=2e-3, atol=1e-5), (imp - ref).abs().max()
     assert comp.last_mask.shape == (1, 160)
+
+
+def test_hook_full_cache_mode_keeps_c4_boundary_semantics():
+    """C4 through the hook (real scorer, 35 % eviction, first and last 2 layers
+    fp16, K3V2 between): compat_reference_hook=False compresses the whole cache
+    once with one mask, as NexusQuantEvict.compress does on a full cache."""
+    import nexusquant_amd as nq
+    from transformers import DynamicCache
+    print("[gpu] hook full-cache C4 boundary 2", flush=True)
+    model = _tiny_llama(layers=6)
+    ids = torch.randint(0, 256, (1, 256), generator=torch.Generator().manual_seed(7)).to(DEV)
+    with torch.no_grad():
+        plain = DynamicCache()
+        plain_logits = model(ids, past_key_values=plain, use_cache=True).logits
+        cache = DynamicCache()
+        with nq.nexusquant_evict(model, quality="high", scorer="real", input_ids=ids, protect_boundary=2,
+                                 compat_reference_hook=False, verbose=False) as comp:
+            logits = model(ids, past_key_values=cache, use_cache=True).logits
+    # the prefill attention saw the uncompressed cache
+    assert torch.equal(logits, plain_logits)
+    imp = comp._cached_real_importance.float().cpu()
+    ref = Cache([lay.keys.cpu() for lay in plain.layers], [lay.values.cpu() for lay in plain.layers])
+    _, ref_mask, _, skip = T.evict_compress(ref, 8, 4, 0.35, sliding_window=32, obs_window=32,
+                                            rope_base=10000.0, protect_boundary=2, importance=imp)
+    assert skip == {0, 1, 4, 5}
+    assert torch.equal(comp.last_mask.cpu(), ref_mask)
+    for li in range(6):
+        k, v = cache.layers[li].keys, cache.layers[li].values
+        assert k.dtype == torch.float16 and k.shape == plain.layers[li].keys.shape
+        if li in skip:
+            assert torch.equal(k.cpu(), ref.key_cache[li]) and torch.equal(v.cpu(), ref.value_cache[li])
+        else:
+            _assert_close_rows(k, ref.key_cache[li].numpy())
+            _assert_close_rows(v, ref.value_cache[li].numpy())
+            # quantized, not the masked fp16 passthrough
+            assert not torch.equal(k, plain.layers[li].keys * comp.last_mask[:, None, :, None].half())
+
+
+def test_hook_default_mode_protects_every_layer_with_boundary_2():
+    """The reference's per-layer hook with protect_boundary=2: each single-layer
+    compress protects its only layer, so every layer stays fp16 (evicted rows
+    zeroed) under the one injected real-attention mask."""
+    import nexusquant_amd as nq
+    from transformers import DynamicCache
+    print("[gpu] hook per-layer boundary 2", flush=True)
+    model = _tiny_llama(layers=6)
+    ids = torch.randint(0, 256, (1, 256), generator=torch.Generator().manual_seed(7)).to(DEV)
+    with torch.no_grad():
+        plain = DynamicCache()
+        model(ids, past_key_values=plain, use_cache=True)
+        cache = DynamicCache()
+        with nq.nexusquant_evict(model, quality="high", scorer="real", input_ids=ids, protect_boundary=2,
+                                 verbose=False) as comp:
+            model(ids, past_key_values=cache, use_cache=True)
+    imp = comp._cached_real_importance.float().cpu()
+    ref = Cache([plain.layers[0].keys.cpu()], [plain.layers[0].values.cpu()])
+    _, ref_mask, _, skip = T.evict_compress(ref, 8, 4, 0.35, sliding_window=32, obs_window=32,
+                                            rope_base=10000.0, protect_boundary=2, importance=imp)
+    assert skip == {0}
+    assert torch.equal(comp.last_mask.cpu(), ref_mask)
+    # layer 0 sees the plain prefill inputs: exactly the masked fp16 passthrough
+    assert torch.equal(cache.layers[0].keys.cpu(), ref.key_cache[0])
+    assert torch.equal(cache.layers[0].values.cpu(), ref.value_cache[0])
+    evicted = ~ref_mask.bool()[0]
+    for li in range(6):
+        k = cache.layers[li].keys
+        assert k.dtype == torch.float16
+        assert torch.all(k[0, :, evicted.to(DEV), :] == 0)
