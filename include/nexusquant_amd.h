@@ -483,6 +483,27 @@ int nq_e8_dequant_matmul(const int8_t* codes, const float* scales, const float* 
 int nq_e8_nearest_point(const float* x, float* out, int64_t n_groups, void* stream);
 int nq_e8_quantize_perhead(const float* x, float* out, int64_t rows, int32_t d, int32_t levels, void* stream);
 
+/*
+ * Symbol side of the single-stream E8 container (encode_e8 / decode_e8); the
+ * rANS chain is nq_rans_encode / nq_rans_decode with one chunk of n_groups * 8
+ * symbols.  Groups of 8 coordinates share scales[g], or scales[0] when
+ * n_scales == 1.
+ *   nq_e8_stream_codes: codes[i] = clip(rint(2 * (quantized[i] / max(s, 1e-8))),
+ *     -levels, levels) as int8 (IEEE fp32 division); *has_half is OR-ed with 1
+ *     when some rint(2x) is odd before the clip (|x - round(x)| > 0.25).  The
+ *     caller zeroes *has_half.  quantized 16-byte aligned, codes 8-byte aligned;
+ *     levels 2, 4, 8 or 16.
+ *   nq_e8_stream_values: out[i] = (codes[i] / 2) * fp32(scales_f16[g]) (fp32
+ *     product); codes 8-byte and out 16-byte aligned.
+ *
+ * Replaces: encode_e8 symbol mapping  entropy_coder.py:375-386, 35-75
+ *           decode_e8 reconstruction  entropy_coder.py:418-420, 78-86
+ */
+int nq_e8_stream_codes(const float* quantized, const float* scales, int64_t n_groups, int64_t n_scales, int32_t levels,
+                       int8_t* codes, uint32_t* has_half, void* stream);
+int nq_e8_stream_values(const int8_t* codes, const uint16_t* scales_f16, int64_t n_groups, int64_t n_scales,
+                        float* out, void* stream);
+
 /* Library version and the last error message of the calling thread. */
 int nq_abi_version(void);
 const char* nq_last_error(void);

@@ -125,6 +125,8 @@ SIGNATURES = {
     "nq_e8_dequant_matmul": ([_P, _P, _P, _P, _I64, _I32, _I32, _I32, _P], ctypes.c_int),
     "nq_e8_nearest_point": ([_P, _P, _I64, _P], ctypes.c_int),
     "nq_e8_quantize_perhead": ([_P, _P, _I64, _I32, _I32, _P], ctypes.c_int),
+    "nq_e8_stream_codes": ([_P, _P, _I64, _I64, _I32, _P, _P, _P], ctypes.c_int),
+    "nq_e8_stream_values": ([_P, _P, _I64, _I64, _P, _P], ctypes.c_int),
 }
 
 _lock = threading.Lock()

@@ -16,12 +16,21 @@ NQR1 container (little endian):
     then an optional fp32 scale section: u64 n_scales, f32 scales[n_scales].
 The reference's encode_e8 writes one stream with fp16 scales; NQR1 keeps the
 fp32 scales (lossless) and the chunk offsets that make decoding parallel.
+
+The reference's own container is written and read by encode_e8 / decode_e8
+below (entropy_coder.py:360-431): header '<IBBI' (n_groups, levels, has_half,
+n_symbols), lengths '<III', u16 alphabet + u16 freq[alphabet], fp16 scales,
+then the u16 words of ONE rANS stream over all symbols.  That stream is a
+single dependency chain, coded here by one GPU lane (the chunked coder with one
+chunk spanning the stream), so it runs at the chain's latency (about 80 ns a
+symbol); NQR1 is the parallel format.
 """
 
 from __future__ import annotations
 
 import ctypes
 import dataclasses
+import math
 import struct
 from typing import Optional
 
@@ -109,8 +118,23 @@ def _stream(dev) -> ctypes.c_void_p:
     return ctypes.c_void_p(_lib.current_stream_handle(dev))
 
 
-def rans_encode(codes: torch.Tensor, levels: int, chunk: int = DEFAULT_CHUNK) -> RansStream:
-    """rANS-code int8 codes c = 2p (|c| <= levels) on the device."""
+def _code_counts(flat: torch.Tensor, levels: int) -> np.ndarray:
+    """Histogram of c + levels over the 2 * levels + 1 codes (device pass)."""
+    lib = _lib.load()
+    dev = flat.device
+    hist = torch.zeros(2 * levels + 1, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.nq_rans_histogram(_addr(flat), flat.numel(), levels, _addr(hist), _stream(dev)),
+                   "nq_rans_histogram")
+    return hist.cpu().numpy().astype(np.int64)
+
+
+def rans_encode(codes: torch.Tensor, levels: int, chunk: int = DEFAULT_CHUNK,
+                has_half: Optional[bool] = None) -> RansStream:
+    """rANS-code int8 codes c = 2p (|c| <= levels) on the device.
+
+    has_half (default: some code is odd) selects the alphabet: c + levels over
+    2 * levels + 1 symbols, else c / 2 + levels / 2 over levels + 1."""
     lib = _lib.load()
     _lib.require_device(codes, "codes")
     if codes.dtype != torch.int8:
@@ -122,12 +146,12 @@ def rans_encode(codes: torch.Tensor, levels: int, chunk: int = DEFAULT_CHUNK) ->
     if flat.data_ptr() % 16:
         flat = flat.clone()
     n = flat.numel()
-    hist = torch.zeros(2 * levels + 1, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
-        _lib.check(lib.nq_rans_histogram(_addr(flat), n, levels, _addr(hist), _stream(dev)), "nq_rans_histogram")
-    h = hist.cpu().numpy().astype(np.int64)
-    has_half = bool(h[1::2].sum() > 0) if levels > 0 else False
-    # odd bins hold the half-integer codes (c + L odd <=> c odd for even L)
+    h = _code_counts(flat, levels)
+    if has_half is None:
+        # odd bins hold the half-integer codes (c + L odd <=> c odd for even L)
+        has_half = bool(h[1::2].sum() > 0)
+    elif not has_half and h[1::2].sum() > 0:
+        raise ValueError("has_half=False but some codes are odd (half-integer points)")
     counts = h if has_half else h[0::2]
     freq = build_freq_table(counts)
     alphabet = len(freq)
@@ -288,3 +312,186 @@ def shannon_bits(counts: np.ndarray) -> float:
         return 0.0
     p = c / c.sum()
     return float(-(c * np.log2(p)).sum())
+
+
+# ---------------------------------------------------------------------------
+# The reference's single-stream container: encode_e8 / decode_e8
+# ---------------------------------------------------------------------------
+
+E8_HEADER = struct.Struct("<IBBI")    # n_groups, levels, has_half, n_symbols (entropy_coder.py:406-408)
+E8_LENGTHS = struct.Struct("<III")    # freq, scale and rANS section lengths in bytes (:421-424)
+
+
+def _e8_codes(quantized: torch.Tensor, scale_factors: torch.Tensor, levels: int):
+    """(codes int8 [n], has_half, device fp32 scales) of encode_e8's symbol step."""
+    lib = _lib.load()
+    _lib.require_device(quantized, "quantized")
+    if levels not in (2, 4, 8, 16):
+        raise ValueError(f"levels must be 2, 4, 8 or 16, got {levels}")
+    if quantized.numel() % 8:
+        raise RuntimeError(f"shape '[-1, 8]' is invalid for input of size {quantized.numel()}")
+    dev = quantized.device
+    flat = quantized.reshape(-1, 8).float().contiguous()
+    if flat.data_ptr() % 16:
+        flat = flat.clone()
+    scales = scale_factors.reshape(-1).float().to(dev).contiguous()
+    n_groups, n_scales = flat.shape[0], scales.numel()
+    if n_scales not in (1, n_groups):
+        raise ValueError(f"operands could not be broadcast together: {n_groups} groups of 8 and {n_scales} "
+                         "scale factors")
+    codes = torch.empty(n_groups * 8, dtype=torch.int8, device=dev)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.nq_e8_stream_codes(_addr(flat), _addr(scales), n_groups, n_scales, levels, _addr(codes),
+                                          _addr(flag), _stream(dev)), "nq_e8_stream_codes")
+    return codes, bool(flag.item()), scales
+
+
+def encode_e8(quantized: torch.Tensor, scale_factors: torch.Tensor, levels: int = 8) -> bytes:
+    """The reference's rANS container of an E8-quantized tensor (entropy_coder.py:360-426).
+
+    quantized: scaled lattice points on a ROCm device (any shape, groups of 8);
+    scale_factors: one per group of 8, or one in all.  The bytes equal the
+    reference's for the same inputs."""
+    codes, has_half, scales = _e8_codes(quantized, scale_factors, levels)
+    n = codes.numel()
+    if n:
+        st = rans_encode(codes, levels, chunk=n, has_half=has_half)
+        freq, words = st.freq, st.words.cpu().numpy().view("<u2")
+    else:
+        # no symbols: the table of an empty histogram, and the initial state
+        # 2^16 flushed as two words
+        freq = build_freq_table(np.zeros(levels + 1, np.int64))
+        words = np.array([1, 0], dtype="<u2")
+    freq_bytes = struct.pack("<H", len(freq)) + freq.astype("<u2").tobytes()
+    scale_f16 = scales.clamp_min(1e-8).half().cpu().numpy().astype("<f2").tobytes()
+    rans = words.astype("<u2").tobytes()
+    return (E8_HEADER.pack(n // 8, levels, int(has_half), n) + E8_LENGTHS.pack(len(freq_bytes), len(scale_f16),
+                                                                               len(rans))
+            + freq_bytes + scale_f16 + rans)
+
+
+def decode_e8(compressed: bytes, original_shape: Optional[tuple] = None, device=None):
+    """(quantized fp32, scales fp32) of an encode_e8 container (entropy_coder.py:429-475).
+
+    Decoding runs on the GPU (the current device unless `device` is given);
+    the results come back on the host, as the reference returns them, unless
+    `device` is given."""
+    lib = _lib.load()
+    n_groups, levels, has_half, n_symbols = E8_HEADER.unpack_from(compressed, 0)
+    at = E8_HEADER.size
+    freq_len, scale_len, rans_len = E8_LENGTHS.unpack_from(compressed, at)
+    at += E8_LENGTHS.size
+    if at + freq_len + scale_len + rans_len > len(compressed):
+        raise ValueError(f"truncated E8 stream: sections of {freq_len}, {scale_len} and {rans_len} bytes "
+                         f"after a {at}-byte header, {len(compressed)} bytes in all")
+    if freq_len < 2:
+        raise ValueError("E8 stream without a frequency table")
+    (alphabet,) = struct.unpack_from("<H", compressed, at)
+    if 2 + 2 * alphabet > freq_len:
+        raise ValueError(f"frequency table of {alphabet} entries does not fit its {freq_len} bytes")
+    freq = np.frombuffer(compressed, dtype="<u2", count=alphabet, offset=at + 2).astype(np.uint16)
+    at += freq_len
+    scales_f16 = np.frombuffer(compressed, dtype="<f2", count=scale_len // 2, offset=at).copy()
+    at += scale_len
+    words = np.frombuffer(compressed, dtype="<u2", count=rans_len // 2, offset=at).copy()
+    if n_symbols != 8 * n_groups:
+        raise ValueError(f"cannot reshape {n_symbols} symbols into {n_groups} groups of 8")
+    n_scales = scales_f16.size
+    if n_scales not in (1, n_groups) and n_groups:
+        raise ValueError(f"operands could not be broadcast together: {n_groups} groups of 8 and {n_scales} scales")
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    out = torch.empty(n_groups, 8, dtype=torch.float32, device=dev)
+    if n_symbols:
+        stream = RansStream(words=torch.from_numpy(words.view(np.int16)).to(dev),
+                            offsets=torch.tensor([0, words.size], dtype=torch.int64, device=dev),
+                            freq=freq, levels=levels, has_half=bool(has_half), n=n_symbols, chunk=n_symbols,
+                            shape=(n_symbols,))
+        codes = rans_decode(stream)
+        sc = torch.from_numpy(scales_f16.view(np.int16)).to(dev)
+        with torch.cuda.device(dev):
+            _lib.check(lib.nq_e8_stream_values(_addr(codes), _addr(sc), n_groups, n_scales, _addr(out),
+                                               _stream(dev)), "nq_e8_stream_values")
+    scales = torch.from_numpy(scales_f16.astype(np.float32))
+    if original_shape is not None:
+        out = out.reshape(original_shape)
+    if device is None:
+        return out.cpu(), scales
+    return out, scales.to(dev)
+
+
+def measure_entropy(indices, alphabet_size: Optional[int] = None) -> dict:
+    """Shannon entropy statistics of a symbol stream (entropy_coder.py:94-133)."""
+    if torch.is_tensor(indices):
+        counts = torch.bincount(indices.reshape(-1).long()).cpu().numpy()
+        unique = np.nonzero(counts)[0]
+        counts = counts[unique]
+    else:
+        unique, counts = np.unique(np.asarray(indices), return_counts=True)
+    return _entropy_from_counts(unique, counts, alphabet_size)
+
+
+def _entropy_from_counts(unique: np.ndarray, counts: np.ndarray, alphabet_size: Optional[int]) -> dict:
+    n = int(np.sum(counts))
+    if n == 0:
+        return {"entropy_bps": 0, "uniform_bps": 0, "compression_ratio": 1.0, "n_symbols": 0, "n_unique": 0}
+    probs = counts / n
+    entropy = -np.sum(probs * np.log2(probs + 1e-30))
+    if alphabet_size is None:
+        alphabet_size = int(unique.max()) + 1
+    uniform_bps = math.log2(max(alphabet_size, 2))
+    return {"entropy_bps": float(entropy), "uniform_bps": float(uniform_bps),
+            "compression_ratio": float(uniform_bps / max(entropy, 0.01)), "n_symbols": int(n),
+            "n_unique": int(len(unique))}
+
+
+def _symbol_stats(codes: torch.Tensor, levels: int, has_half: bool) -> dict:
+    h = _code_counts(codes, levels)
+    counts = h if has_half else h[0::2]
+    unique = np.nonzero(counts)[0]
+    return _entropy_from_counts(unique, counts[unique], len(counts))
+
+
+def measure_e8_entropy(quantized: torch.Tensor, scale_factors: torch.Tensor, levels: int = 8) -> dict:
+    """Entropy statistics of the symbols encode_e8 would code (entropy_coder.py:136-157)."""
+    codes, has_half, _ = _e8_codes(quantized, scale_factors, levels)
+    return _symbol_stats(codes, levels, has_half)
+
+
+def e8_quantize_with_entropy(x: torch.Tensor, levels: int = 8, return_stats: bool = True) -> dict:
+    """Per-8-group E8 quantization, encode_e8 and decode_e8 with the size
+    accounting of entropy_coder.py:478-570.  Tensors stay on x's device."""
+    from .kernels import e8_quantize_perhead
+    _lib.require_device(x, "x")
+    shape = x.shape
+    pad = (8 - shape[-1] % 8) % 8
+    x_padded = torch.nn.functional.pad(x, (0, pad)) if pad else x
+    flat = x_padded.reshape(-1, 8).float()
+    # per-group scale: the per-row rule on rows of 8 (amax clamped to 1e-8, / (levels / 2))
+    sc = flat.abs().amax(dim=-1, keepdim=True).clamp(min=1e-8) / (levels / 2)
+    quantized_scaled = e8_quantize_perhead(flat, levels)
+    compressed = encode_e8(quantized_scaled, sc, levels=levels)
+    decoded, _ = decode_e8(compressed, original_shape=flat.shape, device=x.device)
+    reconstructed = decoded.reshape(x_padded.shape)
+    if pad:
+        reconstructed = reconstructed[..., :shape[-1]]
+    reconstructed = reconstructed.reshape(shape)
+    n_coords, n_groups = flat.numel(), flat.shape[0]
+    n_bytes_uniform = math.ceil(n_coords * math.ceil(math.log2(levels + 1)) / 8) + n_groups * 2
+    n_bytes_compressed = len(compressed)
+    original_bytes = n_coords * 2
+    result = {
+        "compressed_bytes": compressed,
+        "reconstructed": reconstructed,
+        "scale_factors": sc,
+        "n_bytes_compressed": n_bytes_compressed,
+        "n_bytes_uniform": n_bytes_uniform,
+        "n_bytes_original": original_bytes,
+        "rans_compression_ratio": n_bytes_uniform / max(n_bytes_compressed, 1),
+        "e8_base_ratio": original_bytes / n_bytes_uniform,
+        "total_compression_ratio": original_bytes / n_bytes_compressed,
+    }
+    if return_stats:
+        codes, has_half, _ = _e8_codes(quantized_scaled, sc, levels)
+        result["entropy_stats"] = _symbol_stats(codes, levels, has_half)
+    return result

@@ -9,7 +9,7 @@ eager attention.  Nothing under /root/reference is copied; only the numbers it
 produces are stored, as small .npz files next to this script.
 
 Usage:  python tests/golden/make_golden.py [/root/reference [evict_soft | vllm_pages | evict_merge | rans |
-                                                              temporal_codec]]
+                                                              temporal_codec | e8stream]]
 """
 
 from __future__ import annotations
@@ -29,7 +29,7 @@ from nexusquant.pipeline import (NexusQuantEvict, NexusQuantEvictTruncate,  # no
 from nexusquant.core.e8_lattice import E8Lattice  # noqa: E402
 from nexusquant.core.rope_utils import inverse_rope, forward_rope  # noqa: E402
 
-from make_golden_cases import temporal_cases  # noqa: E402
+from make_golden_cases import e8_entropy_input, e8stream_cases, temporal_cases  # noqa: E402
 
 
 class ListCache:
@@ -336,6 +336,27 @@ def make_temporal():
     save("temporal_codec", **out)
 
 
+def make_e8stream():
+    """encode_e8 / decode_e8 containers and e8_quantize_with_entropy (entropy_coder.py:360-570)."""
+    from nexusquant.core import entropy_coder as ec
+    out = {}
+    for name, q, s, levels in e8stream_cases():
+        blob = ec.encode_e8(torch.from_numpy(q), torch.from_numpy(s), levels=levels)
+        dq, ds = ec.decode_e8(blob)
+        out.update({f"{name}_quantized": q, f"{name}_scales": s, f"{name}_levels": levels,
+                    f"{name}_blob": np.frombuffer(blob, np.uint8), f"{name}_decoded": dq, f"{name}_dscales": ds})
+    x = torch.from_numpy(e8_entropy_input())
+    r = ec.e8_quantize_with_entropy(x, levels=8)
+    keys = ["n_bytes_compressed", "n_bytes_uniform", "n_bytes_original", "rans_compression_ratio",
+            "e8_base_ratio", "total_compression_ratio"]
+    stats = sorted(r["entropy_stats"])
+    out.update({"e2e_blob": np.frombuffer(r["compressed_bytes"], np.uint8), "e2e_reconstructed": r["reconstructed"],
+                "e2e_scale_factors": r["scale_factors"], "e2e_keys": np.array(keys),
+                "e2e_values": np.array([float(r[k]) for k in keys]), "e2e_stat_keys": np.array(stats),
+                "e2e_stat_values": np.array([float(r["entropy_stats"][k]) for k in stats])})
+    save("e8stream", **out)
+
+
 if __name__ == "__main__":
     if sys.argv[2:] == ["evict_soft"]:
         make_soft()
@@ -347,6 +368,8 @@ if __name__ == "__main__":
         make_rans()
     elif sys.argv[2:] == ["temporal_codec"]:
         make_temporal()
+    elif sys.argv[2:] == ["e8stream"]:
+        make_e8stream()
     else:
         main()
         make_soft()
@@ -354,3 +377,4 @@ if __name__ == "__main__":
         make_merge()
         make_rans()
         make_temporal()
+        make_e8stream()
