@@ -104,10 +104,19 @@ class RansStream:
     n: int
     chunk: int
     shape: tuple
+    # layout key of the state last checked against the decoder's bounds (set by
+    # rans_encode, unpack_nqr1 and rans_decode); any reassignment or in-place
+    # change of words, offsets or freq makes it stale
+    _checked: Optional[tuple] = dataclasses.field(default=None, repr=False, compare=False)
 
     @property
     def alphabet(self) -> int:
         return len(self.freq)
+
+    def _layout_key(self) -> tuple:
+        return (id(self.words), self.words._version, id(self.offsets), self.offsets._version, self.levels,
+                bool(self.has_half), self.n, self.chunk, self.freq.tobytes(), self.words.numel(),
+                self.offsets.numel())
 
     def nbytes(self) -> int:
         """Coded size: words, chunk offsets and the frequency table."""
@@ -168,8 +177,10 @@ def rans_encode(codes: torch.Tensor, levels: int, chunk: int = DEFAULT_CHUNK,
         words = torch.empty(max(total, 1), dtype=torch.int16, device=dev)
         _lib.check(lib.nq_rans_compact(_addr(scratch), _addr(n_words), _addr(offsets), n, chunk, _addr(words),
                                        _stream(dev)), "nq_rans_compact")
-    return RansStream(words=words[:total], offsets=offsets, freq=freq, levels=levels, has_half=has_half, n=n,
-                      chunk=chunk, shape=tuple(codes.shape))
+    st = RansStream(words=words[:total], offsets=offsets, freq=freq, levels=levels, has_half=has_half, n=n,
+                    chunk=chunk, shape=tuple(codes.shape))
+    st._checked = st._layout_key()  # offsets written by nq_rans_encode's scan: consistent by construction
+    return st
 
 
 def check_stream_header(levels: int, has_half: bool, alphabet: int, n: int, chunk: int, n_chunks: int) -> None:
@@ -219,9 +230,12 @@ def check_stream_layout(levels: int, has_half: bool, alphabet: int, n: int, chun
 def rans_decode(stream: RansStream, device=None) -> torch.Tensor:
     """int8 codes of a RansStream, in its original shape."""
     lib = _lib.load()
-    check_stream_layout(stream.levels, stream.has_half, stream.alphabet, stream.n, stream.chunk,
-                        stream.offsets.numel() - 1, stream.freq, stream.offsets.cpu().numpy(),
-                        stream.words.numel())
+    key = stream._layout_key()
+    if stream._checked != key:
+        check_stream_layout(stream.levels, stream.has_half, stream.alphabet, stream.n, stream.chunk,
+                            stream.offsets.numel() - 1, stream.freq, stream.offsets.cpu().numpy(),
+                            stream.words.numel())
+        stream._checked = key
     if int(np.prod(stream.shape)) != stream.n:
         raise ValueError(f"stream shape {stream.shape} does not hold {stream.n} symbols")
     dev = stream.words.device if device is None else torch.device(device)
@@ -301,6 +315,7 @@ def unpack_nqr1(blob: bytes, shape=None, device="cuda"):
     stream = RansStream(words=torch.from_numpy(words.copy()).to(dev), offsets=torch.from_numpy(offsets.copy()).to(dev),
                         freq=freq, levels=levels, has_half=bool(has_half), n=n, chunk=chunk,
                         shape=tuple(shape) if shape is not None else (n,))
+    stream._checked = stream._layout_key()  # checked above against the blob
     return stream, scales
 
 

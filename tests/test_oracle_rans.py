@@ -126,3 +126,25 @@ def test_nqr1_rejects_chunk_with_too_many_words():
     s.words = torch.zeros(19, dtype=torch.int16)
     t, _ = unpack_nqr1(pack_nqr1(s), device="cpu")
     assert t.n == 15 and t.offsets.tolist() == [0, 10, 19]
+
+
+@pytest.mark.parametrize("change", ["offsets_in_place", "offsets_reassigned", "freq_in_place", "n"])
+def test_decode_rechecks_a_stream_changed_after_its_check(change):
+    # a checked stream skips the host check only while its tensors, their
+    # in-place versions and the frequency table are unchanged; any change is
+    # checked again (and raises here before any device work)
+    from nexusquant_amd.entropy import rans_decode, unpack_nqr1
+    _, blob = _good_blob()
+    st, _ = unpack_nqr1(blob, device="cpu")
+    assert st._checked == st._layout_key()
+    if change == "offsets_in_place":
+        st.offsets[1] += 450
+    elif change == "offsets_reassigned":
+        st.offsets = torch.tensor([0, 950, 900], dtype=torch.int64)
+    elif change == "freq_in_place":
+        st.freq[0] = 999
+    else:
+        st.n = 20000
+    assert st._checked != st._layout_key()
+    with pytest.raises(ValueError):
+        rans_decode(st)
