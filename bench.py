@@ -188,10 +188,22 @@ def aux_workload(name, steps, warmup, emit=True):
         step_ms = _timed(torch, lambda: comp.compress(Cache(ks, vs)), steps, warmup) * 1e3
         flops = layers * 2 * (2 * hq * d * s * (s + 1) / 2)
         tflops = flops / (score_ms * 1e-3) / 1e12
+        # the scoring forward's attention itself: layer output + column sums in
+        # one call (nq_attention_real), four causal passes per layer
+        from nexusquant_amd.scoring import attention_real
+
+        def attend():
+            imp2 = torch.zeros(1, s, device=dev)
+            for q, k, v in zip(qs, ks, vs):
+                attention_real(q, k, v, d ** -0.5, imp2)
+        attn_ms = _timed(torch, attend, steps, warmup) * 1e3
+        attn_tflops = 2 * flops / (attn_ms * 1e-3) / 1e12
         out.update(config={"workload": "real-attention scorer: Q fp16 [1, 32, 8192, 128], GQA 4 vs K,V "
                            "[1, 8, 8192, 128], causal, 32 layers; 35% eviction, boundary 2, K3V2"},
                    ms_per_step=round(score_ms + step_ms, 3), value=round(score_ms + step_ms, 3),
                    real_score_ms=round(score_ms, 3), evict_quant_ms=round(step_ms, 3),
+                   attention_with_scores_ms=round(attn_ms, 3),
+                   attention_with_scores_tflops=round(attn_tflops, 1),
                    roofline={"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                              "algorithmic_flops": flops,
@@ -561,7 +573,7 @@ def aux_summary(steps=2, warmup=1):
         r = aux_workload(name, steps, warmup, emit=False)
         out[f"{name}_ms_per_step"] = r["ms_per_step"]
         for k in ("keykey_score_ms", "keykey_device_ms", "keykey_score_gbs", "real_score_ms", "evict_quant_ms",
-                  "gbs_fp16_compressed"):
+                  "attention_with_scores_ms", "gbs_fp16_compressed"):
             if k in r:
                 out[f"{name}_{k}"] = r[k]
         if name == "c4":

@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define NQ_ABI_VERSION 6
+#define NQ_ABI_VERSION 7
 
 /* status codes */
 #define NQ_OK 0
@@ -156,6 +156,25 @@ int64_t nq_score_real_workspace(int32_t batch, int32_t q_heads, int32_t seq);
 int nq_score_real(const void* q, const void* k, int32_t dtype, int32_t batch, int32_t q_heads,
                   int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, float* importance,
                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * The scoring pass's attention output without materialising P: the row
+ * statistics and (importance != NULL) the column sums of nq_score_real, then
+ * out = round_T(P V) [batch, q_heads, seq, head_dim] with P = round_T(softmax_fp32
+ * (round_T(round_T(Q K^T) * scaling))), causal, query head h reading kv head
+ * h / (q_heads / kv_heads) -- eager_attention_forward's arithmetic, P V summed
+ * in fp32 on the matrix cores.  fp16 / bf16, head_dim 64 or 128, 16-byte aligned
+ * tensors; v [batch, kv_heads, seq, head_dim].  workspace:
+ * nq_attention_real_workspace bytes (row statistics, column sums and V
+ * transposed with the keys of each 32-key block in the accumulator's order).
+ *
+ * Replaces: eager_attention_forward (transformers modeling_llama.py:179-213) in
+ *           the scoring forward of _score_importance_real  pipeline.py:784-836
+ */
+int64_t nq_attention_real_workspace(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t seq, int32_t head_dim);
+int nq_attention_real(const void* q, const void* k, const void* v, int32_t dtype, int32_t batch, int32_t q_heads,
+                      int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, float* importance, void* out,
+                      void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Keep mask from importance[batch, seq] (fp32): position 0, the last

@@ -14,7 +14,7 @@ from .build import LIB_PATH, source_hash
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
 NQ_KEEP_ZERO, NQ_KEEP_WRITE_KEPT, NQ_KEEP_WRITE_EVICTED = 0, 1, 2
-ABI_VERSION = 6  # NQ_ABI_VERSION of the header these bindings mirror
+ABI_VERSION = 7  # NQ_ABI_VERSION of the header these bindings mirror
 _P = ctypes.c_void_p
 
 
@@ -107,6 +107,8 @@ SIGNATURES = {
     "nq_delta_decode": ([_P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "nq_score_real_workspace": ([_I32, _I32, _I32], _I64),
     "nq_score_real": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
+    "nq_attention_real_workspace": ([_I32, _I32, _I32, _I32, _I32], _I64),
+    "nq_attention_real": ([_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _P, _I64, _P], ctypes.c_int),
     "nq_rans_histogram": ([_P, _I64, _I32, _P, _P], ctypes.c_int),
     "nq_rans_scratch_words": ([_I64, _I32], _I64),
     "nq_rans_encode": ([_P, _I64, _I32, _I32, _P, _I32, _I32, _P, _P, _P, _P], ctypes.c_int),

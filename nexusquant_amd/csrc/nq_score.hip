@@ -655,6 +655,231 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Attention output of the scoring pass, O = round_T(P V) with P the same
+// rounded probabilities the column sums use (eager_attention_forward:
+// matmul(softmax_fp32(w).to(T), repeat_kv(V))), without materialising P.
+//
+// The matrix cores contract over keys, so V is first written transposed, Vt
+// [batch * hkv, D, s64] (s64 = seq rounded up to 64, zero past seq), with the
+// keys of every 32-key block in "slot order": position 16 kk + 8 g + e holds
+// key 16 kk + (e < 4 ? 4 g + e : 8 + 4 g + e - 4).  That is the order in which
+// a logit accumulator lane (query c, half g) holds its keys (acc_row), so the
+// lane's rounded probabilities are directly the A operand of the P V product
+// (rows = queries, K = keys) and its B operand (K = keys, columns = D) is one
+// 16-byte read of a Vt row.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int slot_key(int p) {  // key (within its 32-key block) at slot position p
+    const int kk = p >> 4, g = (p >> 3) & 1, e = p & 7;
+    return 16 * kk + (e < 4 ? 4 * g + e : 8 + 4 * g + e - 4);
+}
+
+// Vt rows of one 64-key stage of one (batch, kv head): V tile in LDS, then
+// each thread packs 8 slot-ordered keys of one d into a 16-byte store.
+template <int D>
+__global__ __launch_bounds__(256) void vt_slots_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt,
+                                                       int seq, int s64) {
+    __shared__ uint16_t tile[64][D + 2];
+    const int st = blockIdx.x, bh = blockIdx.y;
+    const uint16_t* src = v + (size_t)bh * seq * D;
+    for (int u = threadIdx.x; u < 64 * D / 8; u += 256) {
+        const int r = u / (D / 8), c8 = (u % (D / 8)) * 8;
+        const int key = 64 * st + r;
+        uint4 x = make_uint4(0u, 0u, 0u, 0u);
+        if (key < seq) x = *reinterpret_cast<const uint4*>(src + (size_t)key * D + c8);
+        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            tile[r][c8 + 2 * i] = (uint16_t)w[i];
+            tile[r][c8 + 2 * i + 1] = (uint16_t)(w[i] >> 16);
+        }
+    }
+    __syncthreads();
+    uint16_t* dst = vt + (size_t)bh * D * s64 + 64 * st;
+    for (int u = threadIdx.x; u < D * 8; u += 256) {
+        const int d = u >> 3, p0 = (u & 7) * 8;  // slots p0 .. p0 + 7 of the stage
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int a = p0 + 2 * i, b = a + 1;
+            const uint32_t lo = tile[32 * (a >> 5) + slot_key(a & 31)][d];
+            const uint32_t hi = tile[32 * (b >> 5) + slot_key(b & 31)][d];
+            w[i] = lo | (hi << 16);
+        }
+        *reinterpret_cast<uint4*>(dst + (size_t)d * s64 + p0) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// Direct-to-LDS plan for a 64-key stage of Vt: D rows of 128 bytes, padded to
+// 144 in LDS (9 units, the last masked), windows of 64 units as in DmaPlan.
+template <int D>
+struct VtPlan {
+    static constexpr int UPR = 9;
+    static constexpr int ROWB = 144;
+    static constexpr int WINDOWS = (D * UPR + 63) / 64;
+    static constexpr int NW = (WINDOWS + 3) / 4;
+    static constexpr int BUF = D * ROWB;
+    uint32_t off[NW];
+    bool ok[NW];
+    __device__ __forceinline__ VtPlan(int s64) {
+        const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            const int w = 4 * k + wave;
+            const int slot = 64 * w + lane;
+            const int r = slot / UPR, u = slot - r * UPR;
+            ok[k] = w < WINDOWS && r < D && u < 8;
+            off[k] = ok[k] ? (uint32_t)(r * s64 * 2 + 16 * u) : 0u;
+        }
+    }
+};
+
+template <int D>
+__device__ __forceinline__ void vt_dma(const VtPlan<D>& plan, const uint16_t* vt_bh, int it, char* buf) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const char* stage = reinterpret_cast<const char*>(vt_bh + 64 * it);  // wave-uniform
+#pragma unroll
+    for (int k = 0; k < VtPlan<D>::NW; ++k) {
+        const int w = 4 * k + wave;
+        if (w < VtPlan<D>::WINDOWS && plan.ok[k])
+            __builtin_amdgcn_global_load_lds((global_void_t*)(stage + plan.off[k]), (lds_void_t*)(buf + 1024 * w), 16,
+                                             0, 0);
+    }
+}
+
+struct OutArgs {
+    RealArgs r;
+    const uint16_t* vt;  // [batch * hkv, D, s64]
+    void* out;           // [batch, hq, seq, D] in the model dtype
+    int32_t s64;
+};
+
+// Rounded probabilities of one 32 x 32 logit tile for this lane's query (nm,
+// rz its row statistics), packed for the two 16-deep K steps of P V.
+// MASKED: keys acc_row(j, g) > diag (the lane's query within the tile) are 0.
+template <int DT, bool MASKED>
+__device__ __forceinline__ void out_probs(const f32x16& acc, float nm, float rz, float scaling, int diag, int g,
+                                          uint4 (&pa)[2]) {
+    uint32_t pk[8];
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+        float x0, x1;
+        exp_args2<DT>(acc[j], acc[j + 1], scaling, nm, nm, x0, x1);
+        float p0 = __builtin_amdgcn_exp2f(x0) * rz;
+        float p1 = __builtin_amdgcn_exp2f(x1) * rz;
+        if constexpr (MASKED) {
+            p0 = acc_row(j, 32 * g) <= diag ? p0 : 0.0f;
+            p1 = acc_row(j + 1, 32 * g) <= diag ? p1 : 0.0f;
+        }
+        pk[j / 2] = round_pair<DT>(p0, p1);
+    }
+    pa[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    pa[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+}
+
+// One 32-key tile of P V: for each 32-wide column block, two MFMAs (K = the
+// tile's two slot-ordered key halves).  vbuf: the stage's Vt rows in LDS,
+// tile t of the stage at byte 64 t of a row.
+template <int DT, int D>
+__device__ __forceinline__ void out_pv(const uint4 (&pa)[2], const char* vbuf, int t, int c, int g,
+                                       f32x16 (&oacc)[D / 32]) {
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+        const char* row = vbuf + (32 * db + c) * VtPlan<D>::ROWB + 64 * t + 16 * g;
+        oacc[db] = mfma16<DT>(pa[0], *reinterpret_cast<const uint4*>(row), oacc[db]);
+        oacc[db] = mfma16<DT>(pa[1], *reinterpret_cast<const uint4*>(row + 32), oacc[db]);
+    }
+}
+
+// A workgroup owns 128 query rows of one query head (wave w: rows 32 w ..),
+// queries resident as the QK^T B operand as in real_rowstats, and streams
+// 64-key stages of K (logits) and Vt (values) through two LDS buffers each.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void real_output(OutArgs o) {
+    __shared__ __align__(16) char k0buf[RealTile<D>::BUF];
+    __shared__ __align__(16) char k1buf[RealTile<D>::BUF];
+    __shared__ __align__(16) char v0buf[VtPlan<D>::BUF];
+    __shared__ __align__(16) char v1buf[VtPlan<D>::BUF];
+    const RealArgs& a = o.r;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 5, c = lane & 31;
+    const int item = xcd_item(a);
+    if (item >= a.n_items) return;
+    const int n_blocks = (a.seq + 127) / 128;
+    const int grp = a.hq / a.hkv;
+    const int hh = item % grp;
+    const int rest = item / grp;
+    const int qb = n_blocks - 1 - rest % n_blocks;
+    const int bg = rest / n_blocks;
+    const int b = bg / a.hkv, hk = bg - b * a.hkv;
+    const int hq = hk * grp + hh;
+    const int bhq = b * a.hq + hq;
+    const uint16_t* qbase = static_cast<const uint16_t*>(a.q) + (size_t)bhq * a.seq * D;
+    const uint16_t* kbase = static_cast<const uint16_t*>(a.k) + ((size_t)b * a.hkv + hk) * a.seq * D;
+    const uint16_t* vt_bh = o.vt + ((size_t)b * a.hkv + hk) * D * o.s64;
+    const int q0 = qb * 128 + wave * 32;
+    const bool live = q0 < a.seq;
+    const int my_diag = q0 / 32;
+    const int last_key = min(qb * 128 + 127, a.seq - 1);
+    const int n_it = last_key / 64 + 1;
+    uint4 qa[RealTile<D>::KS];
+    row_operand<D>(qbase, q0 + c, a.seq, g, qa);
+    const size_t stat = (size_t)bhq * a.seq;
+    const int qi = min(q0 + c, a.seq - 1);
+    const float nm = a.row_max[stat + qi], rz = a.row_sum[stat + qi];
+    f32x16 oacc[D / 32];
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) oacc[db] = f32x16{};
+    const DmaPlan<D> kplan;
+    const VtPlan<D> vplan(o.s64);
+    tile_dma<D>(kplan, kbase, 0, a.seq, k0buf);
+    vt_dma<D>(vplan, vt_bh, 0, v0buf);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    auto stage = [&](int it, const char* ck, const char* cv, char* nk, char* nv) {
+        if (it + 1 < n_it) {
+            tile_dma<D>(kplan, kbase, (it + 1) * 64, a.seq, nk);
+            vt_dma<D>(vplan, vt_bh, it + 1, nv);
+        }
+        if (live) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int kt = 2 * it + t;
+                if (kt > my_diag) break;
+                const f32x16 acc = logits_lds_regs<DT, D>(ck + t * 32 * RealTile<D>::ROWB, qa, c, g);
+                uint4 pa[2];
+                if (kt < my_diag) out_probs<DT, false>(acc, nm, rz, a.scaling, 0, g, pa);
+                else out_probs<DT, true>(acc, nm, rz, a.scaling, c, g, pa);
+                out_pv<DT, D>(pa, cv, t, c, g, oacc);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        __syncthreads();
+    };
+#pragma unroll 1
+    for (int it = 0; it < n_it; it += 2) {
+        stage(it, k0buf, v0buf, k1buf, v1buf);
+        if (it + 1 < n_it) stage(it + 1, k1buf, v1buf, k0buf, v0buf);
+    }
+    if (!live) return;
+    // lane (c, g) holds O[q0 + acc_row(j, g)][32 db + c]
+    uint16_t* out = static_cast<uint16_t*>(o.out) + (size_t)bhq * a.seq * D;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int qrow = q0 + acc_row(j, 32 * g);
+            if (qrow < a.seq) {
+                const float y = oacc[db][j];
+                uint16_t h;
+                if constexpr (DT == NQ_F16) h = __builtin_bit_cast(uint16_t, (__fp16)y);
+                else h = (uint16_t)(__builtin_bit_cast(uint32_t, round_bf16(y)) >> 16);
+                out[(size_t)qrow * D + 32 * db + c] = h;
+            }
+        }
+}
+
 __global__ __launch_bounds__(256) void head_mean_accumulate(const float* colsum, float* importance, int hq,
                                                             int seq) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -684,6 +909,31 @@ static hipError_t launch_real(const RealArgs& a, hipStream_t st) {
     }
     hipLaunchKernelGGL(head_mean_accumulate, dim3((a.seq + 255) / 256, a.batch), dim3(256), 0, st, a.colsum,
                        a.importance, a.hq, a.seq);
+    return hipGetLastError();
+}
+
+template <int DT, int D>
+static hipError_t launch_attention(const RealArgs& a, const void* v, void* out, uint16_t* vt, int s64,
+                                   bool with_importance, hipStream_t st) {
+    RealArgs w = a;
+    const int n_blocks = (a.seq + 127) / 128;
+    w.n_items = n_blocks * a.batch * a.hq;
+    w.per_xcd = (w.n_items + 7) / 8;
+    dim3 grid(8 * w.per_xcd);
+    hipLaunchKernelGGL((real_rowstats<DT, D>), grid, dim3(256), 0, st, w);
+    if (with_importance) {
+        hipLaunchKernelGGL((real_colsum<DT, D>), grid, dim3(256), 0, st, w);
+        hipLaunchKernelGGL(head_mean_accumulate, dim3((a.seq + 255) / 256, a.batch), dim3(256), 0, st, a.colsum,
+                           a.importance, a.hq, a.seq);
+    }
+    hipLaunchKernelGGL((vt_slots_kernel<D>), dim3(s64 / 64, a.batch * a.hkv), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(v), vt, a.seq, s64);
+    OutArgs o;
+    o.r = w;
+    o.vt = vt;
+    o.out = out;
+    o.s64 = s64;
+    hipLaunchKernelGGL((real_output<DT, D>), grid, dim3(256), 0, st, o);
     return hipGetLastError();
 }
 
@@ -738,6 +988,62 @@ extern "C" int nq_score_real(const void* q, const void* k, int32_t dtype, int32_
         case NQ_BF16: e = dispatch_real_d<NQ_BF16>(head_dim, a, st); break;
         default: e = dispatch_real_d<NQ_F32>(head_dim, a, st); break;
     }
+    NQ_CHECK_HIP(e);
+    return NQ_OK;
+}
+
+extern "C" int64_t nq_attention_real_workspace(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t seq,
+                                               int32_t head_dim) {
+    if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq <= 0 || head_dim <= 0) return 0;
+    const int64_t stats = (nq_score_real_workspace(batch, q_heads, seq) + 255) / 256 * 256;
+    const int64_t s64 = ((int64_t)seq + 63) / 64 * 64;
+    return stats + (int64_t)batch * kv_heads * head_dim * s64 * 2;
+}
+
+extern "C" int nq_attention_real(const void* q, const void* k, const void* v, int32_t dtype, int32_t batch,
+                                 int32_t q_heads, int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling,
+                                 float* importance, void* out, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
+    using namespace nq;
+    NQ_CHECK_ARG(q && k && v && out && workspace, "nq_attention_real: NULL pointer");
+    NQ_CHECK_ARG(batch > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
+                 "nq_attention_real: q_heads must be a positive multiple of kv_heads");
+    NQ_CHECK_ARG((int64_t)batch * q_heads <= 65535 && seq >= 0, "nq_attention_real: bad shape");
+    NQ_CHECK_ARG(head_dim == 64 || head_dim == 128, "nq_attention_real: head_dim %d unsupported (64, 128)",
+                 head_dim);
+    NQ_CHECK_ARG(dtype == NQ_F16 || dtype == NQ_BF16, "nq_attention_real: dtype must be fp16 or bf16");
+    NQ_CHECK_ARG((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)workspace) & 15) == 0,
+                 "nq_attention_real: tensors must be 16-byte aligned");
+    if (seq == 0) return NQ_OK;
+    NQ_CHECK_ARG((int64_t)seq * head_dim < (1ll << 31), "nq_attention_real: seq too long");
+    const int64_t need = nq_attention_real_workspace(batch, q_heads, kv_heads, seq, head_dim);
+    NQ_CHECK_ARG(workspace_bytes >= need, "nq_attention_real: workspace %lld bytes < %lld",
+                 (long long)workspace_bytes, (long long)need);
+    RealArgs a;
+    a.q = q;
+    a.k = k;
+    const int64_t n = (int64_t)batch * q_heads * seq;
+    a.row_max = static_cast<float*>(workspace);
+    a.row_sum = a.row_max + n;
+    a.colsum = a.row_sum + n;
+    a.importance = importance;
+    a.seq = seq;
+    a.hq = q_heads;
+    a.hkv = kv_heads;
+    a.batch = batch;
+    a.scaling = scaling;
+    const int64_t stats = (nq_score_real_workspace(batch, q_heads, seq) + 255) / 256 * 256;
+    uint16_t* vt = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + stats);
+    const int s64 = (seq + 63) / 64 * 64;
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e;
+    const bool imp = importance != nullptr;
+    if (dtype == NQ_F16)
+        e = head_dim == 64 ? launch_attention<NQ_F16, 64>(a, v, out, vt, s64, imp, st)
+                           : launch_attention<NQ_F16, 128>(a, v, out, vt, s64, imp, st);
+    else
+        e = head_dim == 64 ? launch_attention<NQ_BF16, 64>(a, v, out, vt, s64, imp, st)
+                           : launch_attention<NQ_BF16, 128>(a, v, out, vt, s64, imp, st);
     NQ_CHECK_HIP(e);
     return NQ_OK;
 }

@@ -3,10 +3,12 @@
 The reference runs model(input_ids, output_attentions=True) under eager
 attention and column-sums the returned [batch, heads, seq, seq] probabilities
 of every layer.  Here the model runs with an attention wrapper registered in
-transformers' AttentionInterface: each layer's attention is computed by the
-model's own implementation, and its (post-RoPE) queries and keys go to the
-nq_score_real kernel, which accumulates the same column sums without
-materialising the probabilities (causal, GQA, HF eager dtype roundings).
+transformers' AttentionInterface.  For fp16 / bf16 models with head_dim 64 or
+128 each layer's attention goes to nq_attention_real, which computes the
+layer output and accumulates the same column sums from its (post-RoPE)
+queries, keys and values with eager's roundings and without materialising
+the probabilities (causal, GQA).  Other models run their own attention for
+the output, and nq_score_real adds the column sums.
 """
 
 from __future__ import annotations
@@ -49,6 +51,36 @@ def score_real_accumulate(query: torch.Tensor, key: torch.Tensor, importance: to
     _lib.check(st, "nq_score_real")
 
 
+def attention_real(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float,
+                   importance: torch.Tensor = None) -> torch.Tensor:
+    """Causal attention output [b, hq, s, d] with eager_attention_forward's roundings
+    (nq_attention_real), and importance[b, s] += the layer's column sums when given."""
+    lib = _lib.load()
+    _lib.require_device(query, "query")
+    if query.dim() != 4 or key.dim() != 4 or value.shape != key.shape:
+        raise ValueError("expected query [b, hq, s, d] and key / value [b, hkv, s, d]")
+    b, hq, s, d = query.shape
+    hkv = key.shape[1]
+    if key.shape[0] != b or key.shape[2] != s or key.shape[3] != d or hq % hkv:
+        raise ValueError(f"incompatible query {tuple(query.shape)} / key {tuple(key.shape)}")
+    if not (query.dtype == key.dtype == value.dtype) or query.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("query, key and value must share an fp16 or bf16 dtype")
+    if d not in (64, 128):
+        raise ValueError(f"head_dim {d} unsupported (64, 128)")
+    q, k, v = (t.contiguous() for t in (query, key, value))
+    q, k, v = (t if t.data_ptr() % 16 == 0 else t.clone() for t in (q, k, v))
+    dev = q.device
+    out = torch.empty_like(q)
+    ws_bytes = lib.nq_attention_real_workspace(b, hq, hkv, s, d)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = lib.nq_attention_real(_addr(q), _addr(k), _addr(v), _lib.dtype_code(q.dtype), b, hq, hkv, s, d,
+                                   ctypes.c_float(scaling), _addr(importance), _addr(out), _addr(ws), ws_bytes,
+                                   ctypes.c_void_p(_lib.current_stream_handle(dev)))
+    _lib.check(st, "nq_attention_real")
+    return out
+
+
 def _model_eager(module):
     mod = sys.modules.get(type(module).__module__)
     fn = getattr(mod, "eager_attention_forward", None)
@@ -82,11 +114,17 @@ def real_importance(model, input_ids: torch.Tensor) -> torch.Tensor:
             raise NotImplementedError(
                 "the real scorer kernel does not implement attention sinks (s_aux); "
                 "use scorer='key-key' for this model")
-        if prev == "eager" or prev is None:
-            base = _model_eager(module)
-        else:
-            base = ALL_ATTENTION_FUNCTIONS[prev]
         sc = scaling if scaling is not None else query.shape[-1] ** -0.5
+        eager = prev == "eager" or prev is None
+        if (eager and dropout == 0.0 and not module.training and query.dtype in (torch.float16, torch.bfloat16)
+                and query.shape[-1] in (64, 128) and key.shape[2] == query.shape[2]):
+            # this pass runs without a cache or a padding mask, so the mask is the
+            # plain causal one: the layer output comes from the same kernels as
+            # the column sums, with eager's roundings, and P is never stored
+            out = attention_real(query, key, value, float(sc), imp)
+            calls[0] += 1
+            return out.transpose(1, 2).contiguous(), None
+        base = _model_eager(module) if eager else ALL_ATTENTION_FUNCTIONS[prev]
         out, _ = base(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
         score_real_accumulate(query, key, imp, float(sc))
         calls[0] += 1

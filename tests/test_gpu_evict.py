@@ -425,3 +425,44 @@ def test_hook_default_mode_protects_every_layer_with_boundary_2():
         k = cache.layers[li].keys
         assert k.dtype == torch.float16
         assert torch.all(k[0, :, evicted.to(DEV), :] == 0)
+
+
+def _eager_attention(q, k, v, scaling):
+    """transformers' eager_attention_forward on the GPU, in the model dtype
+    (right-hand operands made contiguous before the batched products)."""
+    grp = q.shape[1] // k.shape[1]
+    kr = k.repeat_interleave(grp, dim=1)
+    vr = v.repeat_interleave(grp, dim=1)
+    w = torch.matmul(q, kr.transpose(2, 3).contiguous()) * scaling
+    s = q.shape[2]
+    w = w + torch.full((s, s), torch.finfo(q.dtype).min, device=q.device, dtype=q.dtype).triu(1)
+    p = torch.softmax(w, dim=-1, dtype=torch.float32).to(q.dtype)
+    return torch.matmul(p, vr.contiguous())
+
+
+@pytest.mark.parametrize("dtype,d,s,hq,hkv", [(torch.float16, 128, 300, 8, 2), (torch.float16, 64, 1000, 8, 8),
+                                              (torch.bfloat16, 128, 700, 8, 2), (torch.bfloat16, 64, 129, 4, 1),
+                                              (torch.float16, 128, 64, 4, 4)])
+def test_attention_real_output_matches_eager(dtype, d, s, hq, hkv):
+    # out = round_T(P V) with eager's P; the fp32 sums run in another order than
+    # the GEMM's, so an element may differ by one unit of the model dtype
+    from nexusquant_amd.scoring import attention_real, score_real_accumulate
+    print(f"[gpu] attention_real {dtype} d={d} s={s} hq={hq} hkv={hkv}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(s + d)
+    q = torch.randn(2, hq, s, d, device=DEV, generator=g).to(dtype)
+    k = torch.randn(2, hkv, s, d, device=DEV, generator=g).to(dtype)
+    v = torch.randn(2, hkv, s, d, device=DEV, generator=g).to(dtype)
+    sc = d ** -0.5
+    imp = torch.zeros(2, s, device=DEV)
+    out = attention_real(q, k, v, sc, imp)
+    ref = _eager_attention(q, k, v, sc)
+    diff = (out.float() - ref.float()).abs()
+    ulp = 2.0 ** (-10 if dtype == torch.float16 else -7)
+    assert diff.max().item() <= 2 * ulp * max(1.0, ref.float().abs().max().item()), diff.max().item()
+    assert (diff == 0).float().mean().item() > 0.9
+    # the column sums are nq_score_real's, bit for bit
+    imp2 = torch.zeros(2, s, device=DEV)
+    score_real_accumulate(q, k, imp2, sc)
+    assert torch.equal(imp, imp2)
+    # without importance the output is the same
+    assert torch.equal(attention_real(q, k, v, sc), out)
