@@ -208,6 +208,27 @@ def aux_workload(name, steps, warmup, emit=True):
                              "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                              "algorithmic_flops": flops,
                              "note": "two causal QK^T passes per layer, as the kernels run them"})
+    elif name == "c4hook":
+        # the whole scoring forward (real_importance) of a 2-layer Llama-shaped
+        # model at C4's attention shape, with the model's eager attention and
+        # with nq_attention_real; random weights, synthetic token ids
+        from transformers import LlamaConfig, LlamaForCausalLM
+        import nexusquant_amd.scoring as sc
+        torch.manual_seed(0)
+        cfg = LlamaConfig(vocab_size=32000, hidden_size=4096, intermediate_size=14336, num_hidden_layers=2,
+                          num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=16384,
+                          rope_theta=500000.0)
+        cfg._attn_implementation = "eager"
+        model = LlamaForCausalLM(cfg).to(dev, torch.float16).eval()
+        ids = torch.randint(0, 32000, (1, 8192), device=dev, generator=gen)
+        res = {}
+        for label, fused in (("eager_attention", False), ("nq_attention_real", True)):
+            torch.cuda.reset_peak_memory_stats(dev)
+            ms = _timed(torch, lambda: sc.real_importance(model, ids, fused_attention=fused), steps, warmup) * 1e3
+            res[label] = {"ms": round(ms, 2), "peak_gib": round(torch.cuda.max_memory_allocated(dev) / 2 ** 30, 2)}
+        out.update(config={"workload": "scoring forward (real_importance) of a 2-layer Llama-shaped model: hidden "
+                           "4096, 32 query / 8 kv heads, head_dim 128, fp16, 8192 tokens"},
+                   ms_per_step=res["nq_attention_real"]["ms"], value=res["nq_attention_real"]["ms"], **res)
     elif name in ("c5a", "c5b"):
         if name == "c5a":
             layers, h, d, rate, desc = 32, 32, 96, 0.60, "Phi-3-mini shape, 32 layers x K,V fp16 [1, 32, 16384, 96]"
@@ -596,7 +617,8 @@ def main():
     ap.add_argument("--workload", default="c2",
                     help="c2 (headline, default), a secondary config: c3, c4, c5a, c5b, aux (all four), "
                          "decode70b / decode7b (paged decode attention from compressed pages), rans (GPU "
-                         "entropy stage), temporal (temporal_codec container), merge (merge eviction), e8mm (fused E8 dequant + matrix product), "
+                         "entropy stage), temporal (temporal_codec container), c4hook (the real scorer's whole scoring "
+                         "forward on a 2-layer model), merge (merge eviction), e8mm (fused E8 dequant + matrix product), "
                          "or copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

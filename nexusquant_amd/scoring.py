@@ -89,8 +89,12 @@ def _model_eager(module):
     return fn
 
 
-def real_importance(model, input_ids: torch.Tensor) -> torch.Tensor:
-    """importance [batch, seq] averaged over layers, from one scoring forward pass."""
+def real_importance(model, input_ids: torch.Tensor, fused_attention: bool = True) -> torch.Tensor:
+    """importance [batch, seq] averaged over layers, from one scoring forward pass.
+
+    fused_attention=False keeps the model's own attention for every layer's
+    output (nq_score_real then adds the column sums), as for models the fused
+    kernel does not cover."""
     from transformers import AttentionInterface
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 
@@ -116,7 +120,8 @@ def real_importance(model, input_ids: torch.Tensor) -> torch.Tensor:
                 "use scorer='key-key' for this model")
         sc = scaling if scaling is not None else query.shape[-1] ** -0.5
         eager = prev == "eager" or prev is None
-        if (eager and dropout == 0.0 and not module.training and query.dtype in (torch.float16, torch.bfloat16)
+        if (fused_attention and eager and dropout == 0.0 and not module.training
+                and query.dtype in (torch.float16, torch.bfloat16)
                 and query.shape[-1] in (64, 128) and key.shape[2] == query.shape[2]):
             # this pass runs without a cache or a padding mask, so the mask is the
             # plain causal one: the layer output comes from the same kernels as

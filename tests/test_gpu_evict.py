@@ -466,3 +466,18 @@ def test_attention_real_output_matches_eager(dtype, d, s, hq, hkv):
     assert torch.equal(imp, imp2)
     # without importance the output is the same
     assert torch.equal(attention_real(q, k, v, sc), out)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_scoring_forward_fused_attention_matches_model_attention(dtype):
+    # real_importance with nq_attention_real for the layer outputs against the
+    # model's own eager attention: the outputs differ by at most one unit of
+    # the model dtype per element, so the importance agrees closely
+    from nexusquant_amd.scoring import real_importance
+    print(f"[gpu] scoring forward fused vs model attention {dtype}", flush=True)
+    model = _tiny_llama(dtype=dtype, layers=3)
+    ids = torch.randint(0, 256, (2, 300), generator=torch.Generator().manual_seed(9)).to(DEV)
+    with torch.no_grad():
+        fused = real_importance(model, ids)
+        plain = real_importance(model, ids, fused_attention=False)
+    assert torch.allclose(fused, plain, rtol=2e-3, atol=1e-5), (fused - plain).abs().max()
