@@ -42,7 +42,7 @@ from .ops import _addr
 
 PROB_BITS = 12
 M = 1 << PROB_BITS
-DEFAULT_CHUNK = 4096
+DEFAULT_CHUNK = 2048  # symbols per chunk (one lane's chain); see the measurements in the design notes
 _MAGIC = b"NQR1"
 
 

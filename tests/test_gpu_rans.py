@@ -27,7 +27,7 @@ def test_single_chunk_equals_reference_words(golden, tag):
     assert torch.equal(rans_decode(st).cpu(), codes)
 
 
-@pytest.mark.parametrize("levels,n,chunk", [(8, 1_000_003, 4096), (4, 262_144, 1024), (16, 70_000, 4096),
+@pytest.mark.parametrize("levels,n,chunk", [(8, 1_000_003, 4096), (8, 300_001, 2048), (4, 262_144, 1024), (16, 70_000, 4096),
                                             (2, 4096, 4096), (8, 1, 4096), (4, 50_001, 1000), (8, 40_000, 200)])
 def test_chunked_roundtrip_and_chunk_words(levels, n, chunk):
     from nexusquant_amd.entropy import pack_nqr1, rans_decode, rans_encode, shannon_bits, unpack_nqr1
