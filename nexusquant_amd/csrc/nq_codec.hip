@@ -151,26 +151,108 @@ __global__ __launch_bounds__(256) void dequant_kernel(CodecArgs a) {
     }
 }
 
-// int8 2p of this lane's 32 coordinates, packed 4 per dword in coordinate order.
-template <int D, int L>
-__device__ __forceinline__ void codes2p(const CodecArgs& a, uint32_t tensor, size_t row, int q,
-                                        uint32_t (&out)[D / 32][2]) {
-    float p[D / 32][8];
-    int coset[D / 32];
-    float scale;
-    unpack_points<D, L>(a, tensor, row, q, p, coset, scale);
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)(p[c][j] * 2.0f);
-            if (j < 4) lo |= b << (8 * j);
-            else hi |= b << (8 * (j - 4));
+// ---------------------------------------------------------------------------
+// int8 2p codes straight from the packed symbols, in integer arithmetic.  A
+// symbol s decodes to the lattice coordinate x = s - L/2, moved half a step in
+// the half coset: up and capped at L/2 when L/2 is even, down and floored at
+// -L/2 when it is odd (unpack_points above); the code is the int8 byte of 2x.
+// Four codes per dword: with y = 2s + 128 - L (+1 or -1 in the half coset)
+// every byte lies in [0, 256), so one shift-add forms them without carries and
+// an XOR with 0x80 removes the bias; the bytes whose symbol passes the cap
+// (floor) are then replaced by it.  Exact for every symbol value (s < 32).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ constexpr uint32_t splat8(uint32_t b) { return (b & 0xffu) * 0x01010101u; }
+
+template <int L>
+__device__ __forceinline__ uint32_t two_p_bytes(uint32_t s, bool half) {
+    constexpr bool UP = ((L / 2) & 1) == 0;
+    const uint32_t bias = half ? (UP ? 129u - L : 127u - L) : 128u - L;
+    const uint32_t v = ((s << 1) + splat8(bias)) ^ 0x80808080u;
+    uint32_t g;  // bit 7 of the bytes the cap (floor) replaces: s >= L (s == 0), half coset only
+    if constexpr (UP) g = (s + splat8(half ? 128u - L : 96u)) & 0x80808080u;
+    else g = ~(s + splat8(half ? 127u : 128u)) & 0x80808080u;
+    const uint32_t m = g | (g - (g >> 7));  // 0xff in those bytes
+    constexpr uint32_t bound = splat8(UP ? (uint32_t)L : (uint32_t)-L);
+    return (v & ~m) | (bound & m);
+}
+
+// Four B-bit fields (bits 0, B, 2B, 3B of x) moved to bytes 0..3.
+template <int B>
+__device__ __forceinline__ uint32_t spread4(uint32_t x) {
+    constexpr uint32_t M = (1u << B) - 1u;
+    constexpr uint32_t M2 = (1u << (2 * B)) - 1u;
+    x = (x & M2) | ((x << (16 - 2 * B)) & (M2 << 16));  // fields 2, 3 to bit 16
+    return (x & (M | (M << 16))) | ((x << (8 - B)) & ((M << 8) | (M << 24)));
+}
+
+// 32 bits of a little-endian run of ND dwords from bit `bit` on (zeros past the end).
+template <int bit, int ND>
+__device__ __forceinline__ uint32_t window32(const uint32_t (&d)[ND]) {
+    constexpr int k = bit / 32, sh = bit % 32;
+    if constexpr (sh == 0) return d[k];
+    else if constexpr (k + 1 < ND) return __builtin_amdgcn_alignbit(d[k + 1], d[k], sh);
+    else return d[k] >> sh;
+}
+
+// int8 2p of this lane's C groups of one row into an LDS row (D bytes in
+// coordinate order): group c covers coordinates 32c + 8q .. +7, and its 8
+// B-bit symbols are bits [8Bc, 8Bc + 8B) of the lane's run of C * B symbol
+// bytes, turned into bytes 4 at a time.
+template <int D, int L, int c = 0>
+__device__ __forceinline__ void groups_to_row(const uint32_t (&d)[(D / 32 * SymBits<L>::value + 3) / 4], uint32_t cbits,
+                                              int q, uint8_t* lds_row) {
+    constexpr int C = D / 32;
+    constexpr int B = SymBits<L>::value;
+    if constexpr (c < C) {
+        const bool half = ((cbits >> (4 * c + q)) & 1u) != 0;
+        uint32_t lo, hi;
+        if constexpr (B == 4) {
+            const uint32_t w = d[c];
+            const uint32_t ev = w & 0x0f0f0f0fu, od = (w >> 4) & 0x0f0f0f0fu;  // symbols 0 2 4 6 / 1 3 5 7
+            lo = __builtin_amdgcn_perm(od, ev, 0x05010400u);
+            hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);
+        } else {
+            lo = spread4<B>(window32<8 * B * c>(d));
+            hi = spread4<B>(window32<8 * B * c + 4 * B>(d));
         }
-        out[c][0] = lo;
-        out[c][1] = hi;
+        *reinterpret_cast<uint2*>(lds_row + 32 * c + 8 * q) = make_uint2(two_p_bytes<L>(lo, half), two_p_bytes<L>(hi, half));
+        groups_to_row<D, L, c + 1>(d, cbits, q, lds_row);
     }
+}
+
+// The packed symbols (this lane's run of C * B bytes) and coset bits of one row.
+template <int D, int L>
+struct RowSyms {
+    static constexpr int NB = D / 32 * SymBits<L>::value;
+    uint32_t d[(NB + 3) / 4];
+    uint32_t cbits;
+
+    __device__ __forceinline__ void load(const CodecArgs& a, uint32_t tensor, size_t row, int q) {
+        constexpr int ND = (NB + 3) / 4;
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(a.syms[tensor]) + row * (D / 8 * SymBits<L>::value) + q * NB;
+        if constexpr (NB % 4 == 0) {
+#pragma unroll
+            for (int k = 0; k < ND; ++k) d[k] = reinterpret_cast<const uint32_t*>(src)[k];
+        } else {  // NB = 6 or 10 (head_dim 64): 2-byte aligned
+#pragma unroll
+            for (int k = 0; k < ND; ++k) {
+                const uint32_t lo16 = reinterpret_cast<const uint16_t*>(src)[2 * k];
+                const uint32_t hi16 = 4 * k + 2 < NB ? reinterpret_cast<const uint16_t*>(src)[2 * k + 1] : 0u;
+                d[k] = lo16 | (hi16 << 16);
+            }
+        }
+        const uint8_t* cb = reinterpret_cast<const uint8_t*>(a.cosets[tensor]) + row * (D / 64);
+        if constexpr (D == 64) cbits = *cb;
+        else if constexpr (D == 128) cbits = *reinterpret_cast<const uint16_t*>(cb);
+        else cbits = *reinterpret_cast<const uint32_t*>(cb);
+    }
+};
+
+template <int D, int L>
+__device__ __forceinline__ void codes_to_row(const CodecArgs& a, uint32_t tensor, size_t row, int q, uint8_t* lds_row) {
+    RowSyms<D, L> rs;
+    rs.load(a, tensor, row, q);
+    groups_to_row<D, L>(rs.d, rs.cbits, q, lds_row);
 }
 
 // Byte-wise wrapping subtraction of four int8 lanes.
@@ -178,34 +260,75 @@ __device__ __forceinline__ uint32_t sub_bytes(uint32_t a, uint32_t b) {
     return ((a | 0x80808080u) - (b & 0x7f7f7f7fu)) ^ ((a ^ ~b) & 0x80808080u);
 }
 
+constexpr uint32_t kInt8Tiles = 8;  // 64-token tiles per block of int8_codes_kernel
+
+// One block per kInt8Tiles consecutive 64-token tiles of one (tensor, batch x
+// head) stream.  Per tile, each quad decodes one token row into an LDS tile
+// (row stride D + 16 bytes, so the 8-byte writes of a wave's 16 rows spread
+// over all banks); the block then streams the tile out in 16-byte chunks,
+// contiguous across the tile.  DELTA: LDS row 0 holds the token before the
+// tile and each chunk is stored minus the chunk above it.  Lanes 0-3 decode
+// that token for the block's first tile (zeros at token 0); for the next ones
+// the threads that stored the previous tile's last row write it to row 0 once
+// every thread has read the tile, so each row is decoded once.  The symbol
+// loads of the next tile are issued before the current tile is decoded.
 template <int D, int L, bool DELTA>
 __global__ __launch_bounds__(256) void int8_codes_kernel(CodecArgs a) {
-    constexpr int C = D / 32;
+    constexpr int STRIDE = D + 16;
+    constexpr int CPR = D / 16;  // 16-byte chunks per row
+    __shared__ __align__(16) uint8_t tile[65 * STRIDE];
     const int q = threadIdx.x & 3;
     const uint32_t w = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
-    if (w >= a.work) return;
+    if (w >= a.work) return;  // whole block
     const uint32_t tensor = w % a.n_tensors;
     const uint32_t rest = w / a.n_tensors;
     const uint32_t bh = rest % a.bh;
-    const uint32_t t = (rest / a.bh) * 64u + (threadIdx.x >> 2);
-    if (t >= a.seq) return;  // no cross-lane operations below
-    const size_t row = (size_t)bh * a.seq + t;
-    uint32_t cur[C][2];
-    codes2p<D, L>(a, tensor, row, q, cur);
+    const uint32_t t_begin = (rest / a.bh) * (64u * kInt8Tiles);
+    const uint32_t t_end = min(t_begin + 64u * kInt8Tiles, a.seq);
+    const size_t row0 = (size_t)bh * a.seq;  // the stream's token 0
+    const uint32_t r = threadIdx.x >> 2;
     if constexpr (DELTA) {
-        if (t > 0) {
-            uint32_t prev[C][2];
-            codes2p<D, L>(a, tensor, row - 1, q, prev);
+        if (threadIdx.x < 4) {
+            if (t_begin > 0) {
+                codes_to_row<D, L>(a, tensor, row0 + t_begin - 1, q, tile);
+            } else {
 #pragma unroll
-            for (int c = 0; c < C; ++c) {
-                cur[c][0] = sub_bytes(cur[c][0], prev[c][0]);
-                cur[c][1] = sub_bytes(cur[c][1], prev[c][1]);
+                for (int c = 0; c < D / 32; ++c) *reinterpret_cast<uint2*>(tile + 32 * c + 8 * q) = make_uint2(0u, 0u);
             }
         }
     }
-    int8_t* dst = reinterpret_cast<int8_t*>(a.out[tensor]) + row * D;
-#pragma unroll
-    for (int c = 0; c < C; ++c) *reinterpret_cast<uint2*>(dst + 32 * c + 8 * q) = make_uint2(cur[c][0], cur[c][1]);
+    int8_t* dst = reinterpret_cast<int8_t*>(a.out[tensor]) + row0 * D;
+    // this thread's row of the next tile is loaded while the current one is
+    // decoded and stored (rows past the stream read its last row, unused)
+    RowSyms<D, L> next;
+    next.load(a, tensor, row0 + min(t_begin + r, a.seq - 1u), q);
+    for (uint32_t t0 = t_begin; t0 < t_end; t0 += 64) {
+        const uint32_t n_rows = min(64u, t_end - t0);
+        const RowSyms<D, L> cur = next;
+        if (t0 + 64 < t_end) next.load(a, tensor, row0 + min(t0 + 64 + r, a.seq - 1u), q);
+        if (r < n_rows) groups_to_row<D, L>(cur.d, cur.cbits, q, tile + (r + 1) * STRIDE);
+        __syncthreads();
+        uint4 last = make_uint4(0u, 0u, 0u, 0u);
+        int last_cc = -1;  // this thread's chunk of the tile's row 63, if it stored one
+        for (uint32_t k = threadIdx.x; k < n_rows * CPR; k += 256) {
+            const uint32_t rr = k / CPR, cc = k % CPR;
+            const uint4 v = *reinterpret_cast<const uint4*>(tile + (rr + 1) * STRIDE + 16 * cc);
+            uint4 o = v;
+            if constexpr (DELTA) {
+                const uint4 p = *reinterpret_cast<const uint4*>(tile + rr * STRIDE + 16 * cc);
+                o = make_uint4(sub_bytes(v.x, p.x), sub_bytes(v.y, p.y), sub_bytes(v.z, p.z), sub_bytes(v.w, p.w));
+                if (rr == 63) {
+                    last = v;
+                    last_cc = (int)cc;
+                }
+            }
+            *reinterpret_cast<uint4*>(dst + (size_t)t0 * D + 16 * k) = o;
+        }
+        __syncthreads();  // the tile is read: rows 1..64 (and row 0) may be overwritten
+        if constexpr (DELTA) {
+            if (last_cc >= 0) *reinterpret_cast<uint4*>(tile + 16 * last_cc) = last;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -423,10 +546,14 @@ static hipError_t launch_codec(int kind, bool key, const CodecArgs& a, hipStream
     if (kind == 0) {
         if (key) hipLaunchKernelGGL((dequant_kernel<D, L, true, DR>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((dequant_kernel<D, L, false, DR>), grid, dim3(256), 0, s, a);
-    } else if (kind == 1) {
-        hipLaunchKernelGGL((int8_codes_kernel<D, L, false>), grid, dim3(256), 0, s, a);
     } else {
-        hipLaunchKernelGGL((int8_codes_kernel<D, L, true>), grid, dim3(256), 0, s, a);
+        // int8 codes: blocks of kInt8Tiles tiles of one stream
+        CodecArgs b = a;
+        b.work = (uint32_t)((((uint64_t)a.seq + 64u * kInt8Tiles - 1) / (64u * kInt8Tiles)) * a.bh * a.n_tensors);
+        b.per_xcd = (b.work + 7u) / 8u;
+        dim3 grid8(b.per_xcd * 8u);
+        if (kind == 1) hipLaunchKernelGGL((int8_codes_kernel<D, L, false>), grid8, dim3(256), 0, s, b);
+        else hipLaunchKernelGGL((int8_codes_kernel<D, L, true>), grid8, dim3(256), 0, s, b);
     }
     return hipGetLastError();
 }

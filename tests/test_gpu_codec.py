@@ -62,6 +62,39 @@ def test_int8_codes_and_deltas_match_oracle(D, L):
     assert np.array_equal((got.astype(np.float32) * 0.5) * sc, ref["p"] * sc)
 
 
+@pytest.mark.parametrize("D,L,seq", [(128, 8, 64), (128, 4, 65), (128, 2, 1), (128, 16, 130), (64, 16, 37),
+                                     (64, 2, 130), (64, 4, 200), (64, 8, 63), (256, 16, 63), (256, 4, 129),
+                                     (128, 8, 300), (64, 4, 513), (256, 2, 257)])
+def test_int8_codes_of_any_symbol_bytes_match_oracle(D, L, seq):
+    """Random symbol and coset bytes, so every symbol value the packed format can
+    hold appears (also those above L, which the quantizer never writes); three
+    tensors per launch; tiles cut by seq (one row, exactly one tile, one past)
+    and streams longer than one block's run of tiles."""
+    from nexusquant_amd.codec import codes_int8
+    from nexusquant_amd.ops import PackedCodes
+    print(f"[gpu] int8 codes of random bytes D={D} L={L} seq={seq}", flush=True)
+    rng = np.random.default_rng(1000 * D + 10 * L + seq)
+    b, h, n_t = 2, 3, 3
+    n = b * h * seq
+    raw, codes = [], []
+    for _ in range(n_t):
+        syms = rng.integers(0, 256, (b, h, seq, D // 8 * C.bits_for(L)), dtype=np.uint8)
+        cos = rng.integers(0, 256, (b, h, seq, D // 64), dtype=np.uint8)
+        sc = rng.random((b, h, seq), dtype=np.float32)
+        raw.append((syms, cos))
+        codes.append(PackedCodes(syms=torch.from_numpy(syms).to(DEV), cosets=torch.from_numpy(cos).to(DEV),
+                                 scales=torch.from_numpy(sc).to(DEV), levels=L, head_dim=D, padded_dim=D,
+                                 is_key=False))
+    got = codes_int8(codes)
+    deltas = codes_int8(codes, delta=True)
+    torch.cuda.synchronize()
+    for i, (syms, cos) in enumerate(raw):
+        want = C.codes_2p(C.unpack_symbols(syms.reshape(n, -1), L, D), C.unpack_cosets(cos.reshape(n, -1), D // 8), L)
+        assert np.array_equal(got[i].cpu().numpy().reshape(n, D), want), i
+        d = deltas[i].cpu().numpy().reshape(b * h, seq, D)
+        assert np.array_equal(d, C.delta_tokens(want.reshape(b * h, seq, D))), i
+
+
 def test_nqc1_container_roundtrip_and_ratio():
     from nexusquant_amd.codec import codes_int8, pack_nqc1, unpack_nqc1
     print("[gpu] nqc1", flush=True)
