@@ -242,6 +242,31 @@ def test_paged_forward_head_dims_and_value_ranges(d, group, qdt, vmul):
     _close_fp16(out.float().cpu().numpy(), ref.float().numpy(), bf16=qdt == torch.bfloat16)
 
 
+@pytest.mark.parametrize("d,group,qdt", [(128, 8, torch.float16), (64, 2, torch.bfloat16), (256, 4, torch.float32)])
+def test_paged_forward_rows_of_many_chunks(d, group, qdt):
+    """Rows of 66 chunks (33.6K tokens): the combine takes 32-coordinate slices
+    with 32 chunk groups (rows of fewer than 64 chunks on average take a whole
+    head per workgroup, the case of the tests above)."""
+    from nexusquant_amd.vllm_backend import NexusQuantKVCompressor, NexusQuantPagedAttention
+    print(f"[gpu] paged forward, 66 chunks per row, d={d} group={group} {qdt}", flush=True)
+    kv, base = 1, 500000.0
+    comp = NexusQuantKVCompressor(head_dim=d, bits=2, rope_base=base)
+    attn = NexusQuantPagedAttention(comp)
+    gen = torch.Generator().manual_seed(3 * d + group)
+    n_pages = 2100  # x 16 tokens = 33600 = 65.6 chunks of 512
+    k = (torch.randn(n_pages, kv, 16, d, generator=gen) * 2).to(torch.float16)
+    v = (torch.randn(n_pages, kv, 16, d, generator=gen) * 0.5).to(torch.float16)
+    work = [(k[i].to(DEV), v[i].to(DEV), torch.arange(16, dtype=torch.int32) + 16 * i) for i in range(n_pages)]
+    cache = dict(enumerate(comp.compress_pages(work)))
+    tables = [list(range(n_pages)), list(range(n_pages))[::-1]]
+    ctx = [16 * n_pages, 16 * n_pages - 9]
+    query = torch.randn(2, kv * group, d, generator=gen).to(qdt)
+    out = attn.forward(query.to(DEV), cache, cache, tables, torch.tensor(ctx))
+    torch.cuda.synchronize()
+    ref = _oracle_forward(cache, query, tables, ctx, base, group)
+    _close_fp16(out.float().cpu().numpy(), ref.float().numpy(), bf16=qdt == torch.bfloat16)
+
+
 def test_paged_plan_reuse_across_queries():
     from nexusquant_amd.vllm_backend import NexusQuantKVCompressor, NexusQuantPagedAttention
     print("[gpu] paged plan reuse", flush=True)
