@@ -20,9 +20,9 @@
 //  3. Values are never reconstructed per token: the inverse Hadamard is
 //     linear, so sum_t e_t v_t = h_D * S (sum_t e_t (scale_t / 2) c_t) with
 //     c_t the integer codes (exact in fp16).  The matrix cores accumulate
-//     weights x codes over the chunk, 32 tokens per MFMA; the block applies
-//     S to its sum once, and the combine kernel weights the chunks, applies
-//     h_D and divides by the softmax sum.
+//     weights x codes over the chunk, 32 tokens per MFMA; the combine kernel
+//     weights the chunks' sums, applies S and h_D once per (row, query head)
+//     and divides by the softmax sum.
 //
 // Work items are (chunk, kv head) with the kv head fastest, and block 8k + x
 // takes item x * per_xcd + k: the kv heads of one chunk run on one XCD and
@@ -445,29 +445,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
             for (int i = 0; i < RI; ++i) s_acc[wave][4 * kg + i][NB * n16 + j] = pacc[j][i];
     }
     __syncthreads();
-    // the four waves' sums (fixed order), then the unnormalised Walsh-Hadamard
-    // over D in LDS, in place in s_acc[0]
-    for (int i = threadIdx.x; i < G * D; i += 256) {
-        const int gq = i / D, j = i % D;
-        s_acc[0][gq][j] = (s_acc[0][gq][j] + s_acc[1][gq][j]) + (s_acc[2][gq][j] + s_acc[3][gq][j]);
-    }
-#pragma unroll
-    for (int len = 1; len < D; len <<= 1) {
-        __syncthreads();
-        for (int p = threadIdx.x; p < G * D / 2; p += 256) {
-            const int gq = p / (D / 2), r = p % (D / 2);
-            const int i = (r / len) * 2 * len + (r % len);
-            const float x0 = s_acc[0][gq][i], x1 = s_acc[0][gq][i + len];
-            s_acc[0][gq][i] = x0 + x1;
-            s_acc[0][gq][i + len] = x0 - x1;
-        }
-    }
-    __syncthreads();
+    // the four waves' sums (fixed order), still in the lattice domain: the
+    // combine kernel applies the Walsh-Hadamard S once per (row, head) to the
+    // weighted sum of the chunks (S is linear)
     const float wunscale = __builtin_ldexpf(1.0f, wexp - 14);
     for (int i = threadIdx.x; i < G * D; i += 256) {
         const int gq = i / D, j = i % D;
         float* pp = a.part + ((size_t)chunk * a.q_heads + kh * G + gq) * (D + 2);
-        pp[2 + j] = s_acc[0][gq][j] * wunscale;
+        pp[2 + j] = ((s_acc[0][gq][j] + s_acc[1][gq][j]) + (s_acc[2][gq][j] + s_acc[3][gq][j])) * wunscale;
         if (j == 0) {
             pp[0] = head_max(gq) * a.inv_scale;  // the chunk max in the scaled domain
             pp[1] = head_sum(gq);
@@ -475,29 +460,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     }
 }
 
-// Merge the chunks of one (row, query head).  A workgroup of 1024 threads
-// takes a slice of COLS coordinates of one (row, query head); thread (group,
-// coordinate) sums every (1024 / COLS)-th chunk's weighted S y for its
-// coordinate, and the groups are added in a fixed order.  Slices spread a row
-// with many chunks over more workgroups and shorten each thread's chain of
-// dependent loads (one workgroup per (row, head) left 32 loads per thread at
-// 256 chunks); rows of few chunks take the whole head in one workgroup.
-template <int D, int QDT, int COLS>
+// Merge the chunks of one (row, query head): a workgroup of 1024 threads,
+// thread (group, column) summing the weighted y of every 32nd chunk for the
+// D / 32 coordinates column + 32 i (independent chains, so a row of many
+// chunks is not one long chain of dependent loads per thread); the groups are
+// added in a fixed order, then the Walsh-Hadamard S (in LDS), h_D and the
+// softmax sum turn the lattice-domain sum into the attended value.
+template <int D, int QDT>
 __global__ __launch_bounds__(1024) void paged_attn_combine(AttnArgs a) {
-    constexpr int kCombineCols = COLS;
-    constexpr int kCombineGroups = 1024 / COLS;
-    constexpr int NS = D / kCombineCols;  // slices per (row, head)
-    __shared__ float s_y[kCombineGroups][kCombineCols];
-    __shared__ float s_l[kCombineGroups];
+    constexpr int NG = 32, NI = D / 32;
+    __shared__ float s_y[NG][D];
+    __shared__ float s_l[NG];
     __shared__ float s_m[16];
-    const uint32_t slice = blockIdx.x % NS;
-    const uint32_t rq = blockIdx.x / NS;
-    const uint32_t row = rq / a.q_heads;
-    const uint32_t qh = rq % a.q_heads;
+    const uint32_t row = blockIdx.x / a.q_heads;
+    const uint32_t qh = blockIdx.x % a.q_heads;
     const int c0 = a.row_chunks[row], c1 = a.row_chunks[row + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int grp = tid / kCombineCols, jj = tid % kCombineCols;
-    const int j = (int)slice * kCombineCols + jj;
+    const int grp = tid >> 5, col = tid & 31;
     float M = -__builtin_inff();
     for (int c = c0 + tid; c < c1; c += 1024) M = __builtin_fmaxf(M, a.part[((size_t)c * a.q_heads + qh) * (D + 2)]);
     M = wave_max(M);
@@ -506,28 +485,47 @@ __global__ __launch_bounds__(1024) void paged_attn_combine(AttnArgs a) {
     M = s_m[0];
 #pragma unroll
     for (int w = 1; w < 16; ++w) M = __builtin_fmaxf(M, s_m[w]);
-    float y = 0.0f, L = 0.0f;
-#pragma unroll 4
-    for (int c = c0 + grp; c < c1; c += kCombineGroups) {
+    float y[NI], L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) y[i] = 0.0f;
+#pragma unroll 2
+    for (int c = c0 + grp; c < c1; c += NG) {
         const float* pp = a.part + ((size_t)c * a.q_heads + qh) * (D + 2);
         const float f = expf(pp[0] - M);
-        y = __builtin_fmaf(f, pp[2 + j], y);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) y[i] = __builtin_fmaf(f, pp[2 + col + 32 * i], y[i]);
         L = __builtin_fmaf(f, pp[1], L);
     }
-    s_y[grp][jj] = y;
-    if (jj == 0) s_l[grp] = L;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) s_y[grp][col + 32 * i] = y[i];
+    if (col == 0) s_l[grp] = L;
     __syncthreads();
-    if (grp != 0) return;
-    y = s_y[0][jj];
+    // the groups in order, into s_y[0]; then S over D, in place
+    for (int j = tid; j < D; j += 1024) {
+        float v = s_y[0][j];
+#pragma unroll
+        for (int g = 1; g < NG; ++g) v += s_y[g][j];
+        s_y[0][j] = v;
+    }
+#pragma unroll
+    for (int len = 1; len < D; len <<= 1) {
+        __syncthreads();
+        for (int p = tid; p < D / 2; p += 1024) {
+            const int i = (p / len) * 2 * len + (p % len);
+            const float x0 = s_y[0][i], x1 = s_y[0][i + len];
+            s_y[0][i] = x0 + x1;
+            s_y[0][i + len] = x0 - x1;
+        }
+    }
+    __syncthreads();
+    if (tid >= D) return;
     L = s_l[0];
 #pragma unroll
-    for (int g = 1; g < kCombineGroups; ++g) {
-        y += s_y[g][jj];
-        L += s_l[g];
-    }
+    for (int g = 1; g < NG; ++g) L += s_l[g];
+    const int j = tid;
     const size_t o = ((size_t)row * a.q_heads + qh) * D + j;
     // attended value, then fp16 (the reference's .to(float16)), then the output type
-    const float val = c1 > c0 ? (y * a.hscale) / L : 0.0f;
+    const float val = c1 > c0 ? (s_y[0][j] * a.hscale) / L : 0.0f;
     const uint32_t hb = f32_to_f16_bits(val);
     if constexpr (QDT == NQ_F32) {
         static_cast<float*>(a.out)[o] = f16_bits_to_f32(hb);
@@ -547,13 +545,7 @@ static hipError_t launch_attn(const AttnArgs& a, uint32_t n_chunks, uint32_t bat
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    // chunks per row on average: slices of 32 coordinates (one 128-byte line of a
-    // chunk's y per group) from 64 chunks on.  Measured at 256 chunks per row:
-    // 10.2 us whole-head, 6.8 us with 32-wide slices, 8.6 us with 16-wide.
-    const uint32_t cpr = batch > 0 ? (n_chunks + batch - 1) / batch : 0;
-    const dim3 blk(1024);
-    if (cpr >= 64) hipLaunchKernelGGL((paged_attn_combine<D, QDT, 32>), dim3(batch * a.q_heads * (D / 32)), blk, 0, s, a);
-    else hipLaunchKernelGGL((paged_attn_combine<D, QDT, D>), dim3(batch * a.q_heads), blk, 0, s, a);
+    hipLaunchKernelGGL((paged_attn_combine<D, QDT>), dim3(batch * a.q_heads), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 
@@ -616,8 +608,7 @@ extern "C" int nq_paged_attention(const nq_attn_desc* d, void* stream) {
         NQ_CHECK_ARG((uint64_t)d->n_chunks * d->kv_heads < (1ull << 31) - 8, "nq_paged_attention: grid too large");
         NQ_CHECK_ARG(d->scale_divisor > 0.0f, "nq_paged_attention: scale_divisor must be positive");
     }
-    NQ_CHECK_ARG((uint64_t)d->batch * d->q_heads * (d->head_dim / 32) < (1ull << 31),
-                 "nq_paged_attention: grid too large");
+    NQ_CHECK_ARG((uint64_t)d->batch * d->q_heads < (1ull << 31), "nq_paged_attention: grid too large");
     AttnArgs a = {};
     a.query = d->query;
     a.out = d->out;
