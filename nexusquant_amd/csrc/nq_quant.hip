@@ -338,7 +338,8 @@ template <int D, int L, bool IS_KEY, int DR, bool PAGE>
 __device__ __forceinline__ void quant_row_body(const QuantArgs& a, float (&x)[D / 32][8],
                                                float (&cs)[RopeChunks<D, DR>::value][8],
                                                float (&sn)[RopeChunks<D, DR>::value][8], int q, const RowOut& o,
-                                               uint32_t bh, uint32_t t_in, uint32_t t_out, bool active) {
+                                               uint32_t bh, uint32_t t_in, uint32_t t_out, bool active,
+                                               const float* lds_rope = nullptr) {
     constexpr int C = D / 32;
     constexpr int RC = RopeChunks<D, DR>::value;
     // Keys with DR == D: inverse RoPE and the top Hadamard stage in one step
@@ -347,6 +348,7 @@ __device__ __forceinline__ void quant_row_body(const QuantArgs& a, float (&x)[D 
     if constexpr (MERGED) {
         rope_stage_merged<C>(x, cs, sn);
     } else if constexpr (IS_KEY) {
+        if constexpr (!PAGE && DR != D) load_rope_row<D, DR, RC>(lds_rope, q, cs, sn);  // staged in LDS
         apply_rope<D, DR, RC, true>(x, q, cs, sn);
     }
 
@@ -522,6 +524,7 @@ __device__ __forceinline__ void quant_row_body(const QuantArgs& a, float (&x)[D 
         rope_stage_merged<C>(x, cs, sn);
     } else if constexpr (IS_KEY) {
         if (a.gather && t_out != t_in) load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t_out, q, cs, sn);
+        else if constexpr (!PAGE && DR != D) load_rope_row<D, DR, RC>(lds_rope, q, cs, sn);
         apply_rope<D, DR, RC, false>(x, q, cs, sn);
     }
     if (!active) return;
@@ -629,7 +632,28 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a, const uint
                                                  (lds_void_t*)(wstage + (c * ST::parts + h) * 1024), 16, 0, 0);
     };
 
-    if constexpr (IS_KEY && !PAGE) {
+    // Keys with the padded RoPE layout (head_dim 96) read their RoPE rows from
+    // LDS at each rotation instead of holding them in registers for the whole
+    // work item (48 VGPRs, a wave of occupancy): the block stages its 64 rows'
+    // cos and sin (48 + 48 floats each, 24 KiB) once, before the sub-items.
+    constexpr bool LDS_ROPE = IS_KEY && !PAGE && DR != D;
+    __shared__ __attribute__((aligned(16))) float s_rope[LDS_ROPE ? 2 * 64 * (DR / 2) : 4];
+    const float* my_rope = nullptr;
+    if constexpr (LDS_ROPE) {
+        constexpr int H = DR / 2;  // table columns per row
+        const int r = threadIdx.x >> 2;
+        const float* ct = a.rope_cos + (size_t)t_in * H + (H / 4) * q;
+        const float* st = a.rope_sin + (size_t)t_in * H + (H / 4) * q;
+        float* dc = s_rope + r * H + (H / 4) * q;
+        float* ds = s_rope + 64 * H + r * H + (H / 4) * q;
+#pragma unroll
+        for (int k = 0; k < H / 4; k += 4) {
+            *reinterpret_cast<float4*>(dc + k) = *reinterpret_cast<const float4*>(ct + k);
+            *reinterpret_cast<float4*>(ds + k) = *reinterpret_cast<const float4*>(st + k);
+        }
+        __syncthreads();
+        my_rope = s_rope + r * H;
+    } else if constexpr (IS_KEY && !PAGE) {
         if (!a.gather) load_tables(t_in);
     }
     if constexpr (ST::pipe) stage_rows(j0);
@@ -670,7 +694,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a, const uint
             // position cannot read outside it
             const int32_t pp = gptr<const int32_t>(tab_positions[tensor])[t_in % a.page_tokens];
             load_tables(pp < 0 ? 0u : ((uint32_t)pp >= a.rope_n_pos ? a.rope_n_pos - 1u : (uint32_t)pp));
-        } else if constexpr (IS_KEY) {
+        } else if constexpr (IS_KEY && !LDS_ROPE) {
             if (a.gather) load_tables(t_in);
         }
         RowOut o;
@@ -685,7 +709,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a, const uint
             o.codes8 = nullptr;
             o.scales16 = nullptr;
         }
-        quant_row_body<D, L, IS_KEY, DR, PAGE>(a, x, cs, sn, q, o, bh, t_in, t_out, active);
+        quant_row_body<D, L, IS_KEY, DR, PAGE>(a, x, cs, sn, q, o, bh, t_in, t_out, active, my_rope);
     }
 }
 

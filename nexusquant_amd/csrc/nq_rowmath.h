@@ -227,6 +227,23 @@ __device__ __forceinline__ void load_rope(const float* cos_t, const float* sin_t
     }
 }
 
+// The same columns from one token's row staged in LDS: cos at row[0, DR / 2),
+// sin 64 rows (64 * DR / 2 floats) further on.
+template <int D, int DR, int RC>
+__device__ __forceinline__ void load_rope_row(const float* row, int q, float (&cs)[RC][8], float (&sn)[RC][8]) {
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+        const int col = rope_col<D, DR>(c, q);
+        const float4 c0 = *reinterpret_cast<const float4*>(row + col), c1 = *reinterpret_cast<const float4*>(row + col + 4);
+        const float4 s0 = *reinterpret_cast<const float4*>(row + 64 * (DR / 2) + col);
+        const float4 s1 = *reinterpret_cast<const float4*>(row + 64 * (DR / 2) + col + 4);
+        cs[c][0] = c0.x; cs[c][1] = c0.y; cs[c][2] = c0.z; cs[c][3] = c0.w;
+        cs[c][4] = c1.x; cs[c][5] = c1.y; cs[c][6] = c1.z; cs[c][7] = c1.w;
+        sn[c][0] = s0.x; sn[c][1] = s0.y; sn[c][2] = s0.z; sn[c][3] = s0.w;
+        sn[c][4] = s1.x; sn[c][5] = s1.y; sn[c][6] = s1.z; sn[c][7] = s1.w;
+    }
+}
+
 // INVERSE (input side): lo' = fma(lo, c, hi*s), hi' = fma(hi, c, -(lo*s)).
 // Forward (output side): lo' = fma(lo, c, -(hi*s)), hi' = fma(lo, s, hi*c).
 template <int D, int DR, int RC, bool INVERSE>
