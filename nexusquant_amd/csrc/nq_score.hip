@@ -528,17 +528,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     }
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16x16(uint4 a, uint4 b, f32x4 acc) {
+    if constexpr (DT == NQ_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
+                                                      acc, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       acc, 0, 0, 0);
+}
+
 // Column sums of one 32 x 32 tile of a lane's key column (queries = rows
 // acc_row(j, g)): p = round_T(exp2(x * log2(e) + nm[row]) * rz[row]) with x the
-// eager logit, then colacc += P^T . ones on the matrix cores.  The lane's 16
-// rounded values of key c are exactly row c of an A operand (8 per MFMA, in
-// any k order since B is all ones), so two 32x32x16 MFMAs add them in fp32;
-// every lane of the result then holds the running sums of 16 keys.  MASKED:
-// rows r with r < key_off (row before the key) or r >= row_end (past seq)
-// contribute 0.
+// eager logit, then colacc += P^T . B on the matrix cores with two 16x16x32
+// MFMAs (8 rounded values per lane each).  As their A operand, lane l's 8
+// values are row l % 16, K slice l / 16; that lane holds key l % 32 = row +
+// 16 ((l / 16) & 1).  B (ones_sel) is 1 where column 0 meets the slices of key
+// row and column 1 those of key row + 16, else 0, so column 0 of the result
+// accumulates the sums of keys 0..15 and column 1 those of keys 16..31, in
+// fp32.  That is half the matrix-core passes of summing against an all-ones
+// 32x32x16 operand.  MASKED: rows r with r < key_off (row before the key) or
+// r >= row_end (past seq) contribute 0.
 template <int DT, bool MASKED>
 __device__ __forceinline__ void col_fold(const f32x16& acc, const float* nm_rows, const float* rz_rows, float scaling,
-                                         int key_off, int row_end, int g, f32x16& colacc) {
+                                         int key_off, int row_end, int g, const uint4& ones_sel, f32x4& colacc) {
     uint32_t pk[8];
 #pragma unroll
     for (int jq = 0; jq < 4; ++jq) {
@@ -562,10 +577,8 @@ __device__ __forceinline__ void col_fold(const f32x16& acc, const float* nm_rows
             pk[j / 2] = round_pair<DT>(p0, p1);
         }
     }
-    constexpr uint32_t one2 = DT == NQ_F16 ? 0x3C003C00u : 0x3F803F80u;  // (1.0, 1.0) in the model type
-    const uint4 ones = make_uint4(one2, one2, one2, one2);
-    colacc = mfma16<DT>(make_uint4(pk[0], pk[1], pk[2], pk[3]), ones, colacc);
-    colacc = mfma16<DT>(make_uint4(pk[4], pk[5], pk[6], pk[7]), ones, colacc);
+    colacc = mfma16x16<DT>(make_uint4(pk[0], pk[1], pk[2], pk[3]), ones_sel, colacc);
+    colacc = mfma16x16<DT>(make_uint4(pk[4], pk[5], pk[6], pk[7]), ones_sel, colacc);
 }
 
 template <int DT, int D>
@@ -594,7 +607,16 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
     const bool live = k0 < a.seq;
     uint4 kr[RealTile<D>::KS];
     row_operand<D>(kbase, key, a.seq, g, kr);
-    f32x16 colacc = {};  // row r = key k0 + r: its column sum (every column holds it)
+    f32x4 colacc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // 16x16x32 B operand: column n of lane l is l % 16, its K slice l / 16; a
+    // slice holds key (l % 32) = row + 16 ((l / 16) & 1), so column 0 sums the
+    // slices of key row and column 1 those of key row + 16
+    uint4 ones_sel;
+    {
+        constexpr uint32_t one2 = DT == NQ_F16 ? 0x3C003C00u : 0x3F803F80u;
+        const uint32_t v = (lane & 15) == ((lane >> 4) & 1) ? one2 : 0u;
+        ones_sel = make_uint4(v, v, v, v);
+    }
     // One stage: 64 query rows by direct-to-LDS loads, and (wave 0) their row
     // statistics, one dword per lane.  Two buffers in fixed roles as in
     // real_rowstats; each thread waits for its own loads before the barrier.
@@ -621,8 +643,8 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
                 // first tile's VALU work
                 const f32x16 acc0 = logits_lds_regs<DT, D>(cur, kr, c, g);
                 const f32x16 acc1 = logits_lds_regs<DT, D>(cur + 32 * RealTile<D>::ROWB, kr, c, g);
-                col_fold<DT, false>(acc0, cnm, crz, a.scaling, 0, 0, g, colacc);
-                col_fold<DT, false>(acc1, cnm + 32, crz + 32, a.scaling, 0, 0, g, colacc);
+                col_fold<DT, false>(acc0, cnm, crz, a.scaling, 0, 0, g, ones_sel, colacc);
+                col_fold<DT, false>(acc1, cnm + 32, crz + 32, a.scaling, 0, 0, g, ones_sel, colacc);
             } else {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
@@ -630,10 +652,10 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
                     if (qt < my_first) continue;
                     const f32x16 acc = logits_lds_regs<DT, D>(cur + h * 32 * RealTile<D>::ROWB, kr, c, g);
                     if (qt > my_first && qt * 32 + 32 <= a.seq)
-                        col_fold<DT, false>(acc, cnm + 32 * h, crz + 32 * h, a.scaling, 0, 0, g, colacc);
+                        col_fold<DT, false>(acc, cnm + 32 * h, crz + 32 * h, a.scaling, 0, 0, g, ones_sel, colacc);
                     else
                         col_fold<DT, true>(acc, cnm + 32 * h, crz + 32 * h, a.scaling, key - qt * 32,
-                                           a.seq - qt * 32, g, colacc);
+                                           a.seq - qt * 32, g, ones_sel, colacc);
                 }
             }
         }
@@ -645,12 +667,12 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
         stage(it, lds0, st_nm0, st_rz0, lds1, st_nm1, st_rz1);
         if (it + 1 < n_it) stage(it + 1, lds1, st_nm1, st_rz1, lds0, st_nm0, st_rz0);
     }
-    // lanes 0 and 32 hold the sums of keys k0 + acc_row(j, g), j = 0..15
-    if (c == 0 && live) {
+    // lane l (column n = l % 16 < 2) holds the sums of keys k0 + 4 (l / 16) + i + 16 n
+    if ((lane & 15) < 2 && live) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int kk = k0 + acc_row(j, lane);
-            if (kk < a.seq) a.colsum[stat + kk] = colacc[j];
+        for (int i = 0; i < 4; ++i) {
+            const int kk = k0 + 4 * (lane >> 4) + i + 16 * (lane & 15);
+            if (kk < a.seq) a.colsum[stat + kk] = colacc[i];
         }
     }
 }
