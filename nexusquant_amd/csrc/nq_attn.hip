@@ -605,10 +605,10 @@ extern "C" int nq_paged_attention(const nq_attn_desc* d, void* stream) {
         const int64_t need = nq_paged_attention_workspace(d->n_chunks, d->q_heads, d->head_dim);
         NQ_CHECK_ARG(d->workspace != nullptr && d->workspace_bytes >= need,
                      "nq_paged_attention: workspace of %lld bytes needed", (long long)need);
-        NQ_CHECK_ARG((uint64_t)d->n_chunks * d->kv_heads < (1ull << 31) - 8, "nq_paged_attention: grid too large");
+        NQ_CHECK_ARG((uint64_t)d->n_chunks * d->kv_heads + 8 <= max_blocks(256), "nq_paged_attention: grid too large");
         NQ_CHECK_ARG(d->scale_divisor > 0.0f, "nq_paged_attention: scale_divisor must be positive");
     }
-    NQ_CHECK_ARG((uint64_t)d->batch * d->q_heads < (1ull << 31), "nq_paged_attention: grid too large");
+    NQ_CHECK_ARG((uint64_t)d->batch * d->q_heads <= max_blocks(1024), "nq_paged_attention: grid too large");
     AttnArgs a = {};
     a.query = d->query;
     a.out = d->out;

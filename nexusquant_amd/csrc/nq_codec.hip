@@ -601,7 +601,7 @@ static int run_codec(const nq_codes_desc* d, int kind, void* stream) {
     a.n_tensors = (uint32_t)d->n_tensors;
     a.bh = (uint32_t)d->batch * (uint32_t)d->heads;
     const uint64_t work = (uint64_t)((d->seq + 63) / 64) * a.bh * a.n_tensors;
-    NQ_CHECK_ARG(work < (1ull << 32) - 8, "nq codes: grid too large");
+    NQ_CHECK_ARG(work + 8 <= max_blocks(256), "nq codes: grid too large");
     a.work = (uint32_t)work;
     a.per_xcd = (uint32_t)((work + 7) / 8);
     a.hscale = d->hadamard_scale;

@@ -23,6 +23,10 @@ void set_error(const char* fmt, ...);
         }                                  \
     } while (0)
 
+// A dispatch's grid size is a 32-bit count of work-items per dimension, so a
+// launch of `threads`-wide blocks takes at most this many blocks in one.
+constexpr uint64_t max_blocks(uint32_t threads) { return 0xffffffffull / threads; }
+
 #define NQ_CHECK_HIP(expr)                                                   \
     do {                                                                     \
         hipError_t _e = (expr);                                              \

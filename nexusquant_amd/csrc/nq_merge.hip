@@ -546,7 +546,7 @@ extern "C" int nq_merge_values(const nq_merge_desc* d, void* stream) {
     aa.split_len = split_len;
     aa.e_tiles = (s + kMT - 1) / kMT;
     const uint64_t grid = (uint64_t)b * aa.e_tiles * n_split;
-    NQ_CHECK_ARG(grid < (1ull << 31), "nq_merge_values: assignment grid too large");
+    NQ_CHECK_ARG(grid <= max_blocks(256), "nq_merge_values: assignment grid too large");
     // partials of splits a row never reaches stay unwritten: mark them empty
     hipLaunchKernelGGL(nq_fill_i32, dim3((uint32_t)((bs * n_split + 255) / 256)), dim3(256), 0, st, best_idx,
                        bs * n_split, -1);

@@ -8,6 +8,7 @@
 // and each coordinate is scaled once by fl(fl(scale / 2) * h_D); keys leave the
 // top butterfly stage to the merged step with forward RoPE at the stored
 // position.  oracle/nq_spec.c (nqs_page_decode) restates this order.
+#include <algorithm>
 #include "nq_rowmath.h"
 
 namespace nq {
@@ -158,27 +159,33 @@ __device__ __forceinline__ uint32_t nibble_of(int8_t c) {
     return (uint32_t)(v < 0 ? 0 : (v > 15 ? 15 : v));
 }
 
+// Both nibble kernels stride over the grid, which the host caps at
+// kNibbleBlocks blocks: inputs of more than 2^32 elements need no wider grid.
+constexpr int64_t kNibbleBlocks = 1 << 20;
+
 __global__ __launch_bounds__(256) void nibble_pack_kernel(const int8_t* codes, int64_t rows, int32_t d,
                                                           uint8_t* packed) {
     const int32_t pd = (d + 1) / 2;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * pd) return;
-    const int64_t r = i / pd;
-    const int32_t j = (int32_t)(i - r * pd);
-    const int8_t* row = codes + r * d;
-    const uint32_t lo = nibble_of(row[2 * j]);
-    const uint32_t hi = 2 * j + 1 < d ? nibble_of(row[2 * j + 1]) : 0u;  // the pad nibble is 0
-    packed[i] = (uint8_t)(lo | (hi << 4));
+    const int64_t n = rows * pd;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / pd;
+        const int32_t j = (int32_t)(i - r * pd);
+        const int8_t* row = codes + r * d;
+        const uint32_t lo = nibble_of(row[2 * j]);
+        const uint32_t hi = 2 * j + 1 < d ? nibble_of(row[2 * j + 1]) : 0u;  // the pad nibble is 0
+        packed[i] = (uint8_t)(lo | (hi << 4));
+    }
 }
 
 __global__ __launch_bounds__(256) void nibble_unpack_kernel(const uint8_t* packed, int64_t rows, int32_t pd,
                                                             int32_t d, int8_t* codes) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * d) return;
-    const int64_t r = i / d;
-    const int32_t k = (int32_t)(i - r * d);
-    const uint32_t b = packed[r * pd + k / 2];
-    codes[i] = (int8_t)((int)((k & 1) ? (b >> 4) : (b & 15u)) - 8);
+    const int64_t n = rows * d;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / d;
+        const int32_t k = (int32_t)(i - r * d);
+        const uint32_t b = packed[r * pd + k / 2];
+        codes[i] = (int8_t)((int)((k & 1) ? (b >> 4) : (b & 15u)) - 8);
+    }
 }
 
 template <int D>
@@ -212,7 +219,7 @@ extern "C" int nq_page_decode(const nq_page_desc* d, void* stream) {
                      "nq_page_decode: keys need RoPE tables");
     }
     const uint64_t tiles = (rows + 63) / 64;
-    NQ_CHECK_ARG(tiles * (uint64_t)d->n_pages < (1ull << 31), "nq_page_decode: grid too large");
+    NQ_CHECK_ARG(tiles * (uint64_t)d->n_pages <= max_blocks(256), "nq_page_decode: grid too large");
     PageArgs a = {};
     a.codes = d->codes;
     a.scales = d->scales;
@@ -294,13 +301,13 @@ extern "C" int nq_page_logits(const nq_page_desc* d, const void* query, int32_t 
 
 extern "C" int nq_nibble_pack(const int8_t* codes, int64_t rows, int32_t d, uint8_t* packed, void* stream) {
     using namespace nq;
-    NQ_CHECK_ARG(rows >= 0 && d > 0, "nq_nibble_pack: bad geometry");
+    NQ_CHECK_ARG(rows >= 0 && rows <= (1ll << 40) && d > 0, "nq_nibble_pack: bad geometry");
     const int64_t n = rows * ((d + 1) / 2);
     if (n == 0) return NQ_OK;
     NQ_CHECK_ARG(codes && packed, "nq_nibble_pack: NULL pointer");
-    NQ_CHECK_ARG((n + 255) / 256 < (1ll << 31), "nq_nibble_pack: too many elements");
-    hipLaunchKernelGGL(nibble_pack_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                       codes, rows, d, packed);
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, kNibbleBlocks);
+    hipLaunchKernelGGL(nibble_pack_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, codes, rows, d,
+                       packed);
     NQ_CHECK_HIP(hipGetLastError());
     return NQ_OK;
 }
@@ -308,14 +315,14 @@ extern "C" int nq_nibble_pack(const int8_t* codes, int64_t rows, int32_t d, uint
 extern "C" int nq_nibble_unpack(const uint8_t* packed, int64_t rows, int32_t packed_cols, int32_t d, int8_t* codes,
                                 void* stream) {
     using namespace nq;
-    NQ_CHECK_ARG(rows >= 0 && d > 0 && packed_cols > 0 && d <= 2 * (int64_t)packed_cols,
+    NQ_CHECK_ARG(rows >= 0 && rows <= (1ll << 40) && d > 0 && packed_cols > 0 && d <= 2 * (int64_t)packed_cols,
                  "nq_nibble_unpack: bad geometry (d %d, packed_cols %d)", d, packed_cols);
     const int64_t n = rows * d;
     if (n == 0) return NQ_OK;
     NQ_CHECK_ARG(codes && packed, "nq_nibble_unpack: NULL pointer");
-    NQ_CHECK_ARG((n + 255) / 256 < (1ll << 31), "nq_nibble_unpack: too many elements");
-    hipLaunchKernelGGL(nibble_unpack_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0,
-                       (hipStream_t)stream, packed, rows, packed_cols, d, codes);
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, kNibbleBlocks);
+    hipLaunchKernelGGL(nibble_unpack_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, packed, rows,
+                       packed_cols, d, codes);
     NQ_CHECK_HIP(hipGetLastError());
     return NQ_OK;
 }

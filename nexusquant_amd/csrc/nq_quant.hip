@@ -826,7 +826,7 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     a.n_tensors = (uint32_t)d->n_tensors;
     a.batch = (uint32_t)d->batch;
     const uint64_t work = plan_work(a, (uint64_t)(d->seq_out + 63) / 64, d->is_key ? kKeyGroup : kMaxGroup);
-    NQ_CHECK_ARG(work < (1ull << 32) - 8, "nq_quantize: %llu work items exceed the grid limit",
+    NQ_CHECK_ARG(work + 8 <= max_blocks(256), "nq_quantize: %llu work items exceed the grid limit",
                  (unsigned long long)work);
     hipStream_t s = (hipStream_t)stream;
     hipError_t e;
@@ -907,7 +907,7 @@ extern "C" int nq_page_encode(const nq_page_desc* d, void* stream) {
     a.page_tokens = (uint32_t)(d->tokens > 0 ? d->tokens : 1);
     a.rope_n_pos = (uint32_t)(d->is_key ? d->rope_n_pos : 1);
     const uint64_t work = plan_work(a, (rows + 63) / 64, kMaxGroup);
-    NQ_CHECK_ARG(work < (1ull << 32) - 8, "nq_page_encode: %llu work items exceed the grid limit",
+    NQ_CHECK_ARG(work + 8 <= max_blocks(256), "nq_page_encode: %llu work items exceed the grid limit",
                  (unsigned long long)work);
     hipStream_t s = (hipStream_t)stream;
     const bool key = d->is_key != 0;

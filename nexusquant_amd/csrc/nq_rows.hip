@@ -88,7 +88,7 @@ extern "C" int nq_gather_rows(const uint64_t* src, const uint64_t* dst, int32_t 
     a.d = (uint32_t)head_dim;
     a.chunks_per_row = (uint32_t)(head_dim / 8);
     a.chunks = (uint64_t)batch * heads * seq_out * a.chunks_per_row;
-    NQ_CHECK_ARG((a.chunks + 255) / 256 < (1ull << 31), "nq_gather_rows: tensor too large");
+    NQ_CHECK_ARG((a.chunks + 255) / 256 <= max_blocks(256), "nq_gather_rows: tensor too large");
     dim3 grid((uint32_t)((a.chunks + 255) / 256), (uint32_t)n_tensors);
     hipStream_t s = (hipStream_t)stream;
     switch (dtype) {

@@ -94,3 +94,23 @@ def test_noalloc_keykey_rejects_shapes_beyond_its_scratch_without_a_gpu():
     assert st == -1 and b"scratch" in lib.nq_last_error()
     st = lib.nq_score_keykey_noalloc(dummy, _lib.NQ_F16, 0, h, s, 128, obs, ctypes.c_float(1.0), dummy, None)
     assert st == -1
+
+
+def test_grid_limits_are_checked_on_the_host_without_a_gpu():
+    # A dispatch's grid is at most 2^32 - 1 work-items per dimension; shapes
+    # beyond what a launch can cover are refused before any HIP call, and the
+    # dummy pointers are never dereferenced.
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(256)
+    d = _lib.CodesDesc()
+    d.n_tensors, d.batch, d.heads, d.seq = 65535, 1, 8, 1 << 27   # 2^30 rows per tensor
+    d.head_dim, d.levels, d.is_key = 128, 8, 0
+    d.syms = d.cosets = d.scales = d.out = dummy
+    d.hadamard_scale = 1.0
+    assert lib.nq_dequantize(ctypes.byref(d), None) == -1
+    assert b"grid too large" in lib.nq_last_error()
+    # the nibble kernels stride over a capped grid; only absurd row counts are refused
+    assert lib.nq_nibble_pack(dummy, 1 << 41, 128, dummy, None) == -1
+    assert b"bad geometry" in lib.nq_last_error()
+    assert lib.nq_nibble_unpack(dummy, 1 << 41, 64, 128, dummy, None) == -1
+    assert b"bad geometry" in lib.nq_last_error()
