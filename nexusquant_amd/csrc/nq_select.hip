@@ -1,18 +1,29 @@
 // Keep-mask construction on gfx950: BOS + recent window + top-k of the
 // evictable prefix + protected positions, and the ascending kept-index list.
 //
-// One 1024-thread block per batch row.  The k-th largest importance of the
-// prefix is found by an MSB-first radix select over order-preserving 32-bit
-// keys (4 passes of 8 bits, 256-bin LDS histograms, the row read from global
-// memory each pass), then one stable pass marks keys above the threshold and
-// the first (lowest-index) keys equal to it, and compacts the kept indices
-// with a block prefix sum.  Ties at the threshold therefore keep the lowest
-// positions; torch.topk leaves their order unspecified.
+// One 1024-thread block per batch row.  The row's order-preserving 32-bit keys
+// are staged in LDS, 16384 positions per window (a row of at most one window
+// is staged once; longer rows are re-staged per pass and window), with every
+// thread's 16 loads in flight at once.  Thread t owns the 16 consecutive
+// positions 16t .. 16t+15 of a window.
+//  1. The k-th largest key of the prefix is found by an MSB-first radix select
+//     (4 passes of 8 bits into a 256-bin LDS histogram); the bin holding it is
+//     picked by one block scan of the bins in descending order.
+//  2. One stable pass per window marks keys above the threshold and the first
+//     (lowest-position) keys equal to it: a block scan of the threads' counts
+//     of threshold-equal keys ranks them, and keeps the first `want`.
+//  3. Protected positions are set in the window's LDS flags, which are then
+//     written out and compacted into the kept-index list with one more block
+//     scan.
+// Ties at the threshold therefore keep the lowest positions; torch.topk leaves
+// their order unspecified.
 #include "nq_common.h"
 
 namespace nq {
 
 constexpr int kSelThreads = 1024;
+constexpr int kPer = 16;                   // consecutive positions per thread in a window
+constexpr int kWin = kSelThreads * kPer;   // positions per LDS window
 
 __device__ __forceinline__ uint32_t order_key(float f) {
     uint32_t u = __builtin_bit_cast(uint32_t, f);
@@ -62,82 +73,138 @@ struct SelectArgs {
 };
 
 __global__ __launch_bounds__(kSelThreads) void keep_mask_kernel(SelectArgs a) {
+    __shared__ __align__(16) uint32_t s_key[kWin];   // order keys of one window
+    __shared__ __align__(16) uint8_t s_keep[kWin];   // keep flags of one window
     __shared__ uint32_t hist[256];
     __shared__ uint32_t scan_lds[64];
-    __shared__ uint32_t sel[4];
+    __shared__ uint32_t sel[2];
     const int row = blockIdx.x;
     const int t = threadIdx.x;
     const float* imp = a.importance + (size_t)row * a.seq;
-    // candidates: positions 1 .. prefix-1
-    const int lo = 1, hi = a.prefix;
+    const int lo = 1, hi = a.prefix;  // candidates: positions 1 .. prefix-1
+    const int n_win = (a.seq + kWin - 1) / kWin;
+    // keys of window w into s_key: coalesced loads, all of a thread's in flight
+    auto stage = [&](int w) {
+        const int base = w * kWin;
+        uint32_t v[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = base + j * kSelThreads + t;
+            v[j] = i < a.seq ? order_key(imp[i]) : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) s_key[j * kSelThreads + t] = v[j];
+    };
+    // this thread's 16 consecutive keys of the staged window
+    auto my_keys = [&](uint32_t (&u)[kPer]) {
+        const uint4* src = reinterpret_cast<const uint4*>(s_key + kPer * t);
+#pragma unroll
+        for (int q = 0; q < kPer / 4; ++q) {
+            const uint4 x = src[q];
+            u[4 * q] = x.x;
+            u[4 * q + 1] = x.y;
+            u[4 * q + 2] = x.z;
+            u[4 * q + 3] = x.w;
+        }
+    };
+    const bool staged = n_win == 1 && a.k > 0;  // one window: staged once for every pass
+    if (staged) stage(0);
     uint32_t want = (uint32_t)a.k;
     uint32_t prefix_bits = 0, mask = 0;
     if (want > 0) {
         for (int shift = 24; shift >= 0; shift -= 8) {
-            for (int i = t; i < 256; i += kSelThreads) hist[i] = 0;
-            __syncthreads();
-            for (int i = lo + t; i < hi; i += kSelThreads) {
-                uint32_t u = order_key(imp[i]);
-                if ((u & mask) == prefix_bits) atomicAdd(&hist[(u >> shift) & 0xffu], 1u);
-            }
-            __syncthreads();
-            if (t == 0) {
-                uint32_t acc = 0;
-                int b = 255;
-                for (; b > 0; --b) {
-                    if (acc + hist[b] >= want) break;
-                    acc += hist[b];
+            if (t < 256) hist[t] = 0;
+            for (int w = 0; w < n_win; ++w) {
+                if (!staged) {
+                    __syncthreads();  // the previous window's keys are read
+                    stage(w);
                 }
-                sel[0] = (uint32_t)b;
-                sel[1] = acc;
+                __syncthreads();  // keys staged, histogram cleared
+                uint32_t u[kPer];
+                my_keys(u);
+                const int p0 = w * kWin + kPer * t;
+#pragma unroll
+                for (int j = 0; j < kPer; ++j) {
+                    const int p = p0 + j;
+                    if (p >= lo && p < hi && (u[j] & mask) == prefix_bits) atomicAdd(&hist[(u[j] >> shift) & 0xffu], 1u);
+                }
+            }
+            __syncthreads();  // the pass's histogram is complete
+            // bins from the top: the one where the running count reaches want
+            // (unique: want >= 1 and the matching keys number at least want)
+            const uint32_t h = t < 256 ? hist[255 - t] : 0u;
+            uint32_t tot;
+            const uint32_t incl = block_scan(h, scan_lds, &tot);
+            if (t < 256 && incl >= want && incl - h < want) {
+                sel[0] = 255u - (uint32_t)t;
+                sel[1] = incl - h;
             }
             __syncthreads();
             want -= sel[1];
             prefix_bits |= sel[0] << shift;
             mask |= 0xffu << shift;
-            __syncthreads();
         }
     }
     // want = number of threshold-equal keys to keep (lowest positions first)
     const uint32_t thr = prefix_bits;
-    const uint32_t take_eq = (a.k > 0) ? want : 0u;
+    const uint32_t take_eq = a.k > 0 ? want : 0u;
     uint32_t eq_before = 0, kept_before = 0;
-    for (int base = 0; base < a.seq; base += kSelThreads) {
-        const int i = base + t;
-        bool valid = i < a.seq;
-        bool cand = valid && i >= lo && i < hi && a.k > 0;
-        uint32_t u = cand ? order_key(imp[i]) : 0u;
-        uint32_t is_eq = (cand && u == thr) ? 1u : 0u;
-        uint32_t eq_total;
-        uint32_t eq_incl = block_scan(is_eq, scan_lds, &eq_total);
-        bool keep = false;
-        if (valid) {
-            keep = (i == 0) || (a.window > 0 && i >= a.seq - a.window);
-            if (cand && u > thr) keep = true;
-            if (is_eq && (eq_before + eq_incl - 1u) < take_eq) keep = true;
+    uint8_t* krow = a.keep + (size_t)row * a.seq;
+    int32_t* idx = a.kept_idx + (size_t)row * a.seq;
+    for (int w = 0; w < n_win; ++w) {
+        const int base = w * kWin;
+        if (a.k > 0 && !staged) {
+            __syncthreads();
+            stage(w);
         }
-        eq_before += eq_total;
-        if (valid) a.keep[(size_t)row * a.seq + i] = keep ? 1 : 0;
         __syncthreads();
-    }
-    // Protected positions (after the stable pass; they never reduce the set).
-    // The keep bytes are re-read below by other waves of the block: the device
-    // scope fences make the stores complete and visible before the barrier.
-    __threadfence();
-    __syncthreads();
-    for (int j = t; j < a.n_protected; j += kSelThreads) {
-        int p = a.protected_pos[j];
-        if (p >= 0 && p < a.seq) a.keep[(size_t)row * a.seq + p] = 1;
-    }
-    __threadfence();
-    __syncthreads();
-    for (int base = 0; base < a.seq; base += kSelThreads) {
-        const int i = base + t;
-        uint32_t kv = (i < a.seq && a.keep[(size_t)row * a.seq + i]) ? 1u : 0u;
-        uint32_t tot;
-        uint32_t incl = block_scan(kv, scan_lds, &tot);
-        if (kv) a.kept_idx[(size_t)row * a.seq + kept_before + incl - 1u] = i;
-        kept_before += tot;
+        uint32_t u[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) u[j] = 0u;
+        if (a.k > 0) my_keys(u);
+        const int p0 = base + kPer * t;
+        uint32_t eqm = 0, gtm = 0;  // this thread's threshold-equal / greater candidates
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int p = p0 + j;
+            const bool cand = a.k > 0 && p >= lo && p < hi;
+            if (cand && u[j] == thr) eqm |= 1u << j;
+            if (cand && u[j] > thr) gtm |= 1u << j;
+        }
+        const uint32_t n_eq = (uint32_t)__builtin_popcount(eqm);
+        uint32_t eq_tot;
+        uint32_t rank = eq_before + block_scan(n_eq, scan_lds, &eq_tot) - n_eq;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int p = p0 + j;
+            bool keep = p == 0 || (a.window > 0 && p >= a.seq - a.window) || ((gtm >> j) & 1u);
+            if ((eqm >> j) & 1u) {
+                keep = keep || rank < take_eq;
+                ++rank;
+            }
+            s_keep[kPer * t + j] = (p < a.seq && keep) ? 1 : 0;
+        }
+        eq_before += eq_tot;
+        __syncthreads();
+        // protected positions never reduce the set
+        for (int j = t; j < a.n_protected; j += kSelThreads) {
+            const int p = a.protected_pos[j];
+            if (p >= base && p < base + kWin && p < a.seq) s_keep[p - base] = 1;
+        }
+        __syncthreads();
+        uint32_t km = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) km |= (uint32_t)(s_keep[kPer * t + j] != 0) << j;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j)
+            if (p0 + j < a.seq) krow[p0 + j] = (uint8_t)((km >> j) & 1u);
+        const uint32_t n_k = (uint32_t)__builtin_popcount(km);
+        uint32_t k_tot;
+        uint32_t out = kept_before + block_scan(n_k, scan_lds, &k_tot) - n_k;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j)
+            if ((km >> j) & 1u) idx[out++] = p0 + j;
+        kept_before += k_tot;
     }
     if (t == 0) a.n_kept[row] = (int32_t)kept_before;
 }

@@ -130,7 +130,7 @@ def test_real_scorer_at_c4_layer_size():
 
 
 @pytest.mark.parametrize("s,rate,sw", [(8192, 0.25, 32), (1000, 0.6, 32), (300, 0.8, 8), (50, 0.5, 4),
-                                       (33, 0.6, 32), (4096, 0.35, 0)])
+                                       (33, 0.6, 32), (4096, 0.35, 0), (16385, 0.5, 16), (40000, 0.3, 32)])
 def test_keep_mask_matches_oracle(s, rate, sw):
     from nexusquant_amd.ops import keep_mask
     print(f"[gpu] keep mask s={s} rate={rate}", flush=True)
@@ -162,6 +162,48 @@ def test_keep_mask_ties_keep_lowest_positions_and_protected():
     # row 1: the ten high scores, then the lowest tied positions
     assert keep[1, 100:110].all()
     assert int(n_kept[0]) == int(keep[0].sum()) and int(n_kept[1]) == int(keep[1].sum())
+
+
+def _keep_lowest_ties(imp, rate, sw, protected):
+    """Keep mask with threshold ties resolved to the lowest positions (numpy)."""
+    b, s = imp.shape
+    prefix = max(s - sw, 0)
+    k = min(max(1, int(prefix * (1.0 - rate))), prefix - 1)
+    keep = np.zeros((b, s), bool)
+    keep[:, 0] = True
+    if sw > 0:
+        keep[:, max(0, s - sw):] = True
+    for r in range(b):
+        cand = imp[r, 1:prefix]
+        thr = np.sort(cand)[::-1][k - 1]
+        keep[r, 1:prefix] |= cand > thr
+        eq = np.nonzero(cand == thr)[0] + 1
+        keep[r, eq[:k - int((cand > thr).sum())]] = True
+    for pp in protected:
+        if 0 <= pp < s:
+            keep[:, pp] = True
+    return keep
+
+
+def test_keep_mask_ties_across_windows():
+    # rows longer than one 16384-position window, scores with many ties, protected
+    # positions on both sides of the window edges
+    from nexusquant_amd.ops import keep_mask
+    print("[gpu] keep mask ties across windows s=40000", flush=True)
+    g = torch.Generator().manual_seed(7)
+    s = 40000
+    imp = (torch.randint(0, 40, (3, s), generator=g).float() / 40.0)
+    imp[1] = 0.25                       # one value everywhere: every candidate ties
+    imp[2, 20000:20100] = 2.0
+    prot = [5, 16383, 16384, 16385, 32767, 32768, 39999, 25000]
+    keep, kept, n_kept = keep_mask(imp.to(DEV), 0.55, 32, protected_positions=prot)
+    want = _keep_lowest_ties(imp.numpy(), 0.55, 32, prot)
+    assert np.array_equal(keep.cpu().bool().numpy(), want)
+    kk, nk = kept.cpu(), n_kept.cpu()
+    for bi in range(3):
+        pos = np.nonzero(want[bi])[0]
+        assert int(nk[bi]) == pos.size
+        assert np.array_equal(kk[bi, :pos.size].numpy(), pos.astype(np.int32))
 
 
 def test_mask_eviction_matches_reference_fixture(golden):
