@@ -902,13 +902,27 @@ __global__ __launch_bounds__(256) void real_output(OutArgs o) {
         }
 }
 
-__global__ __launch_bounds__(256) void head_mean_accumulate(const float* colsum, float* importance, int hq,
-                                                            int seq) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
+// importance[b, i] += mean over heads of colsum[b, h, i], the heads summed in
+// order; 64-thread blocks spread a row over many CUs, and the loads go out 8
+// heads at a time ahead of their adds.
+constexpr int kHeadMeanThreads = 64;
+
+__global__ __launch_bounds__(kHeadMeanThreads) void head_mean_accumulate(const float* colsum, float* importance,
+                                                                         int hq, int seq) {
+    const int i = blockIdx.x * kHeadMeanThreads + threadIdx.x;
     const int b = blockIdx.y;
     if (i >= seq) return;
+    const float* col = colsum + (size_t)b * hq * seq + i;
     float s = 0.0f;
-    for (int h = 0; h < hq; ++h) s += colsum[((size_t)b * hq + h) * seq + i];
+    int h = 0;
+    for (; h + 8 <= hq; h += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = col[(size_t)(h + u) * seq];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; h < hq; ++h) s += col[(size_t)h * seq];
     importance[(size_t)b * seq + i] += s / (float)hq;
 }
 
@@ -929,8 +943,8 @@ static hipError_t launch_real(const RealArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((real_rowstats<DT, D>), grid, dim3(256), 0, st, w);
         hipLaunchKernelGGL((real_colsum<DT, D>), grid, dim3(256), 0, st, w);
     }
-    hipLaunchKernelGGL(head_mean_accumulate, dim3((a.seq + 255) / 256, a.batch), dim3(256), 0, st, a.colsum,
-                       a.importance, a.hq, a.seq);
+    hipLaunchKernelGGL(head_mean_accumulate, dim3((a.seq + kHeadMeanThreads - 1) / kHeadMeanThreads, a.batch),
+                       dim3(kHeadMeanThreads), 0, st, a.colsum, a.importance, a.hq, a.seq);
     return hipGetLastError();
 }
 
@@ -945,8 +959,8 @@ static hipError_t launch_attention(const RealArgs& a, const void* v, void* out, 
     hipLaunchKernelGGL((real_rowstats<DT, D>), grid, dim3(256), 0, st, w);
     if (with_importance) {
         hipLaunchKernelGGL((real_colsum<DT, D>), grid, dim3(256), 0, st, w);
-        hipLaunchKernelGGL(head_mean_accumulate, dim3((a.seq + 255) / 256, a.batch), dim3(256), 0, st, a.colsum,
-                           a.importance, a.hq, a.seq);
+        hipLaunchKernelGGL(head_mean_accumulate, dim3((a.seq + kHeadMeanThreads - 1) / kHeadMeanThreads, a.batch),
+                           dim3(kHeadMeanThreads), 0, st, a.colsum, a.importance, a.hq, a.seq);
     }
     hipLaunchKernelGGL((vt_slots_kernel<D>), dim3(s64 / 64, a.batch * a.hkv), dim3(256), 0, st,
                        static_cast<const uint16_t*>(v), vt, a.seq, s64);
