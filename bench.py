@@ -498,10 +498,12 @@ def entropy_stage(ck, cv, torch):
     c3_sample = len(z.compress(sample, 3))
     fp16_bytes = 2 * sum(c.scales.numel() * c.head_dim for c in list(ck) + list(cv))
     del dk, dv
+    rans = rans_full_stream(ck, cv, fp16_bytes, torch)
     temporal = temporal_codec_stage(ck[0], torch)
     v = z.version()
     return {
         "temporal_codec": temporal,
+        "gpu_rans_full_stream": rans,
         "gpu_delta": {"ms": round(delta_ms, 3), "bytes_read": n_in, "bytes_written": n_out,
                       "gbs": round((n_in + n_out) / (delta_ms * 1e-3) / 1e9, 1),
                       "kernel": "int8_codes_kernel (delta) over 80 layers x K, V packed codes"},
@@ -518,6 +520,42 @@ def entropy_stage(ck, cv, torch):
                               "sample": "first 8 MiB of layer 0's key delta stream", "host_threads": 1},
         "libzstd": f"{v // 10000}.{v // 100 % 100}.{v % 100}",
     }
+
+
+def rans_full_stream(ck, cv, fp16_bytes, torch):
+    """The GPU entropy coder over the whole C2 code stream: one NQR1 rANS stream
+    per layer and role (K3 codes at levels 8, V2 at levels 4, int8 2p, no token
+    delta), encoded and then decoded on the device; every stream is checked to
+    decode to its codes.  Wall time over the 160 calls, each including its
+    host-side frequency table."""
+    from nexusquant_amd.codec import codes_int8
+    from nexusquant_amd.entropy import rans_decode, rans_encode
+    ik, iv = codes_int8(ck), codes_int8(cv)
+    jobs = [(c, 8) for c in ik] + [(c, 4) for c in iv]
+    warm = rans_encode(ik[0], 8)
+    rans_decode(warm)
+    del warm
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    streams = [rans_encode(c, lv) for c, lv in jobs]
+    torch.cuda.synchronize()
+    enc_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    back = [rans_decode(st) for st in streams]
+    torch.cuda.synchronize()
+    dec_s = time.perf_counter() - t0
+    lossless = all(torch.equal(b, c) for b, (c, _) in zip(back, jobs))
+    n_sym = sum(c.numel() for c, _ in jobs)
+    nbytes = sum(st.nbytes() for st in streams)
+    del back, streams, ik, iv, jobs
+    return {"streams": 2 * len(ck), "symbols": n_sym, "compressed_bytes": nbytes,
+            "bits_per_symbol": round(8.0 * nbytes / n_sym, 4),
+            "ratio_vs_int8": round(n_sym / nbytes, 3), "ratio_vs_fp16_kv": round(fp16_bytes / nbytes, 3),
+            "encode_ms": round(enc_s * 1e3, 2), "decode_ms": round(dec_s * 1e3, 2),
+            "encode_gsym_s": round(n_sym / enc_s / 1e9, 1), "decode_gsym_s": round(n_sym / dec_s / 1e9, 1),
+            "lossless": lossless,
+            "note": "int8 2p codes, one stream per layer and role; wall time including each call's "
+                    "host-side frequency table; sizes without the row scales, as the zstd entries"}
 
 
 def temporal_codec_stage(code0, torch, reps=20):
