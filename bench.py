@@ -523,39 +523,48 @@ def entropy_stage(ck, cv, torch):
 
 
 def rans_full_stream(ck, cv, fp16_bytes, torch):
-    """The GPU entropy coder over the whole C2 code stream: one NQR1 rANS stream
-    per layer and role (K3 codes at levels 8, V2 at levels 4, int8 2p, no token
-    delta), encoded and then decoded on the device; every stream is checked to
-    decode to its codes.  Wall time over the 160 calls, each including its
-    host-side frequency table."""
+    """The GPU entropy coder over the whole C2 code stream (K3 codes at levels 8,
+    V2 at levels 4, int8 2p, no token delta), encoded and then decoded on the
+    device, each stream checked to decode to its codes, in two layouts: one
+    NQR1 stream per layer and role (160 streams of 134M symbols, 65536 chains
+    each), and one stream per role over all 80 layers (2 streams, 5.2M chains
+    each, one frequency table per role).  Wall time over the calls, each
+    including its host-side frequency table."""
     from nexusquant_amd.codec import codes_int8
     from nexusquant_amd.entropy import rans_decode, rans_encode
     ik, iv = codes_int8(ck), codes_int8(cv)
-    jobs = [(c, 8) for c in ik] + [(c, 4) for c in iv]
     warm = rans_encode(ik[0], 8)
     rans_decode(warm)
     del warm
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    streams = [rans_encode(c, lv) for c, lv in jobs]
-    torch.cuda.synchronize()
-    enc_s = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    back = [rans_decode(st) for st in streams]
-    torch.cuda.synchronize()
-    dec_s = time.perf_counter() - t0
-    lossless = all(torch.equal(b, c) for b, (c, _) in zip(back, jobs))
-    n_sym = sum(c.numel() for c, _ in jobs)
-    nbytes = sum(st.nbytes() for st in streams)
-    del back, streams, ik, iv, jobs
-    return {"streams": 2 * len(ck), "symbols": n_sym, "compressed_bytes": nbytes,
-            "bits_per_symbol": round(8.0 * nbytes / n_sym, 4),
-            "ratio_vs_int8": round(n_sym / nbytes, 3), "ratio_vs_fp16_kv": round(fp16_bytes / nbytes, 3),
-            "encode_ms": round(enc_s * 1e3, 2), "decode_ms": round(dec_s * 1e3, 2),
-            "encode_gsym_s": round(n_sym / enc_s / 1e9, 1), "decode_gsym_s": round(n_sym / dec_s / 1e9, 1),
-            "lossless": lossless,
-            "note": "int8 2p codes, one stream per layer and role; wall time including each call's "
-                    "host-side frequency table; sizes without the row scales, as the zstd entries"}
+
+    def run(jobs):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        streams = [rans_encode(c, lv) for c, lv in jobs]
+        torch.cuda.synchronize()
+        enc_s = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        back = [rans_decode(st) for st in streams]
+        torch.cuda.synchronize()
+        dec_s = time.perf_counter() - t0
+        lossless = all(torch.equal(b, c) for b, (c, _) in zip(back, jobs))
+        n_sym = sum(c.numel() for c, _ in jobs)
+        nbytes = sum(st.nbytes() for st in streams)
+        return {"streams": len(jobs), "symbols": n_sym, "compressed_bytes": nbytes,
+                "bits_per_symbol": round(8.0 * nbytes / n_sym, 4),
+                "ratio_vs_int8": round(n_sym / nbytes, 3), "ratio_vs_fp16_kv": round(fp16_bytes / nbytes, 3),
+                "encode_ms": round(enc_s * 1e3, 2), "decode_ms": round(dec_s * 1e3, 2),
+                "encode_gsym_s": round(n_sym / enc_s / 1e9, 1), "decode_gsym_s": round(n_sym / dec_s / 1e9, 1),
+                "lossless": lossless}
+
+    per_layer = run([(c, 8) for c in ik] + [(c, 4) for c in iv])
+    whole_k, whole_v = torch.cat([c.reshape(-1) for c in ik]), torch.cat([c.reshape(-1) for c in iv])
+    del ik, iv
+    per_role = run([(whole_k, 8), (whole_v, 4)])
+    del whole_k, whole_v
+    return {"per_layer": per_layer, "per_role": per_role,
+            "note": "int8 2p codes; wall time including each call's host-side frequency table; sizes "
+                    "without the row scales, as the zstd entries"}
 
 
 def temporal_codec_stage(code0, torch, reps=20):

@@ -315,7 +315,8 @@ int nq_merge_values(const nq_merge_desc* desc, void* stream);
  * on its own from the initial state, so chunk k's words equal the reference
  * encoder's output for that chunk's symbols.
  *   nq_rans_histogram: hist[2 levels + 1] += counts of c + levels (uint32,
- *     caller-zeroed); codes 16-byte aligned.
+ *     caller-zeroed); codes 16-byte aligned; at most 2^32 - 1 codes per call,
+ *     so that no bin wraps (count a longer stream in pieces).
  *   nq_rans_encode: per chunk, words right-aligned in scratch
  *     (nq_rans_scratch_words(n, chunk) uint16), their counts in n_words
  *     [n_chunks], and offset [n_chunks + 1] = exclusive scan of the counts;

@@ -476,6 +476,9 @@ extern "C" int nq_rans_histogram(const int8_t* codes, int64_t n, int32_t levels,
     NQ_CHECK_ARG(levels == 2 || levels == 4 || levels == 8 || levels == 16,
                  "nq_rans_histogram: levels must be 2, 4, 8 or 16 (got %d)", levels);
     NQ_CHECK_ARG(n >= 0 && (n == 0 || (codes && hist)), "nq_rans_histogram: bad arguments");
+    NQ_CHECK_ARG(n <= (int64_t)0xffffffffll,
+                 "nq_rans_histogram: %lld codes in one call; the uint32 bins take at most 2^32 - 1 (count in pieces)",
+                 (long long)n);
     NQ_CHECK_ARG(((uintptr_t)codes & 15) == 0, "nq_rans_histogram: codes must be 16-byte aligned");
     if (n == 0) return NQ_OK;
     int64_t blocks = (n + 256 * 16 - 1) / (256 * 16);

@@ -127,15 +127,27 @@ def _stream(dev) -> ctypes.c_void_p:
     return ctypes.c_void_p(_lib.current_stream_handle(dev))
 
 
+# codes per histogram call: the kernel's bins are 32-bit, read here as int32,
+# so every piece keeps each bin below 2^31; the pieces are summed in int64
+_HIST_PIECE = 1 << 30
+
+
 def _code_counts(flat: torch.Tensor, levels: int) -> np.ndarray:
-    """Histogram of c + levels over the 2 * levels + 1 codes (device pass)."""
+    """Histogram of c + levels over the 2 * levels + 1 codes (device passes).
+
+    flat is 16-byte aligned; so is every piece, at multiples of 2^30 codes."""
     lib = _lib.load()
     dev = flat.device
-    hist = torch.zeros(2 * levels + 1, dtype=torch.int32, device=dev)
+    n = flat.numel()
+    total = torch.zeros(2 * levels + 1, dtype=torch.int64, device=dev)
     with torch.cuda.device(dev):
-        _lib.check(lib.nq_rans_histogram(_addr(flat), flat.numel(), levels, _addr(hist), _stream(dev)),
-                   "nq_rans_histogram")
-    return hist.cpu().numpy().astype(np.int64)
+        for start in range(0, n, _HIST_PIECE):
+            piece = flat[start:start + _HIST_PIECE]
+            hist = torch.zeros(2 * levels + 1, dtype=torch.int32, device=dev)
+            _lib.check(lib.nq_rans_histogram(_addr(piece), piece.numel(), levels, _addr(hist), _stream(dev)),
+                       "nq_rans_histogram")
+            total += hist.to(torch.int64)
+    return total.cpu().numpy()
 
 
 def rans_encode(codes: torch.Tensor, levels: int, chunk: int = DEFAULT_CHUNK,

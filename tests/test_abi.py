@@ -114,3 +114,6 @@ def test_grid_limits_are_checked_on_the_host_without_a_gpu():
     assert b"bad geometry" in lib.nq_last_error()
     assert lib.nq_nibble_unpack(dummy, 1 << 41, 64, 128, dummy, None) == -1
     assert b"bad geometry" in lib.nq_last_error()
+    # the rANS histogram's bins are uint32: one call takes at most 2^32 - 1 codes
+    assert lib.nq_rans_histogram(ctypes.c_void_p(4096), 1 << 32, 4, dummy, None) == -1
+    assert b"2^32 - 1" in lib.nq_last_error()

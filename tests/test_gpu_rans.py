@@ -83,3 +83,25 @@ def test_skewed_streams_roundtrip_and_chunk_words(case):
     for k in sorted({0, 1, 5, len(offs) - 2}):
         want = R.rans_encode(sym[k * chunk:(k + 1) * chunk], st.freq)
         assert np.array_equal(words[offs[k]:offs[k + 1]], np.array(want, np.uint16))
+
+
+def test_stream_longer_than_2_31_codes_roundtrips():
+    """One stream of 2.5e9 codes whose most frequent code passes 2^31: its
+    histogram is counted in pieces, so the frequency table (and the stream)
+    stays right.  Every code is checked after the round trip."""
+    from nexusquant_amd.entropy import _code_counts, rans_decode, rans_encode
+    print("[gpu] rans stream of 2.5e9 codes", flush=True)
+    n, levels = 2_500_000_000, 4
+    g = torch.Generator(device=DEV).manual_seed(9)
+    u = torch.rand(n, device=DEV, generator=g)
+    codes = torch.zeros(n, dtype=torch.int8, device=DEV)
+    codes[u < 0.04] = 2
+    codes[u > 0.96] = -2
+    codes[(u > 0.5) & (u < 0.51)] = 4
+    del u
+    counts = _code_counts(codes, levels)
+    assert counts.sum() == n and counts[levels] > (1 << 31)
+    assert counts[levels + 2] == int((codes == 2).sum()) and counts[levels + 4] == int((codes == 4).sum())
+    st = rans_encode(codes, levels)
+    back = rans_decode(st)
+    assert torch.equal(back, codes)
