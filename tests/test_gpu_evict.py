@@ -523,3 +523,22 @@ def test_scoring_forward_fused_attention_matches_model_attention(dtype):
         fused = real_importance(model, ids)
         plain = real_importance(model, ids, fused_attention=False)
     assert torch.allclose(fused, plain, rtol=2e-3, atol=1e-5), (fused - plain).abs().max()
+
+
+def test_keykey_scorer_and_keep_mask_at_a_c2_length_context():
+    # 131072 tokens (C2's context): the scorer's splits and the keep mask's
+    # eight 16384-position windows, against the oracle
+    from nexusquant_amd.ops import keep_mask, score_keykey
+    print("[gpu] key-key scorer + keep mask at s=131072", flush=True)
+    s = 131072
+    g = torch.Generator().manual_seed(11)
+    k = torch.randn(1, 8, s, 128, generator=g).half()
+    imp = score_keykey(k.to(DEV), 32).cpu()
+    ref = T.score_keykey(k, 32)
+    assert ((imp - ref).abs() / ref.abs().clamp_min(1e-12)).max().item() < 1e-4
+    prot = [7, s // 2, s - 40]
+    keep, kept, n_kept = keep_mask(imp.to(DEV), 0.4, 32, protected_positions=prot)
+    want = T.build_keep_mask(imp, s, 0.4, 32, protected_positions=prot)
+    assert torch.equal(keep.cpu().bool(), want)
+    pos = want[0].nonzero(as_tuple=True)[0].to(torch.int32)
+    assert int(n_kept[0]) == pos.numel() and torch.equal(kept[0, :pos.numel()].cpu(), pos)
