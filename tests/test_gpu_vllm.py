@@ -244,9 +244,9 @@ def test_paged_forward_head_dims_and_value_ranges(d, group, qdt, vmul):
 
 @pytest.mark.parametrize("d,group,qdt", [(128, 8, torch.float16), (64, 2, torch.bfloat16), (256, 4, torch.float32)])
 def test_paged_forward_rows_of_many_chunks(d, group, qdt):
-    """Rows of 66 chunks (33.6K tokens): the combine takes 32-coordinate slices
-    with 32 chunk groups (rows of fewer than 64 chunks on average take a whole
-    head per workgroup, the case of the tests above)."""
+    """Rows of 66 chunks (33.6K tokens): each of the combine's 32 thread groups
+    sums more than one chunk (rows of fewer than 32 chunks, the case of the
+    tests above, give each group at most one)."""
     from nexusquant_amd.vllm_backend import NexusQuantKVCompressor, NexusQuantPagedAttention
     print(f"[gpu] paged forward, 66 chunks per row, d={d} group={group} {qdt}", flush=True)
     kv, base = 1, 500000.0
@@ -265,6 +265,31 @@ def test_paged_forward_rows_of_many_chunks(d, group, qdt):
     torch.cuda.synchronize()
     ref = _oracle_forward(cache, query, tables, ctx, base, group)
     _close_fp16(out.float().cpu().numpy(), ref.float().numpy(), bf16=qdt == torch.bfloat16)
+
+
+def test_paged_forward_at_a_1m_token_context():
+    """One row of 1,048,573 tokens in 1024-token pages (2048 chunks, pages larger
+    than a chunk): the combine's groups each sum 64 chunks."""
+    from nexusquant_amd.vllm_backend import NexusQuantKVCompressor, NexusQuantPagedAttention
+    print("[gpu] paged forward, 1M-token context", flush=True)
+    kv, d, base, group, size, n_pages = 1, 128, 500000.0, 8, 1024, 1024
+    comp = NexusQuantKVCompressor(head_dim=d, bits=2, rope_base=base)
+    attn = NexusQuantPagedAttention(comp)
+    gen = torch.Generator().manual_seed(5)
+    work = []
+    for i in range(n_pages):
+        k = (torch.randn(kv, size, d, generator=gen) * 2).to(torch.float16)
+        v = (torch.randn(kv, size, d, generator=gen) * 0.5).to(torch.float16)
+        work.append((k.to(DEV), v.to(DEV), torch.arange(size, dtype=torch.int32) + size * i))
+    cache = dict(enumerate(comp.compress_pages(work)))
+    del work
+    tables = [list(range(n_pages))]
+    ctx = [size * n_pages - 3]
+    query = torch.randn(1, kv * group, d, generator=gen).half()
+    out = attn.forward(query.to(DEV), cache, cache, tables, torch.tensor(ctx))
+    torch.cuda.synchronize()
+    ref = _oracle_forward(cache, query, tables, ctx, base, group)
+    _close_fp16(out.float().cpu().numpy(), ref.float().numpy())
 
 
 def test_paged_plan_reuse_across_queries():
