@@ -230,6 +230,28 @@ def test_c2_shaped_layer_subsample_bitexact():
     assert torch.isfinite(rk[0]).all() and torch.isfinite(rv[0]).all()
 
 
+def test_keys_at_a_1m_token_context_bitexact():
+    """Keys at positions up to 2^20 - 1 (RoPE base 5e5, angles up to ~1e6 rad); rows subsampled."""
+    print("[gpu] keys at 1M positions", flush=True)
+    ops = _ops()
+    n = 1 << 20
+    g = torch.Generator(device=DEV).manual_seed(7)
+    k = torch.randn(1, 2, n, 128, device=DEV, generator=g).to(torch.bfloat16)
+    rk, ck = ops.quantize_tensors([k], is_key=True, levels=8, rope_base=500000.0, codes=True)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(4)
+    heads = rng.integers(0, 2, 256)
+    toks = np.sort(rng.choice(n, 256, replace=False))
+    toks[-1] = n - 1
+    cs, sn = T.rope_cos_sin(torch.arange(n, dtype=torch.float32), 128, 500000.0)
+    hi = torch.from_numpy(heads).to(DEV)
+    ti = torch.from_numpy(toks).to(DEV)
+    c, s_ = cs.numpy()[toks], sn.numpy()[toks]
+    ref = S.quant_rows(k[0, hi, ti].float().cpu().numpy(), 8, cos_in=c, sin_in=s_, cos_out=c, sin_out=s_)
+    assert_same_fp16(rk[0][0, hi, ti].cpu().numpy(), ref["recon"])
+    assert np.array_equal(ck[0].scales[0, hi, ti].cpu().numpy(), ref["scale"])
+
+
 def _assert_rows_within_tolerance(got_t, ref):
     """North-star tolerance on fp16 outputs: near-tie code flips move a row by
     ~10 % and stay under 1e-4 of the 8-groups (at least one allowed); the other
