@@ -105,7 +105,7 @@ def test_merge_eviction_pipeline_matches_reference_fixture(golden):
 
 @pytest.mark.parametrize("dtype,d,s,h,b", [(torch.float16, 128, 3000, 4, 2), (torch.bfloat16, 96, 700, 2, 3),
                                            (torch.float32, 64, 1100, 3, 1), (torch.float16, 256, 500, 2, 1),
-                                           (torch.float16, 128, 40, 24, 2)])
+                                           (torch.float16, 128, 40, 24, 2), (torch.float16, 128, 32768, 2, 1)])
 def test_merge_values_match_oracle(dtype, d, s, h, b):
     from nexusquant_amd.ops import keep_mask
     print(f"[gpu] merge {dtype} d={d} s={s} h={h} b={b}", flush=True)
