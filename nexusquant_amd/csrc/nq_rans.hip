@@ -9,6 +9,8 @@
 //
 // Symbols: with half-integer points present (has_half) s = c + L (alphabet
 // 2L + 1), otherwise s = c/2 + L/2 (alphabet L + 1) (entropy_coder.py:35-75).
+#include <algorithm>
+
 #include "nq_common.h"
 
 namespace nq {
@@ -255,17 +257,36 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(RansArgs a) {
     a.n_words[ch] = (uint32_t)(end - out) + nbuf;
 }
 
-// copy each chunk's right-aligned words to its compacted offset; one wave per chunk
+// copy each chunk's right-aligned words to its compacted offset: a wave per
+// chunk, the waves striding over the chunks (a chunk is a few hundred words, so
+// a wave per chunk of a long stream spent its time being dispatched)
+constexpr uint32_t kCompactBlocks = 16384;
+constexpr int kCompactUnroll = 16;  // words per lane per piece: 1024 a wave, a chunk of 4096 codes at ~3 bits
+
 __global__ __launch_bounds__(256) void rans_compact_kernel(const uint16_t* scratch, const uint32_t* n_words,
                                                            const uint64_t* offset, int64_t n_chunks, int chunk,
                                                            uint16_t* words) {
-    const int64_t ch = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (ch >= n_chunks) return;
     const int lane = threadIdx.x & 63;
-    const uint32_t nw = n_words[ch];
-    const uint16_t* src = scratch + (ch + 1) * rans_stride(chunk) - nw;
-    uint16_t* dst = words + offset[ch];
-    for (uint32_t i = lane; i < nw; i += 64) dst[i] = src[i];
+    for (int64_t ch = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); ch < n_chunks; ch += (int64_t)gridDim.x * 4) {
+        const uint32_t nw = n_words[ch];
+        const uint16_t* src = scratch + (ch + 1) * rans_stride(chunk) - nw;
+        uint16_t* dst = words + offset[ch];
+        // all of a piece's loads go out before its stores: a chunk costs one
+        // memory latency, not one per 64 words
+        for (uint32_t b = 0; b < nw; b += 64 * kCompactUnroll) {
+            uint16_t v[kCompactUnroll];
+#pragma unroll
+            for (int j = 0; j < kCompactUnroll; ++j) {
+                const uint32_t i = b + lane + 64 * j;
+                v[j] = i < nw ? src[i] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < kCompactUnroll; ++j) {
+                const uint32_t i = b + lane + 64 * j;
+                if (i < nw) dst[i] = v[j];
+            }
+        }
+    }
 }
 
 // One lane per chunk, one wave per block.  Two 4096-entry LDS tables map a
@@ -425,47 +446,109 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(RansArgs a) {
 // exclusive scan of n_words into offset[0..n_chunks]: one block; per pass
 // every thread sums 32 consecutive counts, one block-wide scan of the 1024
 // sums, then every thread writes its 32 offsets
-__global__ __launch_bounds__(1024) void rans_scan_kernel(const uint32_t* n_words, int64_t n_chunks, uint64_t* offset) {
-    __shared__ uint64_t s[1024];
-    constexpr int kPer = 32;
+// Chunk offsets = exclusive prefix sums of the word counts, in three launches
+// over segments of kScanSeg counts.  No workspace: a segment's total, and then
+// its base, live in offset[first chunk of the segment] until the last pass
+// reads that slot and overwrites it with the chunk's own offset.
+constexpr int kScanPer = 32;                                  // counts per thread
+constexpr int64_t kScanSeg = 1024 * (int64_t)kScanPer;        // counts per segment (one block)
+
+// inclusive scan of one value per thread of a 1024-thread block; *total gets
+// the block's sum.  Uses lds[0 .. 32].
+__device__ __forceinline__ uint64_t block_incl_scan(uint64_t v, uint64_t* lds, uint64_t* total) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    uint64_t x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) lds[wave] = x;
+    __syncthreads();
+    if (t < 16) {
+        const uint64_t w = lds[t];
+        uint64_t r = w;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const uint64_t y = __shfl_up(r, o, 64);
+            if (t >= o) r += y;
+        }
+        lds[16 + t] = r - w;
+        if (t == 15) lds[32] = r;
+    }
+    __syncthreads();
+    const uint64_t res = x + lds[16 + wave];
+    *total = lds[32];
+    __syncthreads();
+    return res;
+}
+
+// pass 1: each segment's total into offset[its first chunk]
+__global__ __launch_bounds__(1024) void rans_seg_sum_kernel(const uint32_t* n_words, int64_t n_chunks,
+                                                            uint64_t* offset) {
+    __shared__ uint64_t lds[33];
+    const int64_t seg0 = (int64_t)blockIdx.x * kScanSeg;
+    uint64_t sum = 0;
+#pragma unroll 4
+    for (int k = 0; k < kScanPer; ++k) {
+        const int64_t i = seg0 + (int64_t)k * 1024 + threadIdx.x;
+        if (i < n_chunks) sum += n_words[i];
+    }
+    uint64_t tot;
+    (void)block_incl_scan(sum, lds, &tot);
+    if (threadIdx.x == 0) offset[seg0] = tot;
+}
+
+// pass 2 (one block): the segment totals into exclusive bases, in place, and
+// the stream's word count into offset[n_chunks]
+__global__ __launch_bounds__(1024) void rans_seg_base_kernel(int64_t n_chunks, uint64_t* offset) {
+    __shared__ uint64_t lds[33];
+    const int64_t n_seg = (n_chunks + kScanSeg - 1) / kScanSeg;
     uint64_t carry = 0;
-    for (int64_t b0 = 0; b0 < n_chunks; b0 += 1024 * kPer) {
-        const int64_t i0 = b0 + (int64_t)threadIdx.x * kPer;
-        uint32_t cnt[kPer];
-        if (i0 + kPer <= n_chunks && ((reinterpret_cast<uintptr_t>(n_words + i0) & 15) == 0)) {
-#pragma unroll
-            for (int k = 0; k < kPer; k += 4) {
-                const uint4 v = *reinterpret_cast<const uint4*>(n_words + i0 + k);
-                cnt[k] = v.x;
-                cnt[k + 1] = v.y;
-                cnt[k + 2] = v.z;
-                cnt[k + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < kPer; ++k) cnt[k] = i0 + k < n_chunks ? n_words[i0 + k] : 0u;
-        }
-        uint64_t sum = 0;
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) sum += cnt[k];
-        s[threadIdx.x] = sum;
-        __syncthreads();
-        for (int o = 1; o < 1024; o <<= 1) {
-            const uint64_t add = threadIdx.x >= (unsigned)o ? s[threadIdx.x - o] : 0;
-            __syncthreads();
-            s[threadIdx.x] += add;
-            __syncthreads();
-        }
-        uint64_t run = carry + s[threadIdx.x] - sum;  // exclusive prefix of this thread's first count
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            if (i0 + k < n_chunks) offset[i0 + k] = run;
-            run += cnt[k];
-        }
-        carry += s[1023];
-        __syncthreads();
+    for (int64_t b0 = 0; b0 < n_seg; b0 += 1024) {
+        const int64_t b = b0 + threadIdx.x;
+        const uint64_t v = b < n_seg ? offset[b * kScanSeg] : 0;
+        uint64_t tot;
+        const uint64_t incl = block_incl_scan(v, lds, &tot);
+        if (b < n_seg) offset[b * kScanSeg] = carry + incl - v;
+        carry += tot;
     }
     if (threadIdx.x == 0) offset[n_chunks] = carry;
+}
+
+// pass 3: thread t of segment b writes the offsets of its 32 consecutive chunks
+__global__ __launch_bounds__(1024) void rans_seg_scan_kernel(const uint32_t* n_words, int64_t n_chunks,
+                                                             uint64_t* offset) {
+    __shared__ uint64_t lds[33];
+    __shared__ uint64_t s_base;
+    const int64_t seg0 = (int64_t)blockIdx.x * kScanSeg;
+    if (threadIdx.x == 0) s_base = offset[seg0];
+    const int64_t i0 = seg0 + (int64_t)threadIdx.x * kScanPer;
+    uint32_t cnt[kScanPer];
+    if (i0 + kScanPer <= n_chunks && ((reinterpret_cast<uintptr_t>(n_words + i0) & 15) == 0)) {
+#pragma unroll
+        for (int k = 0; k < kScanPer; k += 4) {
+            const uint4 v = *reinterpret_cast<const uint4*>(n_words + i0 + k);
+            cnt[k] = v.x;
+            cnt[k + 1] = v.y;
+            cnt[k + 2] = v.z;
+            cnt[k + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kScanPer; ++k) cnt[k] = i0 + k < n_chunks ? n_words[i0 + k] : 0u;
+    }
+    uint64_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) sum += cnt[k];
+    uint64_t tot;
+    const uint64_t incl = block_incl_scan(sum, lds, &tot);  // its barriers order s_base before the writes
+    uint64_t run = s_base + incl - sum;
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) {
+        if (i0 + k < n_chunks) offset[i0 + k] = run;
+        run += cnt[k];
+    }
 }
 
 }  // namespace nq
@@ -528,9 +611,13 @@ extern "C" int nq_rans_encode(const int8_t* codes, int64_t n, int32_t levels, in
         a.has_half = has_half;
         a.alphabet = alphabet;
         hipLaunchKernelGGL(rans_encode_kernel, dim3((uint32_t)((n_chunks + 63) / 64)), dim3(64), 0, s, a);
-        NQ_CHECK_HIP(hipGetLastError());
+        const uint32_t n_seg = (uint32_t)((n_chunks + kScanSeg - 1) / kScanSeg);
+        hipLaunchKernelGGL(rans_seg_sum_kernel, dim3(n_seg), dim3(1024), 0, s, n_words, n_chunks, offset);
+        hipLaunchKernelGGL(rans_seg_base_kernel, dim3(1), dim3(1024), 0, s, n_chunks, offset);
+        hipLaunchKernelGGL(rans_seg_scan_kernel, dim3(n_seg), dim3(1024), 0, s, n_words, n_chunks, offset);
+    } else if (offset) {
+        hipLaunchKernelGGL(rans_seg_base_kernel, dim3(1), dim3(1024), 0, s, n_chunks, offset);  // offset[0] = 0
     }
-    hipLaunchKernelGGL(rans_scan_kernel, dim3(1), dim3(1024), 0, s, n_words, n_chunks, offset);
     NQ_CHECK_HIP(hipGetLastError());
     return NQ_OK;
 }
@@ -541,9 +628,9 @@ extern "C" int nq_rans_compact(const uint16_t* scratch, const uint32_t* n_words,
     const int64_t n_chunks = (n + chunk - 1) / chunk;
     if (n_chunks == 0) return NQ_OK;
     NQ_CHECK_ARG(scratch && n_words && offset && words, "nq_rans_compact: NULL buffer");
-    NQ_CHECK_ARG((n_chunks + 3) / 4 < (1ll << 31), "nq_rans_compact: too many chunks");
-    hipLaunchKernelGGL(rans_compact_kernel, dim3((uint32_t)((n_chunks + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
-                       scratch, n_words, offset, n_chunks, chunk, words);
+    const uint32_t blocks = (uint32_t)std::min<int64_t>((n_chunks + 3) / 4, kCompactBlocks);
+    hipLaunchKernelGGL(rans_compact_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, scratch, n_words,
+                       offset, n_chunks, chunk, words);
     NQ_CHECK_HIP(hipGetLastError());
     return NQ_OK;
 }

@@ -85,6 +85,37 @@ def test_skewed_streams_roundtrip_and_chunk_words(case):
         assert np.array_equal(words[offs[k]:offs[k + 1]], np.array(want, np.uint16))
 
 
+@pytest.mark.parametrize("has_half", [False, True])
+def test_offsets_across_scan_segments_and_compact_strides(has_half):
+    """99,304 chunks of 32 codes, the last one ragged: the chunk offsets are
+    scanned in segments of 32,768 chunks and the compaction's waves stride
+    over 65,536 chunks at a time, so chunks on either side of each boundary
+    are checked against the restated encoder, and the offsets against the
+    cumulative sums of those per-chunk word counts."""
+    from nexusquant_amd.entropy import rans_decode, rans_encode
+    print(f"[gpu] rans offsets across scan segments has_half={has_half}", flush=True)
+    chunk, levels, n_chunks = 32, 8, 3 * 32768 + 1000
+    n = n_chunks * chunk - 7
+    rng = np.random.default_rng(11)
+    vals = np.arange(-levels, levels + 1) if has_half else np.arange(-levels, levels + 1, 2)
+    p = np.exp(-0.5 * (vals / 3.0) ** 2)
+    c = rng.choice(vals, n, p=p / p.sum()).astype(np.int8)
+    codes = torch.from_numpy(c).to(DEV)
+    st = rans_encode(codes, levels, chunk=chunk)
+    assert st.has_half == has_half
+    assert torch.equal(rans_decode(st), codes)
+    sym = (c.astype(np.int32) + levels) if has_half else (c.astype(np.int32) // 2 + levels // 2)
+    offs = st.offsets.cpu().numpy()
+    words = st.words.cpu().numpy().view(np.uint16)
+    assert len(offs) == n_chunks + 1 and offs[0] == 0 and offs[-1] == words.size
+    ks = sorted({0, 1, 32767, 32768, 32769, 65535, 65536, 65537, 98303, 98304, n_chunks - 2, n_chunks - 1})
+    for k in ks:
+        want = R.rans_encode(sym[k * chunk:(k + 1) * chunk], st.freq)
+        assert np.array_equal(words[offs[k]:offs[k + 1]], np.array(want, np.uint16)), k
+    lens = np.array([len(R.rans_encode(sym[k * chunk:(k + 1) * chunk], st.freq)) for k in range(32760, 32780)])
+    assert np.array_equal(np.diff(offs[32760:32781]), lens)
+
+
 def test_stream_longer_than_2_31_codes_roundtrips():
     """One stream of 2.5e9 codes whose most frequent code passes 2^31: its
     histogram is counted in pieces, so the frequency table (and the stream)
