@@ -321,7 +321,8 @@ int nq_merge_values(const nq_merge_desc* desc, void* stream);
  *     (nq_rans_scratch_words(n, chunk) uint16), their counts in n_words
  *     [n_chunks], and offset [n_chunks + 1] = exclusive scan of the counts;
  *     codes 16-byte and scratch 8-byte aligned.
- *   nq_rans_compact: words[offset[k] ..] = chunk k's words.
+ *   nq_rans_compact: words[offset[k] ..] = chunk k's words; scratch 8-byte
+ *     and words 4-byte aligned.
  *   nq_rans_decode: codes from the compacted words and offsets; words 8-byte
  *     and codes 16-byte aligned.
  * freq: uint16 [alphabet], summing to 4096, nonzero for every symbol present.

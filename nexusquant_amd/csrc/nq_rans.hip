@@ -257,34 +257,81 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(RansArgs a) {
     a.n_words[ch] = (uint32_t)(end - out) + nbuf;
 }
 
-// copy each chunk's right-aligned words to its compacted offset: a wave per
-// chunk, the waves striding over the chunks (a chunk is a few hundred words, so
-// a wave per chunk of a long stream spent its time being dispatched)
-constexpr uint32_t kCompactBlocks = 16384;
-constexpr int kCompactUnroll = 16;  // words per lane per piece: 1024 a wave, a chunk of 4096 codes at ~3 bits
+// copy each chunk's right-aligned words to its compacted offset.
+// A wave takes `group` (<= 64) consecutive chunks: its lanes load their word
+// counts and offsets at once and the wave copies the chunks one after the
+// other, reading each chunk's count and offset back from its lane, so the
+// metadata costs one memory latency per group, not per chunk.  The waves
+// stride over the groups with a grid the chip holds at once; the host shrinks
+// the group until there are enough groups to give every wave one.
+// Stores are 4-byte: a word before the destination's first 4-byte boundary and
+// a last odd word go alone; the pairs between them come from aligned 4-byte
+// source loads, funnel-shifted when source and destination differ in parity.
+// Scratch rows span a multiple of 4 words, so every load stays in its row:
+// with an odd source start the pair loads begin one word early, at or after the
+// row's start, and the word count past the head is then odd, so they end on
+// the row's last word.
+constexpr uint32_t kCompactBlocks = 2048;  // 256 CUs x 8 blocks of 4 waves
+constexpr int64_t kCompactWaves = 4 * (int64_t)kCompactBlocks;
+constexpr int kCompactUnroll = 8;          // pairs per lane per piece: 1024 words, a 4096-code chunk at ~3 bits
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t x, int lane) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)x, lane);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), lane);
+    return (uint64_t)hi << 32 | lo;
+}
 
 __global__ __launch_bounds__(256) void rans_compact_kernel(const uint16_t* scratch, const uint32_t* n_words,
                                                            const uint64_t* offset, int64_t n_chunks, int chunk,
-                                                           uint16_t* words) {
+                                                           int group, uint16_t* words) {
     const int lane = threadIdx.x & 63;
-    for (int64_t ch = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); ch < n_chunks; ch += (int64_t)gridDim.x * 4) {
-        const uint32_t nw = n_words[ch];
-        const uint16_t* src = scratch + (ch + 1) * rans_stride(chunk) - nw;
-        uint16_t* dst = words + offset[ch];
-        // all of a piece's loads go out before its stores: a chunk costs one
-        // memory latency, not one per 64 words
-        for (uint32_t b = 0; b < nw; b += 64 * kCompactUnroll) {
-            uint16_t v[kCompactUnroll];
+    const int64_t n_groups = (n_chunks + group - 1) / group;
+    const int64_t stride = rans_stride(chunk);
+    for (int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); g < n_groups; g += (int64_t)gridDim.x * 4) {
+        const int64_t c0 = g * group;
+        uint32_t my_nw = 0;
+        uint64_t my_off = 0;
+        if (lane < group && c0 + lane < n_chunks) {
+            my_nw = n_words[c0 + lane];
+            my_off = offset[c0 + lane];
+        }
+        // wait here, once per group: past the loop's stores the compiler
+        // can no longer count these loads and would wait on every store
+        __builtin_amdgcn_s_waitcnt(0);
+        const int cnt = (int)(n_chunks - c0 < group ? n_chunks - c0 : group);
+        for (int c = 0; c < cnt; ++c) {
+            const uint32_t nw = (uint32_t)__builtin_amdgcn_readlane((int)my_nw, c);
+            if (nw == 0) continue;
+            const uint64_t dst0 = readlane_u64(my_off, c);
+            const int64_t src0 = (c0 + c + 1) * stride - nw;
+            const uint32_t head = (uint32_t)(dst0 & 1);
+            const uint32_t pairs = (nw - head) >> 1;
+            const uint32_t tail = (nw - head) & 1;
+            // lane 0 holds the head word, lane 1 the tail word (both loaded by
+            // every lane, to go out with the pair loads; stored after them)
+            const uint16_t edge = scratch[lane == 0 ? src0 : src0 + nw - 1];
+            const int64_t q0 = src0 + head;  // source word of the first pair
+            const uint32_t sh = (uint32_t)(q0 & 1);
+            const uint32_t* s32 = reinterpret_cast<const uint32_t*>(scratch + (q0 & ~(int64_t)1));
+            uint32_t* d32 = reinterpret_cast<uint32_t*>(words + dst0 + head);
+            // all of a piece's loads go out before its stores; loads past the
+            // last pair repeat the last pair's, so none is conditional
+            for (uint32_t b = 0; b < pairs; b += 64 * kCompactUnroll) {
+                uint32_t v[kCompactUnroll];
 #pragma unroll
-            for (int j = 0; j < kCompactUnroll; ++j) {
-                const uint32_t i = b + lane + 64 * j;
-                v[j] = i < nw ? src[i] : 0;
-            }
+                for (int j = 0; j < kCompactUnroll; ++j) {
+                    const uint32_t i = min(b + lane + 64 * j, pairs - 1);
+                    const uint32_t lo = s32[i], hi = s32[i + sh];
+                    v[j] = __builtin_amdgcn_alignbit(hi, lo, 16 * sh);  // lo when sh = 0
+                }
 #pragma unroll
-            for (int j = 0; j < kCompactUnroll; ++j) {
-                const uint32_t i = b + lane + 64 * j;
-                if (i < nw) dst[i] = v[j];
+                for (int j = 0; j < kCompactUnroll; ++j) {
+                    const uint32_t i = b + lane + 64 * j;
+                    if (i < pairs) d32[i] = v[j];
+                }
             }
+            if (lane == 0 && head) words[dst0] = edge;
+            if (lane == 1 && tail) words[dst0 + nw - 1] = edge;
         }
     }
 }
@@ -628,9 +675,14 @@ extern "C" int nq_rans_compact(const uint16_t* scratch, const uint32_t* n_words,
     const int64_t n_chunks = (n + chunk - 1) / chunk;
     if (n_chunks == 0) return NQ_OK;
     NQ_CHECK_ARG(scratch && n_words && offset && words, "nq_rans_compact: NULL buffer");
-    const uint32_t blocks = (uint32_t)std::min<int64_t>((n_chunks + 3) / 4, kCompactBlocks);
+    NQ_CHECK_ARG(((uintptr_t)scratch & 7) == 0 && ((uintptr_t)words & 3) == 0,
+                 "nq_rans_compact: scratch must be 8-byte and words 4-byte aligned");
+    int group = 64;
+    while (group > 1 && n_chunks < group * kCompactWaves) group >>= 1;
+    const int64_t n_groups = (n_chunks + group - 1) / group;
+    const uint32_t blocks = (uint32_t)std::min<int64_t>((n_groups + 3) / 4, kCompactBlocks);
     hipLaunchKernelGGL(rans_compact_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, scratch, n_words,
-                       offset, n_chunks, chunk, words);
+                       offset, n_chunks, chunk, group, words);
     NQ_CHECK_HIP(hipGetLastError());
     return NQ_OK;
 }
