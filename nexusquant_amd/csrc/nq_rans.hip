@@ -497,7 +497,7 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(RansArgs a) {
 // over segments of kScanSeg counts.  No workspace: a segment's total, and then
 // its base, live in offset[first chunk of the segment] until the last pass
 // reads that slot and overwrites it with the chunk's own offset.
-constexpr int kScanPer = 32;                                  // counts per thread
+constexpr int kScanPer = 4;                                   // counts per thread
 constexpr int64_t kScanSeg = 1024 * (int64_t)kScanPer;        // counts per segment (one block)
 
 // inclusive scan of one value per thread of a 1024-thread block; *total gets

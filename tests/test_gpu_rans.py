@@ -88,9 +88,10 @@ def test_skewed_streams_roundtrip_and_chunk_words(case):
 @pytest.mark.parametrize("has_half", [False, True])
 def test_offsets_across_scan_segments_and_compact_strides(has_half):
     """99,304 chunks of 32 codes, the last one ragged: the chunk offsets are
-    scanned in segments of 32,768 chunks and the compaction's waves stride
-    over 65,536 chunks at a time, so chunks on either side of each boundary
-    are checked against the restated encoder, and the offsets against the
+    scanned in segments of 4,096 chunks, and the compaction's waves take the
+    chunks in groups of 8 and stride over them, most waves coming back for a
+    second group; chunks on either side of segment boundaries and at both
+    ends are checked against the restated encoder, and offsets against the
     cumulative sums of those per-chunk word counts."""
     from nexusquant_amd.entropy import rans_decode, rans_encode
     print(f"[gpu] rans offsets across scan segments has_half={has_half}", flush=True)
@@ -108,12 +109,13 @@ def test_offsets_across_scan_segments_and_compact_strides(has_half):
     offs = st.offsets.cpu().numpy()
     words = st.words.cpu().numpy().view(np.uint16)
     assert len(offs) == n_chunks + 1 and offs[0] == 0 and offs[-1] == words.size
-    ks = sorted({0, 1, 32767, 32768, 32769, 65535, 65536, 65537, 98303, 98304, n_chunks - 2, n_chunks - 1})
+    ks = sorted({0, 1, 4095, 4096, 4097, 32767, 32768, 65535, 65536, 65537, 98303, 98304, n_chunks - 2, n_chunks - 1})
     for k in ks:
         want = R.rans_encode(sym[k * chunk:(k + 1) * chunk], st.freq)
         assert np.array_equal(words[offs[k]:offs[k + 1]], np.array(want, np.uint16)), k
-    lens = np.array([len(R.rans_encode(sym[k * chunk:(k + 1) * chunk], st.freq)) for k in range(32760, 32780)])
-    assert np.array_equal(np.diff(offs[32760:32781]), lens)
+    for k0 in (4090, 98300):
+        lens = [len(R.rans_encode(sym[k * chunk:(k + 1) * chunk], st.freq)) for k in range(k0, k0 + 12)]
+        assert np.array_equal(np.diff(offs[k0:k0 + 13]), np.array(lens)), k0
 
 
 def test_stream_longer_than_2_31_codes_roundtrips():
