@@ -64,6 +64,73 @@ __global__ __launch_bounds__(256) void rans_hist_kernel(const int8_t* codes, int
     }
 }
 
+// Histogram for alphabets of at most 9 bins (levels 2 and 4), without an
+// atomic per code: each lane counts in one 64-bit register, 7 bits per bin
+// (bin b at bit 7b), adding 1 << 7b per code, and empties it into 32-bit
+// totals every 64 codes, before any 7-bit counter can pass 127.  The totals are
+// summed across each wave and added once per wave and bin.  The per-code
+// kernel above was bound by the LDS atomic rate, not by HBM.
+constexpr int kHistSmallBins = 9;
+constexpr int kHistSmallLoads = 4;  // 16-byte loads per lane in flight: 64 codes between flushes
+                                    // (8 in flight, flushed every 4, measured the same)
+
+__global__ __launch_bounds__(256) void rans_hist_small_kernel(const int8_t* codes, int64_t n, int L, uint32_t* hist) {
+    __shared__ uint32_t h[kHistSmallBins];
+    if (threadIdx.x < kHistSmallBins) h[threadIdx.x] = 0;
+    __syncthreads();
+    uint32_t tot[kHistSmallBins];
+#pragma unroll
+    for (int b = 0; b < kHistSmallBins; ++b) tot[b] = 0;
+    const int bias = 7 * L;
+    auto count16 = [&](const uint4& w, uint64_t& acc) {
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                int c = (int)(ws[k] << (24 - 8 * j)) >> 24;
+                c = min(max(c, -L), L);  // codes outside [-L, L] are not valid input
+                acc += 1ull << (7 * c + bias);
+            }
+    };
+    auto flush = [&](uint64_t acc) {
+#pragma unroll
+        for (int b = 0; b < kHistSmallBins; ++b) tot[b] += (uint32_t)(acc >> (7 * b)) & 127u;
+    };
+    const uint4* const v = reinterpret_cast<const uint4*>(codes);
+    const int64_t n16 = n / 16;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (; g + (kHistSmallLoads - 1) * stride < n16; g += kHistSmallLoads * stride) {
+        uint4 w[kHistSmallLoads];
+#pragma unroll
+        for (int u = 0; u < kHistSmallLoads; ++u) w[u] = v[g + u * stride];
+        uint64_t acc = 0;
+#pragma unroll
+        for (int u = 0; u < kHistSmallLoads; ++u) count16(w[u], acc);
+        flush(acc);
+    }
+    for (; g < n16; g += stride) {
+        uint64_t acc = 0;
+        count16(v[g], acc);
+        flush(acc);
+    }
+    // the last n % 16 codes, one each to the first threads of block 0
+    if (blockIdx.x == 0 && threadIdx.x < n - 16 * n16) {
+        const int c = min(max((int)codes[16 * n16 + threadIdx.x], -L), L);
+        flush(1ull << (7 * c + bias));
+    }
+#pragma unroll
+    for (int b = 0; b < kHistSmallBins; ++b) {
+        uint32_t t = tot[b];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+        if ((threadIdx.x & 63) == 0 && t) atomicAdd(&h[b], t);
+    }
+    __syncthreads();
+    if (threadIdx.x <= 2 * L && h[threadIdx.x]) atomicAdd(&hist[threadIdx.x], h[threadIdx.x]);
+}
+
 struct RansArgs {
     const int8_t* codes;
     int8_t* out_codes;
@@ -613,8 +680,12 @@ extern "C" int nq_rans_histogram(const int8_t* codes, int64_t n, int32_t levels,
     if (n == 0) return NQ_OK;
     int64_t blocks = (n + 256 * 16 - 1) / (256 * 16);
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(rans_hist_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, codes, n, levels,
-                       hist);
+    if (2 * levels + 1 <= kHistSmallBins)
+        hipLaunchKernelGGL(rans_hist_small_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, codes, n,
+                           levels, hist);
+    else
+        hipLaunchKernelGGL(rans_hist_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, codes, n,
+                           levels, hist);
     NQ_CHECK_HIP(hipGetLastError());
     return NQ_OK;
 }

@@ -118,6 +118,24 @@ def test_offsets_across_scan_segments_and_compact_strides(has_half):
         assert np.array_equal(np.diff(offs[k0:k0 + 13]), np.array(lens)), k0
 
 
+@pytest.mark.parametrize("levels", [2, 4, 8, 16])
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 4097, 1_000_003, 9 * (1 << 20) * 16 + 9])
+def test_histogram_equals_bincount(levels, n):
+    """The code histogram (levels 2 and 4 count in packed registers, 8 and 16
+    with LDS atomics) equals numpy's count of c + levels, at ragged lengths
+    including a remainder past the last 16-byte group and lengths whose
+    16-byte groups outnumber the grid's threads several times."""
+    from nexusquant_amd.entropy import _code_counts
+    print(f"[gpu] rans histogram L={levels} n={n}", flush=True)
+    rng = np.random.default_rng(n + levels)
+    c = rng.integers(-levels, levels + 1, n).astype(np.int8)
+    c[: min(n, 7)] = levels  # the extreme bins, at the head of the stream
+    c[-1] = -levels
+    got = _code_counts(torch.from_numpy(c).to(DEV), levels)
+    want = np.bincount(c.astype(np.int64) + levels, minlength=2 * levels + 1)
+    assert np.array_equal(np.asarray(got, np.int64), want)
+
+
 def test_stream_longer_than_2_31_codes_roundtrips():
     """One stream of 2.5e9 codes whose most frequent code passes 2^31: its
     histogram is counted in pieces, so the frequency table (and the stream)
