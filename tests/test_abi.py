@@ -117,3 +117,7 @@ def test_grid_limits_are_checked_on_the_host_without_a_gpu():
     # the rANS histogram's bins are uint32: one call takes at most 2^32 - 1 codes
     assert lib.nq_rans_histogram(ctypes.c_void_p(4096), 1 << 32, 4, dummy, None) == -1
     assert b"2^32 - 1" in lib.nq_last_error()
+    # the rANS compaction stores word pairs: words must be 4-byte aligned
+    odd = ctypes.c_void_p(4098)
+    assert lib.nq_rans_compact(dummy, dummy, dummy, 4096, 2048, odd, None) == -1
+    assert b"4-byte aligned" in lib.nq_last_error()
