@@ -326,9 +326,10 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(RansArgs a) {
 
 // copy each chunk's right-aligned words to its compacted offset.
 // A wave takes `group` (<= 64) consecutive chunks: its lanes load their word
-// counts and offsets at once and the wave copies the chunks one after the
-// other, reading each chunk's count and offset back from its lane, so the
-// metadata costs one memory latency per group, not per chunk.  The waves
+// counts and offsets, then their chunks' first and last words, and the wave
+// copies the chunks one after the other, reading each chunk's count, offset and
+// edge words back from its lane, so these cost two memory latencies per group,
+// and a chunk's copy waits only on its own pair loads.  The waves
 // stride over the groups with a grid the chip holds at once; the host shrinks
 // the group until there are enough groups to give every wave one.
 // Stores are 4-byte: a word before the destination's first 4-byte boundary and
@@ -362,6 +363,12 @@ __global__ __launch_bounds__(256) void rans_compact_kernel(const uint16_t* scrat
             my_nw = n_words[c0 + lane];
             my_off = offset[c0 + lane];
         }
+        // each lane's chunk's first and last words, for a lone head or tail store
+        uint32_t my_edge = 0;
+        if (my_nw) {
+            const int64_t s0 = (c0 + lane + 1) * stride - my_nw;
+            my_edge = (uint32_t)scratch[s0] | (uint32_t)scratch[s0 + my_nw - 1] << 16;
+        }
         // wait here, once per group: past the loop's stores the compiler
         // can no longer count these loads and would wait on every store
         __builtin_amdgcn_s_waitcnt(0);
@@ -374,9 +381,7 @@ __global__ __launch_bounds__(256) void rans_compact_kernel(const uint16_t* scrat
             const uint32_t head = (uint32_t)(dst0 & 1);
             const uint32_t pairs = (nw - head) >> 1;
             const uint32_t tail = (nw - head) & 1;
-            // lane 0 holds the head word, lane 1 the tail word (both loaded by
-            // every lane, to go out with the pair loads; stored after them)
-            const uint16_t edge = scratch[lane == 0 ? src0 : src0 + nw - 1];
+            const uint32_t edge = (uint32_t)__builtin_amdgcn_readlane((int)my_edge, c);
             const int64_t q0 = src0 + head;  // source word of the first pair
             const uint32_t sh = (uint32_t)(q0 & 1);
             const uint32_t* s32 = reinterpret_cast<const uint32_t*>(scratch + (q0 & ~(int64_t)1));
@@ -397,8 +402,8 @@ __global__ __launch_bounds__(256) void rans_compact_kernel(const uint16_t* scrat
                     if (i < pairs) d32[i] = v[j];
                 }
             }
-            if (lane == 0 && head) words[dst0] = edge;
-            if (lane == 1 && tail) words[dst0 + nw - 1] = edge;
+            if (lane == 0 && head) words[dst0] = (uint16_t)edge;
+            if (lane == 1 && tail) words[dst0 + nw - 1] = (uint16_t)(edge >> 16);
         }
     }
 }
