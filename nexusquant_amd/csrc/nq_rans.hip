@@ -428,11 +428,19 @@ constexpr int kRingStride = 34;  // dwords per lane: 64 words + 4 bytes, 8-byte 
 typedef uint16_t __attribute__((may_alias)) ring_word_t;
 typedef uint64_t __attribute__((may_alias)) ring_group_t;
 
-__global__ __launch_bounds__(64) void rans_decode_kernel(RansArgs a) {
+// W waves per block share the slot tables.  The tables and one wave's rings
+// take 20.6 KB and 8.7 KB of LDS, so one-wave blocks fit 5 to a CU; a long
+// stream's chains (more than the chip holds at once) run in blocks of 6 waves,
+// 2 to a CU, 12 waves in all.  A short stream keeps one wave per block, so its
+// few chains spread over every CU.
+constexpr int kDecodeWaves = 6;
+
+template <int W>
+__global__ __launch_bounds__(64 * W) void rans_decode_kernel(RansArgs a) {
     __shared__ uint32_t tab[kRansM];
     __shared__ uint8_t code_of[kRansM];
     __shared__ uint16_t cf[kRansMaxAlpha + 1];
-    __shared__ __attribute__((aligned(8))) uint32_t ring_all[64 * kRingStride];
+    __shared__ __attribute__((aligned(8))) uint32_t ring_all[64 * W * kRingStride];
     if (threadIdx.x == 0) {
         uint32_t acc = 0;
         for (int s = 0; s < a.alphabet; ++s) {
@@ -446,14 +454,14 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(RansArgs a) {
         const uint32_t lo = cf[s], hi = cf[s + 1] < kRansM ? cf[s + 1] : kRansM;
         const uint8_t code = (uint8_t)rans_code(s, a.L, a.has_half);
         const uint32_t f = hi > lo ? hi - lo : 1u;  // f <= 4096: 13 bits
-        for (uint32_t k = lo + threadIdx.x; k < hi; k += 64) {
+        for (uint32_t k = lo + threadIdx.x; k < hi; k += 64 * W) {
             tab[k] = f | ((k - lo) << 13);
             code_of[k] = code;
         }
     }
     __syncthreads();
-    const int64_t ch = (int64_t)blockIdx.x * 64 + threadIdx.x;
-    if (ch >= a.n_chunks) return;
+    const int64_t ch = (int64_t)blockIdx.x * (64 * W) + threadIdx.x;
+    if (ch >= a.n_chunks) return;  // no barrier follows
     const int64_t c0 = ch * a.chunk;
     const uint32_t n_sym = (uint32_t)((c0 + a.chunk < a.n ? c0 + a.chunk : a.n) - c0);
     const uint64_t w0 = a.offset[ch];
@@ -785,8 +793,13 @@ extern "C" int nq_rans_decode(const uint16_t* words, const uint64_t* offset, int
     a.L = levels;
     a.has_half = has_half;
     a.alphabet = alphabet;
-    hipLaunchKernelGGL(rans_decode_kernel, dim3((uint32_t)((n_chunks + 63) / 64)), dim3(64), 0,
-                       (hipStream_t)stream, a);
+    if (n_chunks >= (int64_t)64 * kDecodeWaves * 2 * 256)  // two blocks for each of 256 CUs
+        hipLaunchKernelGGL(rans_decode_kernel<kDecodeWaves>,
+                           dim3((uint32_t)((n_chunks + 64 * kDecodeWaves - 1) / (64 * kDecodeWaves))),
+                           dim3(64 * kDecodeWaves), 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL(rans_decode_kernel<1>, dim3((uint32_t)((n_chunks + 63) / 64)), dim3(64), 0,
+                           (hipStream_t)stream, a);
     NQ_CHECK_HIP(hipGetLastError());
     return NQ_OK;
 }

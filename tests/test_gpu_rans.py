@@ -85,17 +85,19 @@ def test_skewed_streams_roundtrip_and_chunk_words(case):
         assert np.array_equal(words[offs[k]:offs[k + 1]], np.array(want, np.uint16))
 
 
+@pytest.mark.parametrize("n_chunks", [3 * 32768 + 1000, 6 * 32768 + 1001])
 @pytest.mark.parametrize("has_half", [False, True])
-def test_offsets_across_scan_segments_and_compact_strides(has_half):
+def test_offsets_across_scan_segments_and_compact_strides(has_half, n_chunks):
     """99,304 chunks of 32 codes, the last one ragged: the chunk offsets are
     scanned in segments of 4,096 chunks, and the compaction's waves take the
     chunks in groups of 8 and stride over them, most waves coming back for a
     second group; chunks on either side of segment boundaries and at both
     ends are checked against the restated encoder, and offsets against the
-    cumulative sums of those per-chunk word counts."""
+    cumulative sums of those per-chunk word counts.  At 197,609 chunks the
+    decoder runs six waves per block, the last block partly empty."""
     from nexusquant_amd.entropy import rans_decode, rans_encode
-    print(f"[gpu] rans offsets across scan segments has_half={has_half}", flush=True)
-    chunk, levels, n_chunks = 32, 8, 3 * 32768 + 1000
+    print(f"[gpu] rans offsets across scan segments has_half={has_half} n_chunks={n_chunks}", flush=True)
+    chunk, levels = 32, 8
     n = n_chunks * chunk - 7
     rng = np.random.default_rng(11)
     vals = np.arange(-levels, levels + 1) if has_half else np.arange(-levels, levels + 1, 2)
