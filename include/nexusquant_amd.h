@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define NQ_ABI_VERSION 7
+#define NQ_ABI_VERSION 8
 
 /* status codes */
 #define NQ_OK 0
@@ -66,6 +66,16 @@ extern "C" {
  * and otherwise forms from rope_cos / rope_sin.  Either way the results are
  * identical; the precomputed tables save two operations per pair.
  *
+ * Row lists (mask eviction without work on evicted rows): with keep_mode
+ * NQ_KEEP_ZERO, a keep list and order != NULL (then n_kept != NULL, gather ==
+ * NULL, seq_out == seq_in), order[b*seq_in .. +seq_in) is a permutation of the
+ * row's positions with its n_kept[b] kept positions first, as nq_keep_mask
+ * writes kept_idx.  The kept positions are quantized and written at their own
+ * positions; the evicted ones are not read, and get the outputs a zeroed row
+ * has (recon 0, every symbol L/2, coset bits 0, scale 1e-8 * 2/L: the
+ * reference's amax clamp).  The outputs equal those of the same call without
+ * order, bit for bit, up to the sign of zero in recon.
+ *
  * Replaces (keep_mode 1 + 2): the soft-eviction loop   pipeline.py:1129-1183
  *
  * Replaces: NexusQuantQuantOnly.compress            pipeline.py:232-265
@@ -99,6 +109,8 @@ typedef struct nq_quant_desc {
     float reserved_f;
     const float* rope_sin_minus_cos;  /* optional, [rope_n_pos, head_dim/2]; NULL: formed in-kernel */
     const float* rope_cos_plus_sin;
+    const int32_t* order;   /* device [batch * seq_in] row list (kept first) or NULL */
+    const int32_t* n_kept;  /* device [batch]: kept entries at the head of each order row */
 } nq_quant_desc;
 
 int nq_quantize(const nq_quant_desc* desc, void* stream);
@@ -182,8 +194,10 @@ int nq_attention_real(const void* q, const void* k, const void* v, int32_t dtype
  * (ties at the k-th value keep the lowest positions), and protected_pos.
  * prefix = max(seq - sliding_window, 0) and k = min(n_keep, prefix - 1) are
  * computed by the caller exactly as the reference does (Python double).
- * Writes keep[batch, seq] (0/1), kept_idx[batch, seq] (ascending kept
- * positions, first n_kept[b] entries valid) and n_kept[batch].
+ * Writes keep[batch, seq] (0/1), kept_idx[batch, seq] and n_kept[batch]:
+ * row b of kept_idx holds its n_kept[b] kept positions ascending, then its
+ * evicted positions descending (a permutation of 0 .. seq-1, the row list
+ * nq_quantize takes as `order`).
  *
  * Replaces: NexusQuantEvict._build_keep_mask (topk + scatter)  pipeline.py:895-959
  *           keep_mask[0].nonzero() of the truncation path      pipeline.py:1319

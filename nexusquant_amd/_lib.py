@@ -14,7 +14,7 @@ from .build import LIB_PATH, source_hash
 
 NQ_F16, NQ_BF16, NQ_F32 = 0, 1, 2
 NQ_KEEP_ZERO, NQ_KEEP_WRITE_KEPT, NQ_KEEP_WRITE_EVICTED = 0, 1, 2
-ABI_VERSION = 7  # NQ_ABI_VERSION of the header these bindings mirror
+ABI_VERSION = 8  # NQ_ABI_VERSION of the header these bindings mirror
 _P = ctypes.c_void_p
 
 
@@ -31,6 +31,7 @@ class QuantDesc(ctypes.Structure):
         ("rope_n_pos", ctypes.c_int64),
         ("hadamard_scale", ctypes.c_float), ("reserved_f", ctypes.c_float),
         ("rope_sin_minus_cos", _P), ("rope_cos_plus_sin", _P),
+        ("order", _P), ("n_kept", _P),
     ]
 
 

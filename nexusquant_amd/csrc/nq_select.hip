@@ -14,7 +14,8 @@
 //     of threshold-equal keys ranks them, and keeps the first `want`.
 //  3. Protected positions are set in the window's LDS flags, which are then
 //     written out and compacted into the kept-index list with one more block
-//     scan.
+//     scan: kept positions ascending from the front, evicted positions
+//     descending from the back.
 // Ties at the threshold therefore keep the lowest positions; torch.topk leaves
 // their order unspecified.
 #include "nq_common.h"
@@ -65,7 +66,7 @@ __device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t* lds, uint32
 struct SelectArgs {
     const float* importance;  // [batch, seq]
     uint8_t* keep;            // [batch, seq]
-    int32_t* kept_idx;        // [batch, seq] ascending kept positions (rest untouched)
+    int32_t* kept_idx;        // [batch, seq] kept positions ascending, then evicted descending
     int32_t* n_kept;          // [batch]
     const int32_t* protected_pos;
     int32_t n_protected;
@@ -201,9 +202,15 @@ __global__ __launch_bounds__(kSelThreads) void keep_mask_kernel(SelectArgs a) {
         const uint32_t n_k = (uint32_t)__builtin_popcount(km);
         uint32_t k_tot;
         uint32_t out = kept_before + block_scan(n_k, scan_lds, &k_tot) - n_k;
+        // kept positions ascending from the front; an evicted position p has
+        // p - out evicted positions before it and goes to seq - 1 - (p - out),
+        // so the evicted ones fill the tail descending
 #pragma unroll
-        for (int j = 0; j < kPer; ++j)
-            if ((km >> j) & 1u) idx[out++] = p0 + j;
+        for (int j = 0; j < kPer; ++j) {
+            const int p = p0 + j;
+            if ((km >> j) & 1u) idx[out++] = p;
+            else if (p < a.seq) idx[a.seq - 1 - (p - (int)out)] = p;
+        }
         kept_before += k_tot;
     }
     if (t == 0) a.n_kept[row] = (int32_t)kept_before;

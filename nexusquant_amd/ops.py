@@ -160,6 +160,7 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
                      gather: Optional[torch.Tensor] = None, keep: Optional[torch.Tensor] = None,
                      keep_mode: int = _lib.NQ_KEEP_ZERO, recon_out: Optional[Sequence[torch.Tensor]] = None,
                      recon: bool = True, codes: bool = False, launch_events=None, merged_tables: bool = True,
+                     order: Optional[torch.Tensor] = None, n_kept: Optional[torch.Tensor] = None,
                      ) -> Tuple[Optional[List[torch.Tensor]], Optional[List[PackedCodes]]]:
     """Run the fused quantizer over same-shaped [b, h, s, d] tensors in one launch.
 
@@ -173,6 +174,10 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
     launch stream immediately around the kernel launch.
     merged_tables: pass the precomputed fl(sin - cos) / fl(cos + sin) tables for
             keys (False: the kernel forms them from cos / sin; same results).
+    order, n_kept: keep_mask()'s kept_idx [b, seq] (kept positions first, then
+            the evicted ones) and n_kept [b], with `keep` and keep_mode
+            NQ_KEEP_ZERO: only the kept rows are read and quantized; evicted rows
+            get the zero-row outputs directly.  Same results as without them.
     Returns (fp16 reconstructions or None, PackedCodes or None), one per tensor.
     """
     lib = _lib.load()
@@ -216,6 +221,15 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
         raise ValueError(f"unknown keep_mode {keep_mode}")
     if keep_mode != _lib.NQ_KEEP_ZERO and k is None:
         raise ValueError("keep_mode other than NQ_KEEP_ZERO needs a keep mask")
+    o = nk = None
+    if order is not None:
+        if k is None or keep_mode != _lib.NQ_KEEP_ZERO or g is not None or n_kept is None:
+            raise ValueError("a row list (order) takes a keep mask, n_kept, keep_mode NQ_KEEP_ZERO and no gather")
+        o = order.to(device=dev, dtype=torch.int32).contiguous()
+        nk = n_kept.to(device=dev, dtype=torch.int32).contiguous()
+        if tuple(o.shape) != (b, s) or tuple(nk.shape) != (b,):
+            raise ValueError(f"order must be [batch, seq] = {(b, s)} and n_kept [batch], got "
+                             f"{tuple(o.shape)} and {tuple(nk.shape)}")
     n = len(src)
     # one allocation per output kind; every tensor gets a contiguous slice
     recon_t = None
@@ -260,7 +274,7 @@ def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: i
         cosets=_addr(arrays["cosets"]), scales=_addr(arrays["scales"]),
         gather=_addr(g), keep=_addr(k), rope_cos=_addr(cos), rope_sin=_addr(sin),
         rope_n_pos=n_pos, hadamard_scale=hadamard_constant(D),
-        rope_sin_minus_cos=_addr(dm), rope_cos_plus_sin=_addr(dp))
+        rope_sin_minus_cos=_addr(dm), rope_cos_plus_sin=_addr(dp), order=_addr(o), n_kept=_addr(nk))
     with torch.cuda.device(dev):
         try:
             if launch_events is not None:
@@ -342,7 +356,10 @@ def keep_plan(seq: int, rate: float, sliding_window: int) -> Tuple[int, int]:
 
 def keep_mask(importance: torch.Tensor, rate: float, sliding_window: int = 32,
               protected_positions=None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(keep uint8 [b, s], kept_idx int32 [b, s], n_kept int32 [b]) on the device."""
+    """(keep uint8 [b, s], kept_idx int32 [b, s], n_kept int32 [b]) on the device.
+
+    Row b of kept_idx holds its n_kept[b] kept positions ascending, then its
+    evicted positions descending."""
     lib = _lib.load()
     _lib.require_device(importance, "importance")
     imp = importance.to(torch.float32).contiguous()

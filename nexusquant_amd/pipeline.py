@@ -311,11 +311,15 @@ class NexusQuantEvict:
             return self._score_importance_real(model, input_ids), k_score
         return self._score_importance(k_score), k_score
 
-    def _apply(self, past_key_values, n_layers: int, skip: set, *, keep=None, gather=None, soft=False):
+    def _apply(self, past_key_values, n_layers: int, skip: set, *, keep=None, gather=None, soft=False,
+               kept_idx=None, n_kept=None):
         """Quantize (or pass through at fp16) every layer with one mask / gather list.
 
         soft: kept rows at the layer's levels and evicted rows at levels 2, no row
-        zeroed (pipeline.py:1129-1183); protected layers pass through unmasked."""
+        zeroed (pipeline.py:1129-1183); protected layers pass through unmasked.
+        kept_idx / n_kept (keep_mask's row list): mask eviction reads and
+        quantizes only the kept rows of layers as long as the mask; evicted rows
+        get the zero-row outputs directly (the same results)."""
         todo: Dict[tuple, List[int]] = {}
         passthrough: Dict[tuple, List[int]] = {}
         for li in range(n_layers):
@@ -362,9 +366,12 @@ class NexusQuantEvict:
                 quantize_tensors(vs, is_key=False, levels=2, keep=kp, keep_mode=NQ_KEEP_WRITE_EVICTED,
                                  recon_out=v_out)
             else:
+                lst = {}
+                if kp is not None and gp is None and kept_idx is not None and key[0][2] == keep.shape[1]:
+                    lst = dict(order=kept_idx, n_kept=n_kept)
                 k_out, _ = quantize_tensors(ks, is_key=True, levels=kl, rope_base=self.rope_base,
-                                            rope_scaling=self.rope_scaling, gather=gp, keep=kp)
-                v_out, _ = quantize_tensors(vs, is_key=False, levels=vl, gather=gp, keep=kp)
+                                            rope_scaling=self.rope_scaling, gather=gp, keep=kp, **lst)
+                v_out, _ = quantize_tensors(vs, is_key=False, levels=vl, gather=gp, keep=kp, **lst)
             for i, li in enumerate(layers):
                 set_layer_kv(past_key_values, li, k_out[i], v_out[i])
 
@@ -398,7 +405,7 @@ class NexusQuantEvict:
             return past_key_values, torch.ones(b, seq, dtype=torch.float32, device=device)
         if self.merge_eviction:
             self._merge(past_key_values, n, seq, keep, kept_idx, n_kept, importance)
-        self._apply(past_key_values, n, skip, keep=keep)
+        self._apply(past_key_values, n, skip, keep=keep, kept_idx=kept_idx, n_kept=n_kept)
         return past_key_values, prefix_attention_mask
 
 

@@ -57,7 +57,7 @@ def test_struct_layout_matches_the_c_compiler(tmp_path, cname, pystruct):
 
 def test_abi_version_and_error_calls_need_no_gpu():
     lib = _lib.load()
-    assert lib.nq_abi_version() == _lib.ABI_VERSION == 7
+    assert lib.nq_abi_version() == _lib.ABI_VERSION == 8
     assert isinstance(lib.nq_last_error(), bytes)
 
 

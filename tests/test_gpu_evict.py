@@ -144,6 +144,9 @@ def test_keep_mask_matches_oracle(s, rate, sw):
         want = ref[bi].nonzero(as_tuple=True)[0].to(torch.int32)
         assert int(nk[bi]) == want.numel()
         assert torch.equal(kk[bi, :want.numel()], want)
+        # the tail lists the evicted positions, descending
+        gone = (~ref[bi]).nonzero(as_tuple=True)[0].to(torch.int32).flip(0)
+        assert torch.equal(kk[bi, want.numel():], gone)
 
 
 def test_keep_mask_ties_keep_lowest_positions_and_protected():
@@ -204,6 +207,7 @@ def test_keep_mask_ties_across_windows():
         pos = np.nonzero(want[bi])[0]
         assert int(nk[bi]) == pos.size
         assert np.array_equal(kk[bi, :pos.size].numpy(), pos.astype(np.int32))
+        assert np.array_equal(kk[bi, pos.size:].numpy(), np.nonzero(~want[bi])[0][::-1].astype(np.int32))
 
 
 def test_mask_eviction_matches_reference_fixture(golden):

@@ -141,6 +141,65 @@ def test_keep_mask_path_zeroes_rows_bitexact():
         assert np.all(sy[0][:, keep[0] == 0, :] == L // 2)
 
 
+LIST_CASES = [(128, 8, True, torch.float16, 2, 300), (128, 4, False, torch.bfloat16, 2, 300),
+              (64, 16, True, torch.float32, 1, 200), (96, 4, True, torch.float16, 2, 257),
+              (96, 2, False, torch.float16, 1, 130), (256, 4, True, torch.bfloat16, 1, 190),
+              (256, 16, False, torch.float16, 2, 129), (128, 2, True, torch.float16, 3, 64)]
+
+
+@pytest.mark.parametrize("d,L,key,dt,b,s", LIST_CASES)
+def test_row_list_mask_eviction_equals_zeroing(d, L, key, dt, b, s):
+    # nq_quantize with keep_mask's row list reads and quantizes only the kept
+    # rows and stores the zero-row outputs for the others: bit-exact with the
+    # plain keep path and with the C spec, for batch rows with different kept
+    # counts (kept counts on and off 64-row tile edges, fully evicted tiles)
+    from nexusquant_amd.ops import keep_mask
+    print(f"[gpu] row list d={d} L={L} key={key} {dt} b={b} s={s}", flush=True)
+    x = _inputs((b, 3, s, d), dt, seed=d + L + s, key=key)
+    g = torch.Generator().manual_seed(s)
+    imp = torch.rand(b, s, generator=g)
+    # protected positions overlap each row's top-k differently, so the rows'
+    # kept counts differ
+    prot = [p for p in range(3, 200, 7) if p < s]
+    keep, kept, n_kept = keep_mask(imp.to(DEV), 0.7, 8, protected_positions=prot)
+    kw = dict(rope_base=10000.0) if key else {}
+    rec_l, cd_l = gpu_quant(x.to(DEV), L, key, keep=keep, order=kept, n_kept=n_kept, **kw)
+    rec_z, cd_z = gpu_quant(x.to(DEV), L, key, keep=keep, **kw)
+    assert_same_fp16(rec_l.cpu().numpy(), rec_z.cpu().numpy())
+    for f in ("syms", "cosets", "scales"):
+        assert torch.equal(getattr(cd_l, f), getattr(cd_z, f)), f
+    ref = spec_tensor(x.float().numpy(), L, key, 10000.0, keep=keep.cpu().numpy())
+    assert_bitexact(rec_l, cd_l, ref, L)
+    r = rec_l.cpu().float().numpy()
+    km = keep.cpu().numpy()
+    for bi in range(b):
+        assert np.all(r[bi][:, km[bi] == 0, :] == 0)
+
+
+def test_row_list_pipeline_matches_plain_keep_path():
+    # NexusQuantEvict's mask path (row list) against the same layers through the
+    # plain keep path, C3-like shape at a small size
+    import nexusquant_amd as nq
+    from nexusquant_amd.ops import quantize_tensors
+    g = torch.Generator().manual_seed(4)
+    ks = [_inputs((4, 8, 512, 128), torch.float16, seed=40 + i).to(DEV) for i in range(3)]
+    vs = [(torch.randn(4, 8, 512, 128, generator=g) * 0.5).half().to(DEV) for _ in range(3)]
+
+    class Cache:
+        pass
+
+    c = Cache()
+    c.key_cache, c.value_cache = list(ks), list(vs)
+    comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.25, rope_base=10000.0)
+    _, mask = comp.compress(c)
+    keep = mask.to(torch.uint8)
+    rk, _ = quantize_tensors(ks, is_key=True, levels=8, rope_base=10000.0, keep=keep)
+    rv, _ = quantize_tensors(vs, is_key=False, levels=4, keep=keep)
+    for li in range(3):
+        assert_same_fp16(c.key_cache[li].cpu().numpy(), rk[li].cpu().numpy())
+        assert_same_fp16(c.value_cache[li].cpu().numpy(), rv[li].cpu().numpy())
+
+
 def test_zero_and_tiny_rows():
     print("[gpu] zero rows", flush=True)
     x = torch.zeros(1, 1, 64, 128)
