@@ -152,22 +152,32 @@ int nq_score_keykey_noalloc(const void* keys, int32_t dtype, int32_t batch, int3
 
 /*
  * Real-attention importance of one layer, accumulated: importance[b, j] +=
- * mean over q_heads of sum_{i >= j} p[b, h, i, j], with
- * p = round(softmax_fp32(round(round(q . k) * scaling))) under the causal
+ * mean over q_heads of sum_i p[b, h, i, j], with
+ * p = round(softmax_fp32(f(round(round(q . k) * scaling)))) under the causal
  * mask, round = rounding to the model dtype (fp16/bf16; none for fp32) as
  * transformers' eager attention does; query head h reads key head
  * h / (q_heads / kv_heads).  q [batch, q_heads, seq, head_dim],
- * k [batch, kv_heads, seq, head_dim], both post-RoPE.  workspace: at least
+ * k [batch, kv_heads, seq, head_dim], both post-RoPE.
+ * sliding_window > 0: query i sees keys i - sliding_window < j <= i only
+ * (transformers' sliding_window_overlay); 0: plain causal.
+ * logit_map (fp16/bf16 only; NULL: f = identity): 65536 entries, the bits of
+ * f(x) at the model-dtype bits of x, for an elementwise logit transform f that
+ * is monotone non-decreasing -- Gemma-2's soft-capping
+ * round(round(tanh(round(x / cap))) * cap), built by the host with the
+ * framework's own ops.  workspace: at least
  * nq_score_real_workspace(batch, q_heads, seq) bytes (caller owned).
  *
  * Replaces: NexusQuantEvict._score_importance_real   pipeline.py:784-836
  *           (eager_attention_forward + repeat_kv, transformers 5.15.0
- *            models/llama/modeling_llama.py:179-213)
+ *            models/llama/modeling_llama.py:179-213; soft-capping
+ *            models/gemma2/modeling_gemma2.py:184-215; the sliding-window
+ *            mask masking_utils.py:92-101)
  */
 int64_t nq_score_real_workspace(int32_t batch, int32_t q_heads, int32_t seq);
 int nq_score_real(const void* q, const void* k, int32_t dtype, int32_t batch, int32_t q_heads,
-                  int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, float* importance,
-                  void* workspace, int64_t workspace_bytes, void* stream);
+                  int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, int32_t sliding_window,
+                  const uint16_t* logit_map, float* importance, void* workspace, int64_t workspace_bytes,
+                  void* stream);
 
 /*
  * The scoring pass's attention output without materialising P: the row
@@ -176,7 +186,8 @@ int nq_score_real(const void* q, const void* k, int32_t dtype, int32_t batch, in
  * (round_T(round_T(Q K^T) * scaling))), causal, query head h reading kv head
  * h / (q_heads / kv_heads) -- eager_attention_forward's arithmetic, P V summed
  * in fp32 on the matrix cores.  fp16 / bf16, head_dim 64 or 128, 16-byte aligned
- * tensors; v [batch, kv_heads, seq, head_dim].  workspace:
+ * tensors; v [batch, kv_heads, seq, head_dim]; sliding_window and logit_map as
+ * for nq_score_real.  workspace:
  * nq_attention_real_workspace bytes (row statistics, column sums and V
  * transposed with the keys of each 32-key block in the accumulator's order).
  *
@@ -185,8 +196,9 @@ int nq_score_real(const void* q, const void* k, int32_t dtype, int32_t batch, in
  */
 int64_t nq_attention_real_workspace(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t seq, int32_t head_dim);
 int nq_attention_real(const void* q, const void* k, const void* v, int32_t dtype, int32_t batch, int32_t q_heads,
-                      int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, float* importance, void* out,
-                      void* workspace, int64_t workspace_bytes, void* stream);
+                      int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, int32_t sliding_window,
+                      const uint16_t* logit_map, float* importance, void* out, void* workspace,
+                      int64_t workspace_bytes, void* stream);
 
 /*
  * Keep mask from importance[batch, seq] (fp32): position 0, the last

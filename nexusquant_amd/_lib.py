@@ -107,9 +107,11 @@ SIGNATURES = {
     "nq_delta_encode": ([_P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "nq_delta_decode": ([_P, _P, _I32, _I32, _I32, _I32, _P], ctypes.c_int),
     "nq_score_real_workspace": ([_I32, _I32, _I32], _I64),
-    "nq_score_real": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
+    "nq_score_real": ([_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P, _P, _P, _I64, _P],
+                      ctypes.c_int),
     "nq_attention_real_workspace": ([_I32, _I32, _I32, _I32, _I32], _I64),
-    "nq_attention_real": ([_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _P, _P, _I64, _P], ctypes.c_int),
+    "nq_attention_real": ([_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P, _P, _P, _P, _I64, _P],
+                          ctypes.c_int),
     "nq_rans_histogram": ([_P, _I64, _I32, _P, _P], ctypes.c_int),
     "nq_rans_scratch_words": ([_I64, _I32], _I64),
     "nq_rans_encode": ([_P, _I64, _I32, _I32, _P, _I32, _I32, _P, _P, _P, _P], ctypes.c_int),

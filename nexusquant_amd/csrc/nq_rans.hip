@@ -708,7 +708,10 @@ static int rans_check(const char* who, int64_t n, int32_t chunk, int32_t levels,
     NQ_CHECK_ARG(levels == 2 || levels == 4 || levels == 8 || levels == 16, "%s: levels must be 2, 4, 8 or 16", who);
     NQ_CHECK_ARG(alphabet == (has_half ? 2 * levels + 1 : levels + 1), "%s: alphabet %d does not match levels %d%s",
                  who, alphabet, levels, has_half ? " (half-integer codes)" : "");
-    NQ_CHECK_ARG(chunk >= 1 && chunk <= (1 << 24), "%s: chunk %d out of range", who, chunk);
+    // chunk is at most INT32_MAX by its type: the encoder's and decoder's
+    // per-chunk counters (word counts, ring positions) are 32-bit unsigned and
+    // stay below 2^32 for chunk + 64 words
+    NQ_CHECK_ARG(chunk >= 1, "%s: chunk %d out of range", who, chunk);
     NQ_CHECK_ARG(n >= 0 && freq != nullptr, "%s: bad arguments", who);
     return NQ_OK;
 }

@@ -84,7 +84,17 @@ struct RealArgs {
     int32_t seq, hq, hkv, batch;
     float scaling;
     int32_t n_items, per_xcd;  // 128-row blocks x batch*hq; blocks per XCD range
+    // sliding window (transformers' sliding_window_overlay): query i sees keys
+    // j with i - window < j <= i; kNoWindow when the mask is plain causal
+    int32_t window;
+    // MAP instantiations: logit_map[bits of w] = bits of the model's
+    // elementwise logit transform of w (soft-capping), 65536 entries in the
+    // model dtype; monotone non-decreasing, so a row's maximum maps to the
+    // maximum of the mapped logits
+    const uint16_t* logit_map;
 };
+
+constexpr int32_t kNoWindow = 0x3fffffff;  // wider than any sequence, and 2 * it fits an int
 
 // Block -> work item: consecutive block ids go round-robin to the 8 XCDs, so
 // block 8k + x takes item x * per_xcd + k and each XCD walks one contiguous
@@ -140,7 +150,7 @@ __global__ __launch_bounds__(64) void real_sweep(RealArgs a) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const int i = qt * 32 + acc_row(j, lane);
-                if (key <= i && i < a.seq) {
+                if (key <= i && i - key < a.window && i < a.seq) {
                     const float x = round_model<DT>(round_model<DT>(acc[j]) * a.scaling);
                     if constexpr (SWEEP == 0) m[j] = __builtin_fmaxf(m[j], x);
                     else z[j] += expf(x - m[j]);
@@ -165,7 +175,7 @@ __global__ __launch_bounds__(64) void real_sweep(RealArgs a) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const int i = qt * 32 + acc_row(j, lane);
-                if (key <= i && i < a.seq) {
+                if (key <= i && i - key < a.window && i < a.seq) {
                     const float x = round_model<DT>(round_model<DT>(acc[j]) * a.scaling);
                     const float p = expf(x - a.row_max[stat + i]) / a.row_sum[stat + i];
                     col += round_model<DT>(p);
@@ -352,11 +362,25 @@ __device__ __forceinline__ void row_operand(const uint16_t* base, int row, int s
 // x = round_T(round_T(logit) * scaling), both roundings kept (the empty asm
 // stops the fp32 product and the second rounding from fusing into one
 // mixed-precision instruction that would round once).
+// Bits of a model-dtype value held exactly in an fp32 register, and back.
 template <int DT>
-__device__ __forceinline__ float eager_logit(float acc, float scaling) {
+__device__ __forceinline__ uint32_t model_bits(float x) {
+    if constexpr (DT == NQ_F16) return (uint32_t)__builtin_bit_cast(uint16_t, (__fp16)x);  // exact
+    else return __builtin_bit_cast(uint32_t, x) >> 16;                                     // exact
+}
+template <int DT>
+__device__ __forceinline__ float from_model_bits(uint32_t h) {
+    if constexpr (DT == NQ_F16) return (float)__builtin_bit_cast(__fp16, (uint16_t)h);
+    else return __builtin_bit_cast(float, h << 16);
+}
+
+template <int DT, bool MAP = false>
+__device__ __forceinline__ float eager_logit(float acc, float scaling, const uint16_t* map = nullptr) {
     float t = round_model<DT>(acc) * scaling;
     asm("" : "+v"(t));
-    return round_model<DT>(t);
+    const float x = round_model<DT>(t);
+    if constexpr (MAP) return from_model_bits<DT>(map[model_bits<DT>(x)]);
+    return x;
 }
 
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
@@ -374,21 +398,31 @@ __device__ __forceinline__ f16x2v cvt_pk_f16(float lo, float hi) {
 
 // exp2 arguments of two logits: round_T(round_T(acc) * scaling) * log2(e) + nm,
 // the roundings done on packed pairs.
-template <int DT>
+// MAP: the pair goes through the logit map (two table reads) before the exp2
+// arguments are formed.
+template <int DT, bool MAP = false>
 __device__ __forceinline__ void exp_args2(float a0, float a1, float scaling, float nm0, float nm1, float& o0,
-                                          float& o1) {
+                                          float& o1, const uint16_t* map = nullptr) {
     if constexpr (DT == NQ_F16) {
         const f16x2v h = cvt_pk_f16(a0, a1);
         float t0 = __builtin_fmaf((float)h.x, scaling, 0.0f), t1 = __builtin_fmaf((float)h.y, scaling, 0.0f);
         asm("" : "+v"(t0), "+v"(t1));
-        const f16x2v x = cvt_pk_f16(t0, t1);
+        f16x2v x = cvt_pk_f16(t0, t1);
+        if constexpr (MAP) {
+            const uint32_t bits = __builtin_bit_cast(uint32_t, x);
+            x = __builtin_bit_cast(f16x2v, (uint32_t)map[bits & 0xffffu] | ((uint32_t)map[bits >> 16] << 16));
+        }
         o0 = __builtin_fmaf((float)x.x, kLog2e, nm0);
         o1 = __builtin_fmaf((float)x.y, kLog2e, nm1);
     } else {
         const bf16x2v h = {(__bf16)a0, (__bf16)a1};
         float t0 = (float)h.x * scaling, t1 = (float)h.y * scaling;
         asm("" : "+v"(t0), "+v"(t1));
-        const bf16x2v x = {(__bf16)t0, (__bf16)t1};
+        bf16x2v x = {(__bf16)t0, (__bf16)t1};
+        if constexpr (MAP) {
+            const uint32_t bits = __builtin_bit_cast(uint32_t, x);
+            x = __builtin_bit_cast(bf16x2v, (uint32_t)map[bits & 0xffffu] | ((uint32_t)map[bits >> 16] << 16));
+        }
         o0 = __builtin_fmaf((float)x.x, kLog2e, nm0);
         o1 = __builtin_fmaf((float)x.y, kLog2e, nm1);
     }
@@ -406,7 +440,8 @@ __device__ __forceinline__ uint32_t round_pair(float p0, float p1) {
 }
 
 // Online row statistics of one lane (one query): fold the valid logits of a
-// tile (raw dot products acc[j], j in [0, 16) x NT tiles) into (mt, m, nm, z):
+// tile (raw dot products acc[j], j in [0, 16) x NT tiles; MASKED: only keys
+// lo < acc_row(j) <= hi of the tile) into (mt, m, nm, z):
 // mt the largest raw logit so far; m <= mt the reference the sum is kept
 // against, nm = -round_T(round_T(m) * scaling) * log2(e); z = sum of
 // exp2(x * log2(e) + nm) over the logits folded in.  The reference moves (and
@@ -414,18 +449,19 @@ __device__ __forceinline__ uint32_t round_pair(float p0, float p1) {
 // logit distance whose exp2 argument is 32: every term stays below 2^32, the
 // sum far from overflow, and most tiles skip the rescale.  The row's true
 // maximum is applied once at the end.
-template <int DT, int NT, bool MASKED>
-__device__ __forceinline__ void row_fold(const f32x16 (&acc)[NT], float scaling, float span, int diag_key, int g,
-                                         float& mt, float& m, float& nm, float& z) {
+template <int DT, int NT, bool MASKED, bool MAP = false, bool WIN = false>
+__device__ __forceinline__ void row_fold(const f32x16 (&acc)[NT], float scaling, float span, int lo, int hi, int g,
+                                         float& mt, float& m, float& nm, float& z, const uint16_t* map = nullptr) {
+    auto valid = [&](int j) { return (!WIN || lo < acc_row(j, 32 * g)) && acc_row(j, 32 * g) <= hi; };
     float tm = -__builtin_inff();
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-            tm = fmaxf(tm, (!MASKED || acc_row(j, 32 * g) <= diag_key) ? acc[t][j] : -__builtin_inff());
+            tm = fmaxf(tm, (!MASKED || valid(j)) ? acc[t][j] : -__builtin_inff());
     mt = fmaxf(mt, tm);
     if (tm > m + span) {  // per lane: move the reference to this tile's maximum, rescale the sum
-        const float nm_new = -(eager_logit<DT>(tm, scaling) * kLog2e);
+        const float nm_new = -(eager_logit<DT, MAP>(tm, scaling, map) * kLog2e);
         z = m == -__builtin_inff() ? 0.0f : z * __builtin_amdgcn_exp2f(nm_new - nm);
         m = tm;
         nm = nm_new;
@@ -435,11 +471,11 @@ __device__ __forceinline__ void row_fold(const f32x16 (&acc)[NT], float scaling,
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
             float x0, x1;
-            exp_args2<DT>(acc[t][j], acc[t][j + 1], scaling, nm, nm, x0, x1);
+            exp_args2<DT, MAP>(acc[t][j], acc[t][j + 1], scaling, nm, nm, x0, x1, map);
             const float e0 = __builtin_amdgcn_exp2f(x0), e1 = __builtin_amdgcn_exp2f(x1);
             if constexpr (MASKED) {
-                z += acc_row(j, 32 * g) <= diag_key ? e0 : 0.0f;
-                z += acc_row(j + 1, 32 * g) <= diag_key ? e1 : 0.0f;
+                z += valid(j) ? e0 : 0.0f;
+                z += valid(j + 1) ? e1 : 0.0f;
             } else {
                 z += e0;
                 z += e1;
@@ -447,7 +483,24 @@ __device__ __forceinline__ void row_fold(const f32x16 (&acc)[NT], float scaling,
         }
 }
 
-template <int DT, int D>
+// Which rows of a wave's 32 queries [q0, q0 + 31] see the keys of 32-key tile
+// kt under the causal mask with window W (query i sees i - W < key <= i):
+// every row sees every key (whole), none does (none), or each lane tests its
+// keys against (i - W - 32 kt, i - 32 kt] (the rest).
+template <bool WIN>
+__device__ __forceinline__ bool tile_whole(int kt, int my_diag, int q0, int W) {
+    if constexpr (WIN) return kt < my_diag && kt * 32 > q0 + 31 - W;
+    return kt < my_diag;
+}
+// tiles past the diagonal, and (WIN) tiles wholly left of the window
+template <bool WIN>
+__device__ __forceinline__ bool tile_left(int kt, int q0, int W) {
+    if constexpr (WIN) return kt * 32 + 31 <= q0 - W;
+    return false;
+}
+
+// WIN instantiations take a.window; the others fold the plain causal mask.
+template <int DT, int D, bool MAP = false, bool WIN = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1))) void real_rowstats(
     RealArgs a) {
     __shared__ __align__(16) char lds0[RealTile<D>::BUF];
@@ -473,34 +526,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     const int my_diag = q0 / 32;                     // the key tile on this wave's diagonal
     const int last_key = min(qb * 128 + 127, a.seq - 1);
     const int n_it = last_key / 64 + 1;              // 64-key stages
+    const int W = WIN ? a.window : kNoWindow;
+    const int it_lo = WIN ? max(qb * 128 - W + 1, 0) / 64 : 0;  // the first stage any row of the block sees
     uint4 qa[RealTile<D>::KS];
     row_operand<D>(qbase, q0 + c, a.seq, g, qa);
     // this lane: query q0 + c, keys tile * 32 + acc_row(j, g)
     float mt = -__builtin_inff(), m = -__builtin_inff(), nm = 0.0f, z = 0.0f;
-    // raw logit distance with exp2 argument 32 (|round_T| error is far below it)
+    // raw logit distance with exp2 argument 32 (|round_T| error is far below
+    // it; a soft-cap map only shrinks distances)
     const float span = 32.0f / (a.scaling * kLog2e);
     const DmaPlan<D> plan;
-    tile_dma<D>(plan, kbase, 0, a.seq, lds0);
+    tile_dma<D>(plan, kbase, it_lo * 64, a.seq, lds0);
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
     auto stage = [&](int it, const char* cur, char* nxt) {
         if (it + 1 < n_it) tile_dma<D>(plan, kbase, (it + 1) * 64, a.seq, nxt);
         if (live) {
             const int kt0 = 2 * it;
-            if (kt0 + 1 < my_diag) {  // both tiles wholly before this wave's queries: no mask
+            // both tiles wholly before this wave's queries (and inside its window): no mask
+            if (kt0 + 1 < my_diag && tile_whole<WIN>(kt0, my_diag, q0, W)) {
                 f32x16 acc[2];
                 acc[0] = logits_lds_regs<DT, D>(cur, qa, c, g);
                 acc[1] = logits_lds_regs<DT, D>(cur + 32 * RealTile<D>::ROWB, qa, c, g);
-                row_fold<DT, 2, false>(acc, a.scaling, span, 0, g, mt, m, nm, z);
+                row_fold<DT, 2, false, MAP>(acc, a.scaling, span, 0, 0, g, mt, m, nm, z, a.logit_map);
             } else {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int kt = kt0 + h;
                     if (kt > my_diag) break;
+                    if (tile_left<WIN>(kt, q0, W)) continue;
                     f32x16 acc[1];
                     acc[0] = logits_lds_regs<DT, D>(cur + h * 32 * RealTile<D>::ROWB, qa, c, g);
-                    if (kt < my_diag) row_fold<DT, 1, false>(acc, a.scaling, span, 0, g, mt, m, nm, z);
-                    else row_fold<DT, 1, true>(acc, a.scaling, span, c, g, mt, m, nm, z);  // key <= query
+                    if (tile_whole<WIN>(kt, my_diag, q0, W))
+                        row_fold<DT, 1, false, MAP>(acc, a.scaling, span, 0, 0, g, mt, m, nm, z, a.logit_map);
+                    else  // query - W < key <= query
+                        row_fold<DT, 1, true, MAP, WIN>(acc, a.scaling, span, q0 + c - W - 32 * kt, q0 + c - 32 * kt,
+                                                        g, mt, m, nm, z, a.logit_map);
                 }
             }
         }
@@ -508,7 +569,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
         __syncthreads();
     };
 #pragma unroll 1
-    for (int it = 0; it < n_it; it += 2) {
+    for (int it = it_lo; it < n_it; it += 2) {
         stage(it, lds0, lds1);
         if (it + 1 < n_it) stage(it + 1, lds1, lds0);
     }
@@ -516,7 +577,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     // lanes c and c + 32 hold the same query over disjoint keys: the row
     // maximum, and both sums moved from their references to it
     const float M = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float nmM = -(eager_logit<DT>(M, a.scaling) * kLog2e);
+    const float nmM = -(eager_logit<DT, MAP>(M, a.scaling, a.logit_map) * kLog2e);
     float zs = m == -__builtin_inff() ? 0.0f : z * __builtin_amdgcn_exp2f(nmM - nm);
     const float m_o = __shfl_xor(m, 32, 64), nm_o = __shfl_xor(nm, 32, 64), z_o = __shfl_xor(z, 32, 64);
     zs += m_o == -__builtin_inff() ? 0.0f : z_o * __builtin_amdgcn_exp2f(nmM - nm_o);
@@ -550,10 +611,11 @@ __device__ __forceinline__ f32x4 mfma16x16(uint4 a, uint4 b, f32x4 acc) {
 // accumulates the sums of keys 0..15 and column 1 those of keys 16..31, in
 // fp32.  That is half the matrix-core passes of summing against an all-ones
 // 32x32x16 operand.  MASKED: rows r with r < key_off (row before the key) or
-// r >= row_end (past seq) contribute 0.
-template <int DT, bool MASKED>
+// r >= row_end (past seq, or at or past key + window) contribute 0.
+template <int DT, bool MASKED, bool MAP = false>
 __device__ __forceinline__ void col_fold(const f32x16& acc, const float* nm_rows, const float* rz_rows, float scaling,
-                                         int key_off, int row_end, int g, const uint4& ones_sel, f32x4& colacc) {
+                                         int key_off, int row_end, int g, const uint4& ones_sel, f32x4& colacc,
+                                         const uint16_t* map = nullptr) {
     uint32_t pk[8];
 #pragma unroll
     for (int jq = 0; jq < 4; ++jq) {
@@ -566,7 +628,7 @@ __device__ __forceinline__ void col_fold(const f32x16& acc, const float* nm_rows
         for (int u = 0; u < 4; u += 2) {
             const int j = 4 * jq + u;
             float x0, x1;
-            exp_args2<DT>(acc[j], acc[j + 1], scaling, nm[u], nm[u + 1], x0, x1);
+            exp_args2<DT, MAP>(acc[j], acc[j + 1], scaling, nm[u], nm[u + 1], x0, x1, map);
             float p0 = __builtin_amdgcn_exp2f(x0) * rz[u];
             float p1 = __builtin_amdgcn_exp2f(x1) * rz[u + 1];
             if constexpr (MASKED) {
@@ -581,7 +643,7 @@ __device__ __forceinline__ void col_fold(const f32x16& acc, const float* nm_rows
     colacc = mfma16x16<DT>(make_uint4(pk[4], pk[5], pk[6], pk[7]), ones_sel, colacc);
 }
 
-template <int DT, int D>
+template <int DT, int D, bool MAP = false, bool WIN = false>
 __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
     __shared__ __align__(16) char lds0[RealTile<D>::BUF];
     __shared__ __align__(16) char lds1[RealTile<D>::BUF];
@@ -603,8 +665,18 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
     const int key = k0 + c;
     const int my_first = k0 / 32;                    // first 32-row query block that sees these keys
     const int it0 = kb * 2;                          // first 64-row query stage of the block
-    const int n_it = (a.seq + 63) / 64;
+    const int W = WIN ? a.window : kNoWindow;
+    // one past the last 64-row stage holding a query that sees a key of the block
+    // (key j is seen by queries j .. j + W - 1)
+    const int n_it = WIN ? min((a.seq + 63) / 64, (kb * 128 + 126 + W) / 64 + 1) : (a.seq + 63) / 64;
     const bool live = k0 < a.seq;
+    // a query tile is whole for this wave's keys [k0, k0 + 31] when all its rows
+    // come after them, lie below seq and (WIN) before k0 + W; none when all its
+    // rows come before the keys or (WIN) at or past k0 + 31 + W
+    auto q_whole = [&](int qt) {
+        return qt > my_first && qt * 32 + 32 <= a.seq && (!WIN || qt * 32 + 31 < k0 + W);
+    };
+    auto q_none = [&](int qt) { return qt < my_first || (WIN && qt * 32 >= k0 + 31 + W); };
     uint4 kr[RealTile<D>::KS];
     row_operand<D>(kbase, key, a.seq, g, kr);
     f32x4 colacc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -637,25 +709,27 @@ __global__ __launch_bounds__(256) void real_colsum(RealArgs a) {
         if (it + 1 < n_it) load_stage(it + 1, nxt, nnm, nrz);
         if (live) {
             const int qt0 = 2 * it;
-            if (qt0 > my_first && qt0 * 32 + 64 <= a.seq) {
-                // both blocks interior (all rows after all keys, all rows < seq):
-                // one basic block, so the second tile's MFMAs run under the
-                // first tile's VALU work
+            if (qt0 > my_first && qt0 * 32 + 64 <= a.seq && (!WIN || qt0 * 32 + 63 < k0 + W)) {
+                // both blocks interior: one basic block, so the second tile's
+                // MFMAs run under the first tile's VALU work
                 const f32x16 acc0 = logits_lds_regs<DT, D>(cur, kr, c, g);
                 const f32x16 acc1 = logits_lds_regs<DT, D>(cur + 32 * RealTile<D>::ROWB, kr, c, g);
-                col_fold<DT, false>(acc0, cnm, crz, a.scaling, 0, 0, g, ones_sel, colacc);
-                col_fold<DT, false>(acc1, cnm + 32, crz + 32, a.scaling, 0, 0, g, ones_sel, colacc);
+                col_fold<DT, false, MAP>(acc0, cnm, crz, a.scaling, 0, 0, g, ones_sel, colacc, a.logit_map);
+                col_fold<DT, false, MAP>(acc1, cnm + 32, crz + 32, a.scaling, 0, 0, g, ones_sel, colacc,
+                                         a.logit_map);
             } else {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int qt = qt0 + h;
-                    if (qt < my_first) continue;
+                    if (q_none(qt)) continue;
                     const f32x16 acc = logits_lds_regs<DT, D>(cur + h * 32 * RealTile<D>::ROWB, kr, c, g);
-                    if (qt > my_first && qt * 32 + 32 <= a.seq)
-                        col_fold<DT, false>(acc, cnm + 32 * h, crz + 32 * h, a.scaling, 0, 0, g, ones_sel, colacc);
+                    if (q_whole(qt))
+                        col_fold<DT, false, MAP>(acc, cnm + 32 * h, crz + 32 * h, a.scaling, 0, 0, g, ones_sel,
+                                                 colacc, a.logit_map);
                     else
-                        col_fold<DT, true>(acc, cnm + 32 * h, crz + 32 * h, a.scaling, key - qt * 32,
-                                           a.seq - qt * 32, g, ones_sel, colacc);
+                        col_fold<DT, true, MAP>(acc, cnm + 32 * h, crz + 32 * h, a.scaling, key - qt * 32,
+                                                WIN ? min(a.seq, key + W) - qt * 32 : a.seq - qt * 32, g, ones_sel,
+                                                colacc, a.logit_map);
                 }
             }
         }
@@ -780,20 +854,21 @@ struct OutArgs {
 
 // Rounded probabilities of one 32 x 32 logit tile for this lane's query (nm,
 // rz its row statistics), packed for the two 16-deep K steps of P V.
-// MASKED: keys acc_row(j, g) > diag (the lane's query within the tile) are 0.
-template <int DT, bool MASKED>
-__device__ __forceinline__ void out_probs(const f32x16& acc, float nm, float rz, float scaling, int diag, int g,
-                                          uint4 (&pa)[2]) {
+// MASKED: keys outside lo < acc_row(j, g) <= hi (the lane's query's window
+// within the tile) are 0.
+template <int DT, bool MASKED, bool MAP = false, bool WIN = false>
+__device__ __forceinline__ void out_probs(const f32x16& acc, float nm, float rz, float scaling, int lo, int hi, int g,
+                                          uint4 (&pa)[2], const uint16_t* map = nullptr) {
     uint32_t pk[8];
 #pragma unroll
     for (int j = 0; j < 16; j += 2) {
         float x0, x1;
-        exp_args2<DT>(acc[j], acc[j + 1], scaling, nm, nm, x0, x1);
+        exp_args2<DT, MAP>(acc[j], acc[j + 1], scaling, nm, nm, x0, x1, map);
         float p0 = __builtin_amdgcn_exp2f(x0) * rz;
         float p1 = __builtin_amdgcn_exp2f(x1) * rz;
         if constexpr (MASKED) {
-            p0 = acc_row(j, 32 * g) <= diag ? p0 : 0.0f;
-            p1 = acc_row(j + 1, 32 * g) <= diag ? p1 : 0.0f;
+            p0 = (!WIN || lo < acc_row(j, 32 * g)) && acc_row(j, 32 * g) <= hi ? p0 : 0.0f;
+            p1 = (!WIN || lo < acc_row(j + 1, 32 * g)) && acc_row(j + 1, 32 * g) <= hi ? p1 : 0.0f;
         }
         pk[j / 2] = round_pair<DT>(p0, p1);
     }
@@ -818,7 +893,7 @@ __device__ __forceinline__ void out_pv(const uint4 (&pa)[2], const char* vbuf, i
 // A workgroup owns 128 query rows of one query head (wave w: rows 32 w ..),
 // queries resident as the QK^T B operand as in real_rowstats, and streams
 // 64-key stages of K (logits) and Vt (values) through two LDS buffers each.
-template <int DT, int D>
+template <int DT, int D, bool MAP = false, bool WIN = false>
 __global__ __launch_bounds__(256) void real_output(OutArgs o) {
     __shared__ __align__(16) char k0buf[RealTile<D>::BUF];
     __shared__ __align__(16) char k1buf[RealTile<D>::BUF];
@@ -845,6 +920,8 @@ __global__ __launch_bounds__(256) void real_output(OutArgs o) {
     const int my_diag = q0 / 32;
     const int last_key = min(qb * 128 + 127, a.seq - 1);
     const int n_it = last_key / 64 + 1;
+    const int W = WIN ? a.window : kNoWindow;
+    const int it_lo = WIN ? max(qb * 128 - W + 1, 0) / 64 : 0;
     uint4 qa[RealTile<D>::KS];
     row_operand<D>(qbase, q0 + c, a.seq, g, qa);
     const size_t stat = (size_t)bhq * a.seq;
@@ -855,8 +932,8 @@ __global__ __launch_bounds__(256) void real_output(OutArgs o) {
     for (int db = 0; db < D / 32; ++db) oacc[db] = f32x16{};
     const DmaPlan<D> kplan;
     const VtPlan<D> vplan(o.s64);
-    tile_dma<D>(kplan, kbase, 0, a.seq, k0buf);
-    vt_dma<D>(vplan, vt_bh, 0, v0buf);
+    tile_dma<D>(kplan, kbase, it_lo * 64, a.seq, k0buf);
+    vt_dma<D>(vplan, vt_bh, it_lo, v0buf);
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
     auto stage = [&](int it, const char* ck, const char* cv, char* nk, char* nv) {
@@ -869,10 +946,14 @@ __global__ __launch_bounds__(256) void real_output(OutArgs o) {
             for (int t = 0; t < 2; ++t) {
                 const int kt = 2 * it + t;
                 if (kt > my_diag) break;
+                if (tile_left<WIN>(kt, q0, W)) continue;
                 const f32x16 acc = logits_lds_regs<DT, D>(ck + t * 32 * RealTile<D>::ROWB, qa, c, g);
                 uint4 pa[2];
-                if (kt < my_diag) out_probs<DT, false>(acc, nm, rz, a.scaling, 0, g, pa);
-                else out_probs<DT, true>(acc, nm, rz, a.scaling, c, g, pa);
+                if (tile_whole<WIN>(kt, my_diag, q0, W))
+                    out_probs<DT, false, MAP>(acc, nm, rz, a.scaling, 0, 0, g, pa, a.logit_map);
+                else
+                    out_probs<DT, true, MAP, WIN>(acc, nm, rz, a.scaling, q0 + c - W - 32 * kt, q0 + c - 32 * kt, g,
+                                                  pa, a.logit_map);
                 out_pv<DT, D>(pa, cv, t, c, g, oacc);
             }
         }
@@ -880,7 +961,7 @@ __global__ __launch_bounds__(256) void real_output(OutArgs o) {
         __syncthreads();
     };
 #pragma unroll 1
-    for (int it = 0; it < n_it; it += 2) {
+    for (int it = it_lo; it < n_it; it += 2) {
         stage(it, k0buf, v0buf, k1buf, v1buf);
         if (it + 1 < n_it) stage(it + 1, k1buf, v1buf, k0buf, v0buf);
     }
@@ -940,8 +1021,16 @@ static hipError_t launch_real(const RealArgs& a, hipStream_t st) {
         w.n_items = n_blocks * a.batch * a.hq;
         w.per_xcd = (w.n_items + 7) / 8;
         dim3 grid(8 * w.per_xcd);
-        hipLaunchKernelGGL((real_rowstats<DT, D>), grid, dim3(256), 0, st, w);
-        hipLaunchKernelGGL((real_colsum<DT, D>), grid, dim3(256), 0, st, w);
+        if (a.logit_map) {
+            hipLaunchKernelGGL((real_rowstats<DT, D, true, true>), grid, dim3(256), 0, st, w);
+            hipLaunchKernelGGL((real_colsum<DT, D, true, true>), grid, dim3(256), 0, st, w);
+        } else if (a.window != kNoWindow) {
+            hipLaunchKernelGGL((real_rowstats<DT, D, false, true>), grid, dim3(256), 0, st, w);
+            hipLaunchKernelGGL((real_colsum<DT, D, false, true>), grid, dim3(256), 0, st, w);
+        } else {
+            hipLaunchKernelGGL((real_rowstats<DT, D>), grid, dim3(256), 0, st, w);
+            hipLaunchKernelGGL((real_colsum<DT, D>), grid, dim3(256), 0, st, w);
+        }
     }
     hipLaunchKernelGGL(head_mean_accumulate, dim3((a.seq + kHeadMeanThreads - 1) / kHeadMeanThreads, a.batch),
                        dim3(kHeadMeanThreads), 0, st, a.colsum, a.importance, a.hq, a.seq);
@@ -956,9 +1045,14 @@ static hipError_t launch_attention(const RealArgs& a, const void* v, void* out, 
     w.n_items = n_blocks * a.batch * a.hq;
     w.per_xcd = (w.n_items + 7) / 8;
     dim3 grid(8 * w.per_xcd);
-    hipLaunchKernelGGL((real_rowstats<DT, D>), grid, dim3(256), 0, st, w);
+    const bool map = a.logit_map != nullptr, win = a.window != kNoWindow;
+    if (map) hipLaunchKernelGGL((real_rowstats<DT, D, true, true>), grid, dim3(256), 0, st, w);
+    else if (win) hipLaunchKernelGGL((real_rowstats<DT, D, false, true>), grid, dim3(256), 0, st, w);
+    else hipLaunchKernelGGL((real_rowstats<DT, D>), grid, dim3(256), 0, st, w);
     if (with_importance) {
-        hipLaunchKernelGGL((real_colsum<DT, D>), grid, dim3(256), 0, st, w);
+        if (map) hipLaunchKernelGGL((real_colsum<DT, D, true, true>), grid, dim3(256), 0, st, w);
+        else if (win) hipLaunchKernelGGL((real_colsum<DT, D, false, true>), grid, dim3(256), 0, st, w);
+        else hipLaunchKernelGGL((real_colsum<DT, D>), grid, dim3(256), 0, st, w);
         hipLaunchKernelGGL(head_mean_accumulate, dim3((a.seq + kHeadMeanThreads - 1) / kHeadMeanThreads, a.batch),
                            dim3(kHeadMeanThreads), 0, st, a.colsum, a.importance, a.hq, a.seq);
     }
@@ -969,7 +1063,9 @@ static hipError_t launch_attention(const RealArgs& a, const void* v, void* out, 
     o.vt = vt;
     o.out = out;
     o.s64 = s64;
-    hipLaunchKernelGGL((real_output<DT, D>), grid, dim3(256), 0, st, o);
+    if (map) hipLaunchKernelGGL((real_output<DT, D, true, true>), grid, dim3(256), 0, st, o);
+    else if (win) hipLaunchKernelGGL((real_output<DT, D, false, true>), grid, dim3(256), 0, st, o);
+    else hipLaunchKernelGGL((real_output<DT, D>), grid, dim3(256), 0, st, o);
     return hipGetLastError();
 }
 
@@ -990,10 +1086,14 @@ extern "C" int64_t nq_score_real_workspace(int32_t batch, int32_t q_heads, int32
 }
 
 extern "C" int nq_score_real(const void* q, const void* k, int32_t dtype, int32_t batch, int32_t q_heads,
-                             int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, float* importance,
-                             void* workspace, int64_t workspace_bytes, void* stream) {
+                             int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, int32_t sliding_window,
+                             const uint16_t* logit_map, float* importance, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
     using namespace nq;
     NQ_CHECK_ARG(q && k && importance && workspace, "nq_score_real: NULL pointer");
+    NQ_CHECK_ARG(sliding_window >= 0, "nq_score_real: negative sliding window");
+    NQ_CHECK_ARG(logit_map == nullptr || dtype != NQ_F32,
+                 "nq_score_real: a logit map takes fp16 or bf16 models (65536 model-dtype values)");
     NQ_CHECK_ARG(batch > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
                  "nq_score_real: q_heads must be a positive multiple of kv_heads");
     NQ_CHECK_ARG((int64_t)batch * q_heads <= 65535 && seq >= 0, "nq_score_real: bad shape");
@@ -1017,6 +1117,8 @@ extern "C" int nq_score_real(const void* q, const void* k, int32_t dtype, int32_
     a.hkv = kv_heads;
     a.batch = batch;
     a.scaling = scaling;
+    a.window = sliding_window > 0 && sliding_window < kNoWindow ? sliding_window : kNoWindow;
+    a.logit_map = logit_map;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     switch (dtype) {
@@ -1038,10 +1140,11 @@ extern "C" int64_t nq_attention_real_workspace(int32_t batch, int32_t q_heads, i
 
 extern "C" int nq_attention_real(const void* q, const void* k, const void* v, int32_t dtype, int32_t batch,
                                  int32_t q_heads, int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling,
-                                 float* importance, void* out, void* workspace, int64_t workspace_bytes,
-                                 void* stream) {
+                                 int32_t sliding_window, const uint16_t* logit_map, float* importance, void* out,
+                                 void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace nq;
     NQ_CHECK_ARG(q && k && v && out && workspace, "nq_attention_real: NULL pointer");
+    NQ_CHECK_ARG(sliding_window >= 0, "nq_attention_real: negative sliding window");
     NQ_CHECK_ARG(batch > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
                  "nq_attention_real: q_heads must be a positive multiple of kv_heads");
     NQ_CHECK_ARG((int64_t)batch * q_heads <= 65535 && seq >= 0, "nq_attention_real: bad shape");
@@ -1068,6 +1171,8 @@ extern "C" int nq_attention_real(const void* q, const void* k, const void* v, in
     a.hkv = kv_heads;
     a.batch = batch;
     a.scaling = scaling;
+    a.window = sliding_window > 0 && sliding_window < kNoWindow ? sliding_window : kNoWindow;
+    a.logit_map = logit_map;
     const int64_t stats = (nq_score_real_workspace(batch, q_heads, seq) + 255) / 256 * 256;
     uint16_t* vt = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + stats);
     const int s64 = (seq + 63) / 64 * 64;

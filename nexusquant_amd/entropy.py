@@ -42,6 +42,8 @@ from .ops import _addr
 
 PROB_BITS = 12
 M = 1 << PROB_BITS
+# symbols per chunk at most (nq_rans_encode / nq_rans_decode take an int32 chunk)
+MAX_CHUNK = (1 << 31) - 1
 DEFAULT_CHUNK = 2048  # symbols per chunk (one lane's chain); see the measurements in the design notes
 _MAGIC = b"NQR1"
 
@@ -203,8 +205,8 @@ def check_stream_header(levels: int, has_half: bool, alphabet: int, n: int, chun
     if alphabet != want_alpha:
         raise ValueError(f"alphabet {alphabet} does not match levels {levels} "
                          f"({'with' if has_half else 'without'} half-integer points: {want_alpha})")
-    if chunk < 1 or chunk > (1 << 30):
-        raise ValueError(f"chunk must be in [1, 2^30], got {chunk}")
+    if chunk < 1 or chunk > MAX_CHUNK:
+        raise ValueError(f"chunk must be in [1, 2^31 - 1], got {chunk}")
     if n < 0:
         raise ValueError(f"negative symbol count {n}")
     if n_chunks != (n + chunk - 1) // chunk:
@@ -379,7 +381,11 @@ def encode_e8(quantized: torch.Tensor, scale_factors: torch.Tensor, levels: int 
 
     quantized: scaled lattice points on a ROCm device (any shape, groups of 8);
     scale_factors: one per group of 8, or one in all.  The bytes equal the
-    reference's for the same inputs."""
+    reference's for the same inputs.  The container codes every symbol in one
+    rANS chain; this build takes up to 2^31 - 1 symbols per container."""
+    if quantized.numel() > MAX_CHUNK:
+        raise ValueError(f"encode_e8 codes all symbols as one rANS chain; this build takes at most 2^31 - 1 "
+                         f"symbols per container, got {quantized.numel()} (encode the tensor in pieces)")
     codes, has_half, scales = _e8_codes(quantized, scale_factors, levels)
     n = codes.numel()
     if n:
@@ -424,6 +430,9 @@ def decode_e8(compressed: bytes, original_shape: Optional[tuple] = None, device=
     words = np.frombuffer(compressed, dtype="<u2", count=rans_len // 2, offset=at).copy()
     if n_symbols != 8 * n_groups:
         raise ValueError(f"cannot reshape {n_symbols} symbols into {n_groups} groups of 8")
+    if n_symbols > MAX_CHUNK:
+        raise ValueError(f"decode_e8 decodes one rANS chain of at most 2^31 - 1 symbols in this build; the "
+                         f"container holds {n_symbols}")
     n_scales = scales_f16.size
     if n_scales not in (1, n_groups) and n_groups:
         raise ValueError(f"operands could not be broadcast together: {n_groups} groups of 8 and {n_scales} scales")

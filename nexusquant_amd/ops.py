@@ -155,6 +155,34 @@ def _addr(t: Optional[torch.Tensor]):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+_workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
+_workspaces_lock = threading.Lock()
+
+
+def workspace(device, nbytes: int) -> torch.Tensor:
+    """A device byte buffer of at least nbytes for the current stream of `device`,
+    kept between calls (grown when a call needs more).  Calls on one stream run
+    in stream order, so they can share it; each stream has its own.  Freed by
+    release_workspaces()."""
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, _lib.current_stream_handle(torch.device("cuda", idx)))
+    n = max(int(nbytes), 1)
+    with _workspaces_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() < n:
+            # round up to 1 MiB so that slowly growing shapes do not reallocate each call
+            buf = torch.empty(((n + (1 << 20) - 1) >> 20) << 20, dtype=torch.uint8, device=torch.device("cuda", idx))
+            _workspaces[key] = buf
+    return buf
+
+
+def release_workspaces() -> None:
+    """Drop the cached workspaces (their memory returns to torch's allocator)."""
+    with _workspaces_lock:
+        _workspaces.clear()
+
+
 def quantize_tensors(tensors: Sequence[torch.Tensor], *, is_key: bool, levels: int,
                      rope_base: float = 10000.0, rope_scaling: Optional[dict] = None,
                      gather: Optional[torch.Tensor] = None, keep: Optional[torch.Tensor] = None,
@@ -309,7 +337,7 @@ def score_keykey(keys: torch.Tensor, obs_window: int = 32) -> torch.Tensor:
     if int(obs_window) <= 0:
         raise ValueError(f"obs_window must be positive, got {obs_window}")
     ws_bytes = lib.nq_score_keykey_workspace(b, h, s, int(obs_window))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = workspace(dev, ws_bytes)
     scale = float(d) ** -0.5
     with torch.cuda.device(dev):
         st = lib.nq_score_keykey(_addr(k), _lib.dtype_code(k.dtype), b, h, s, d, int(obs_window),
@@ -421,7 +449,7 @@ def merge_values(values: Sequence[torch.Tensor], keep: torch.Tensor, kept_idx: t
     cent = torch.empty(b, s, d, dtype=torch.float32, device=dev) if centroids else None
     surv = torch.empty(b, s, dtype=torch.int32, device=dev) if survivors else None
     ws_bytes = lib.nq_merge_workspace(b, s, d)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = workspace(dev, ws_bytes)
     staged = _PtrArrays([src, out], dev)
     arrays = staged.arrays
     desc = _lib.MergeDesc(n_tensors=len(src), batch=b, heads=h, seq=s, head_dim=d,

@@ -550,7 +550,8 @@ class NexusQuantPagedAttention:
             raise ValueError(f"num_heads {hq} is not a multiple of the pages' num_heads {kv}")
         ws_bytes = lib.nq_paged_attention_workspace(plan.n_chunks, hq, d)
         if workspace is None or workspace.numel() < ws_bytes:
-            workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+            from .ops import workspace as stream_workspace
+            workspace = stream_workspace(dev, ws_bytes)
         cos = sin = dm = dp = None
         n_pos = 0
         if plan.n_chunks:

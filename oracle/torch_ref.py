@@ -238,22 +238,6 @@ def e8_quantize_perhead(x: torch.Tensor, levels: int = 8) -> torch.Tensor:
     return (p * scale).reshape(x.shape)
 
 
-def e8_quantize_pergroup(x: torch.Tensor, levels: int = 8) -> torch.Tensor:
-    """Per-8-group scaled variant (e8_lattice.py:72-94)."""
-    shape = x.shape
-    pad = (8 - shape[-1] % 8) % 8
-    if pad:
-        x = F.pad(x, (0, pad))
-    flat = x.reshape(-1, 8)
-    amax = flat.abs().amax(dim=-1, keepdim=True).clamp(min=1e-8)
-    sc = amax / (levels / 2)
-    lp = e8_nearest_point(flat / sc).clamp(-levels / 2, levels / 2) * sc
-    res = lp.reshape(x.shape)
-    if pad:
-        res = res[..., :shape[-1]]
-    return res.reshape(shape)
-
-
 def lattice_codes_2p(p: torch.Tensor) -> torch.Tensor:
     """Stored int8 code = round(2p), the vLLM page format (vllm_backend.py:309-314)."""
     return (p * 2).round().clamp(-127, 127).to(torch.int8)
@@ -350,34 +334,52 @@ def score_keykey(keys: torch.Tensor, obs_window: int = 32) -> torch.Tensor:
     return att.sum(dim=2).mean(dim=1)
 
 
-def eager_attention_probs(q: torch.Tensor, k: torch.Tensor, scaling: float) -> torch.Tensor:
+def eager_attention_probs(q: torch.Tensor, k: torch.Tensor, scaling: float, sliding_window=None,
+                          softcap=None) -> torch.Tensor:
     """HF eager attention probabilities for one layer.
 
     transformers 5.15.0 models/llama/modeling_llama.py:179-213: repeat_kv for
     GQA, matmul(Q, K^T) * scaling in the model dtype, add the causal mask
     (dtype minimum above the diagonal), softmax in fp32, cast back.
+    softcap: Gemma-2's w = tanh(w / softcap) * softcap before the mask
+    (models/gemma2/modeling_gemma2.py:201-206); sliding_window: keys with
+    key <= query - sliding_window are masked as well (masking_utils.py:92-101).
     q [b, hq, s, d], k [b, hkv, s, d] -> probs [b, hq, s, s] in q.dtype.
     """
     b, hq, s, d = q.shape
     rep = hq // k.shape[1]
     kr = k[:, :, None, :, :].expand(b, k.shape[1], rep, s, d).reshape(b, hq, s, d)
     w = torch.matmul(q, kr.transpose(2, 3)) * scaling
-    mask = torch.full((s, s), torch.finfo(q.dtype).min, dtype=q.dtype, device=q.device).triu(1)
+    if softcap is not None:
+        w = w / softcap
+        w = torch.tanh(w)
+        w = w * softcap
+    i = torch.arange(s, device=q.device)[:, None]
+    j = torch.arange(s, device=q.device)[None, :]
+    allowed = j <= i
+    if sliding_window is not None:
+        allowed = allowed & (j > i - sliding_window)
+    mask = torch.zeros((s, s), dtype=q.dtype, device=q.device).masked_fill(~allowed, torch.finfo(q.dtype).min)
     w = w + mask
     return torch.softmax(w, dim=-1, dtype=torch.float32).to(q.dtype)
 
 
 def score_real_from_qk(q_layers: Sequence[torch.Tensor], k_layers: Sequence[torch.Tensor],
-                       scaling: Optional[float] = None) -> torch.Tensor:
-    """Importance from real attention (pipeline.py:822-836) given per-layer Q, K."""
+                       scaling: Optional[float] = None, windows: Optional[Sequence] = None,
+                       softcaps: Optional[Sequence] = None) -> torch.Tensor:
+    """Importance from real attention (pipeline.py:822-836) given per-layer Q, K
+    (and per-layer sliding windows / soft-caps, None for none)."""
     b, _, s, d = q_layers[0].shape
     if scaling is None:
         scaling = d ** -0.5
+    n = len(q_layers)
+    windows = windows if windows is not None else [None] * n
+    softcaps = softcaps if softcaps is not None else [None] * n
     imp = torch.zeros(b, s, dtype=torch.float32)
-    for q, k in zip(q_layers, k_layers):
-        probs = eager_attention_probs(q, k, scaling).float()
+    for q, k, w, cap in zip(q_layers, k_layers, windows, softcaps):
+        probs = eager_attention_probs(q, k, scaling, sliding_window=w, softcap=cap).float()
         imp += probs.sum(dim=2).mean(dim=1)
-    return imp / len(q_layers)
+    return imp / n
 
 
 # ---------------------------------------------------------------------------

@@ -9,7 +9,8 @@ eager attention.  Nothing under /root/reference is copied; only the numbers it
 produces are stored, as small .npz files next to this script.
 
 Usage:  python tests/golden/make_golden.py [/root/reference [evict_soft | vllm_pages | evict_merge | rans |
-                                                              temporal_codec | e8stream]]
+                                                              temporal_codec | e8stream |
+                                                              real_scorer_window]]
 """
 
 from __future__ import annotations
@@ -177,6 +178,56 @@ def real_scorer_fixture():
     qs = torch.stack([q for q, _, _ in captured])
     kss = torch.stack([k for _, k, _ in captured])
     save("real_scorer", q=qs, k=kss, scaling=captured[0][2], importance=imp)
+
+
+def real_scorer_window_fixtures():
+    """The real scorer through transformers' eager attention on models whose
+    masks or logits differ from plain causal softmax: a tiny Mistral with a
+    sliding window shorter than the sequence, and a tiny Gemma-2 with logit
+    soft-capping and alternating sliding-window / full layers.  fp16 weights
+    on the CPU; per layer the post-RoPE q, k, scaling, window and soft-cap the
+    eager attention received, and the reference's importance."""
+    from transformers import Gemma2Config, Gemma2ForCausalLM, MistralConfig, MistralForCausalLM
+    import transformers.models.gemma2.modeling_gemma2 as mg
+    import transformers.models.mistral.modeling_mistral as mm
+
+    seq = 160
+    cases = {
+        "real_scorer_mistral": (mm, MistralForCausalLM, MistralConfig(
+            vocab_size=128, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+            num_attention_heads=4, num_key_value_heads=2, head_dim=64, max_position_embeddings=512,
+            rope_theta=10000.0, sliding_window=48)),
+        "real_scorer_gemma2": (mg, Gemma2ForCausalLM, Gemma2Config(
+            vocab_size=128, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+            num_attention_heads=4, num_key_value_heads=2, head_dim=64, max_position_embeddings=512,
+            rope_theta=10000.0, sliding_window=40, attn_logit_softcapping=50.0, final_logit_softcapping=30.0,
+            query_pre_attn_scalar=64)),
+    }
+    for name, (mod, cls, cfg) in cases.items():
+        torch.manual_seed(73)
+        cfg._attn_implementation = "eager"
+        model = cls(cfg).to(torch.float16).eval()
+        captured = []
+        orig = mod.eager_attention_forward
+
+        def spy(module, query, key, value, attention_mask, *args, _orig=orig, **kw):
+            captured.append((query.detach().clone(), key.detach().clone(), float(kw.get("scaling", args[0] if args
+                                                                                       else module.scaling)),
+                             kw.get("sliding_window"), kw.get("softcap")))
+            return _orig(module, query, key, value, attention_mask, *args, **kw)
+
+        mod.eager_attention_forward = spy
+        try:
+            ids = torch.randint(0, 128, (1, seq), generator=torch.Generator().manual_seed(74))
+            nq = NexusQuantEvict(scorer="real")
+            imp = nq._score_importance_real(model, ids)
+        finally:
+            mod.eager_attention_forward = orig
+        save(name, q=torch.stack([c[0] for c in captured]), k=torch.stack([c[1] for c in captured]),
+             scaling=np.array([c[2] for c in captured], np.float64),
+             window=np.array([0 if c[3] is None else int(c[3]) for c in captured], np.int64),
+             softcap=np.array([0.0 if c[4] is None else float(c[4]) for c in captured], np.float64),
+             importance=imp)
 
 
 def make_soft():
@@ -370,6 +421,8 @@ if __name__ == "__main__":
         make_temporal()
     elif sys.argv[2:] == ["e8stream"]:
         make_e8stream()
+    elif sys.argv[2:] == ["real_scorer_window"]:
+        real_scorer_window_fixtures()
     else:
         main()
         make_soft()
@@ -378,3 +431,4 @@ if __name__ == "__main__":
         make_rans()
         make_temporal()
         make_e8stream()
+        real_scorer_window_fixtures()

@@ -74,3 +74,17 @@ def test_million_symbol_roundtrip():
     blob = encode_e8(p * s[:, None], s, levels=8)
     vals, sc = decode_e8(blob, device=DEV)
     assert torch.equal(vals, p * s.half().float()[:, None])
+
+
+def test_roundtrip_above_2_24_symbols():
+    # one chain over 2^24 + 64 symbols, above the chunk bound of earlier builds
+    # (a whole [1, 8, 16384, 128] layer is 2^24 symbols)
+    from nexusquant_amd.entropy import decode_e8, encode_e8
+    print("[gpu] encode_e8 2^24 + 64 symbols", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    n_groups = (1 << 21) + 8
+    p = torch.clamp(torch.round(torch.randn(n_groups, 8, device=DEV, generator=g) * 2), -8, 8) / 2
+    s = torch.rand(n_groups, device=DEV, generator=g) + 0.1
+    blob = encode_e8(p * s[:, None], s, levels=8)
+    vals, _ = decode_e8(blob, device=DEV)
+    assert torch.equal(vals, p * s.half().float()[:, None])

@@ -118,15 +118,16 @@ def test_real_scorer_at_c4_layer_size():
     dev = (imp_c - ref).abs().max().item()
     print(f"[gpu]   max |imp - ref| = {dev:.3e} (max ref {ref.max().item():.3e})", flush=True)
     assert torch.allclose(imp_c, ref, rtol=2e-3, atol=1e-6)
-    # Keep sets: a position may differ only where its reference score lies within
-    # the two scorers' largest disagreement of the k-th score.  fp16 eager
-    # attention rounds Q.K^T to fp16, so two correct fp32-accumulating products
-    # (MKL on the host, MFMA here) disagree on ~0.4 % of the rounded logits.
+    # Keep sets: identical except positions whose reference score lies within
+    # 1e-6 of the k-th score (the north star's tie rule).  fp16 eager attention
+    # rounds Q.K^T to fp16, so two correct fp32-accumulating products (MKL on the
+    # host, MFMA here) disagree on ~0.4 % of the rounded logits; on this seed
+    # that moves no position across the threshold.
     keep, _, _ = keep_mask(imp, 0.35, 32)
     kr = T.build_keep_mask(ref, 8192, 0.35, 32).numpy()
     km = keep.cpu().numpy().astype(bool)
     print(f"[gpu]   keep sets differ at {int((km != kr).sum())} positions", flush=True)
-    assert _keep_sets_match(imp_c.numpy(), ref.numpy(), km, kr, tol=max(2 * dev, 1e-6))
+    assert _keep_sets_match(imp_c.numpy(), ref.numpy(), km, kr, tol=1e-6)
 
 
 @pytest.mark.parametrize("s,rate,sw", [(8192, 0.25, 32), (1000, 0.6, 32), (300, 0.8, 8), (50, 0.5, 4),
@@ -473,15 +474,24 @@ def test_hook_default_mode_protects_every_layer_with_boundary_2():
         assert torch.all(k[0, :, evicted.to(DEV), :] == 0)
 
 
-def _eager_attention(q, k, v, scaling):
+def _eager_attention(q, k, v, scaling, window=None, softcap=None):
     """transformers' eager_attention_forward on the GPU, in the model dtype
-    (right-hand operands made contiguous before the batched products)."""
+    (right-hand operands made contiguous before the batched products); softcap
+    as Gemma-2's, with the division a true fp32 division as on the CPU (torch
+    on the GPU multiplies by a scalar divisor's reciprocal)."""
     grp = q.shape[1] // k.shape[1]
     kr = k.repeat_interleave(grp, dim=1)
     vr = v.repeat_interleave(grp, dim=1)
     w = torch.matmul(q, kr.transpose(2, 3).contiguous()) * scaling
+    if softcap is not None:
+        w = (w.float() / torch.tensor(softcap, device=q.device)).to(q.dtype)
+        w = torch.tanh(w)
+        w = w * softcap
     s = q.shape[2]
-    w = w + torch.full((s, s), torch.finfo(q.dtype).min, device=q.device, dtype=q.dtype).triu(1)
+    i = torch.arange(s, device=q.device)[:, None]
+    j = torch.arange(s, device=q.device)[None, :]
+    allowed = (j <= i) if window is None else (j <= i) & (j > i - window)
+    w = w + torch.zeros((s, s), device=q.device, dtype=q.dtype).masked_fill(~allowed, torch.finfo(q.dtype).min)
     p = torch.softmax(w, dim=-1, dtype=torch.float32).to(q.dtype)
     return torch.matmul(p, vr.contiguous())
 
@@ -546,3 +556,105 @@ def test_keykey_scorer_and_keep_mask_at_a_c2_length_context():
     assert torch.equal(keep.cpu().bool(), want)
     pos = want[0].nonzero(as_tuple=True)[0].to(torch.int32)
     assert int(n_kept[0]) == pos.numel() and torch.equal(kept[0, :pos.numel()].cpu(), pos)
+
+
+WINDOW_CASES = [(torch.float16, 300, 64, 8, 2, 48, None), (torch.bfloat16, 515, 128, 4, 1, 100, None),
+                (torch.float16, 700, 128, 8, 2, 257, None), (torch.float16, 260, 96, 4, 4, 1, None),
+                (torch.bfloat16, 200, 256, 2, 1, 64, None), (torch.float32, 300, 64, 4, 2, 70, None),
+                (torch.float16, 300, 64, 8, 2, None, 30.0), (torch.bfloat16, 400, 128, 4, 2, 128, 30.0),
+                (torch.float16, 640, 128, 8, 2, 130, 50.0), (torch.float16, 200, 64, 4, 2, 4096, None)]
+
+
+@pytest.mark.parametrize("dtype,s,d,hq,hkv,window,cap", WINDOW_CASES)
+def test_real_scorer_window_and_softcap_match_eager_oracle(dtype, s, d, hq, hkv, window, cap):
+    # sliding windows (query i sees i - window < key <= i) and Gemma-2 logit
+    # soft-capping against the Tier-A eager restatement; logits spread wide
+    # enough (|w| up to ~25) that the cap changes the result
+    from nexusquant_amd.scoring import score_real_accumulate
+    print(f"[gpu] real scorer window={window} softcap={cap} {dtype} s={s} d={d}", flush=True)
+    g = torch.Generator().manual_seed(11 + s + d)
+    q = (torch.randn(1, hq, s, d, generator=g) * 2.5).to(dtype)
+    k = (torch.randn(1, hkv, s, d, generator=g) * 2.5).to(dtype)
+    imp = torch.zeros(1, s, device=DEV)
+    score_real_accumulate(q.to(DEV), k.to(DEV), imp, d ** -0.5, sliding_window=window, softcap=cap)
+    imp = imp.cpu()
+    cast = (lambda x: x.float()) if dtype == torch.float32 else (lambda x: x)
+    ref = T.score_real_from_qk([cast(q)], [cast(k)], d ** -0.5, windows=[window], softcaps=[cap])
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    assert torch.allclose(imp, ref, rtol=tol, atol=1e-6), (imp - ref).abs().max()
+    if (window is not None and window < s) or cap is not None:
+        plain = T.score_real_from_qk([cast(q)], [cast(k)], d ** -0.5)
+        assert not torch.allclose(plain, ref, rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("name", ["real_scorer_mistral", "real_scorer_gemma2"])
+def test_real_scorer_window_softcap_match_reference_fixtures(golden, name):
+    # the reference's _score_importance_real on a tiny Mistral (window 48) and a
+    # tiny Gemma-2 (soft-cap 50, sliding and full layers), fp16
+    from nexusquant_amd.scoring import score_real_accumulate
+    print(f"[gpu] real scorer fixture {name}", flush=True)
+    g = golden(name)
+    q, k = torch.from_numpy(g["q"]), torch.from_numpy(g["k"])
+    imp = torch.zeros(q.shape[1], q.shape[3], device=DEV)
+    for li in range(q.shape[0]):
+        score_real_accumulate(q[li].to(DEV), k[li].to(DEV), imp, float(g["scaling"][li]),
+                              sliding_window=int(g["window"][li]) or None, softcap=float(g["softcap"][li]) or None)
+    imp = (imp / q.shape[0]).cpu().numpy()
+    assert np.allclose(imp, g["importance"], rtol=1e-5, atol=1e-7), np.abs(imp - g["importance"]).max()
+
+
+@pytest.mark.parametrize("dtype,d,s,hq,hkv,window,cap", [(torch.float16, 128, 300, 8, 2, 70, None),
+                                                        (torch.bfloat16, 64, 400, 4, 1, 33, 30.0),
+                                                        (torch.float16, 64, 700, 8, 8, None, 50.0)])
+def test_attention_real_output_window_softcap_match_eager(dtype, d, s, hq, hkv, window, cap):
+    from nexusquant_amd.scoring import attention_real, score_real_accumulate
+    print(f"[gpu] attention_real window={window} softcap={cap} {dtype} d={d} s={s}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(s + d + 1)
+    q = (torch.randn(2, hq, s, d, device=DEV, generator=g) * 2).to(dtype)
+    k = (torch.randn(2, hkv, s, d, device=DEV, generator=g) * 2).to(dtype)
+    v = torch.randn(2, hkv, s, d, device=DEV, generator=g).to(dtype)
+    sc = d ** -0.5
+    imp = torch.zeros(2, s, device=DEV)
+    out = attention_real(q, k, v, sc, imp, sliding_window=window, softcap=cap)
+    ref = _eager_attention(q, k, v, sc, window=window, softcap=cap)
+    diff = (out.float() - ref.float()).abs()
+    ulp = 2.0 ** (-10 if dtype == torch.float16 else -7)
+    assert diff.max().item() <= 2 * ulp * max(1.0, ref.float().abs().max().item()), diff.max().item()
+    assert (diff == 0).float().mean().item() > 0.9
+    imp2 = torch.zeros(2, s, device=DEV)
+    score_real_accumulate(q, k, imp2, sc, sliding_window=window, softcap=cap)
+    assert torch.equal(imp, imp2)
+
+
+def _tiny_window_model(kind, dtype=torch.float16):
+    from transformers import Gemma2Config, Gemma2ForCausalLM, MistralConfig, MistralForCausalLM
+    torch.manual_seed(6)
+    common = dict(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=3,
+                  num_attention_heads=4, num_key_value_heads=2, head_dim=64, max_position_embeddings=1024,
+                  rope_theta=10000.0)
+    if kind == "mistral":
+        cfg, cls = MistralConfig(sliding_window=48, **common), MistralForCausalLM
+    else:
+        cfg, cls = Gemma2Config(sliding_window=40, attn_logit_softcapping=50.0, final_logit_softcapping=30.0,
+                                query_pre_attn_scalar=48, **common), Gemma2ForCausalLM
+    cfg._attn_implementation = "eager"
+    return cls(cfg).to(DEV, dtype).eval()
+
+
+@pytest.mark.parametrize("kind", ["mistral", "gemma2"])
+@pytest.mark.parametrize("fused", [True, False])
+def test_scoring_forward_with_window_and_softcap_matches_model_attentions(kind, fused):
+    # the whole scoring forward on models the kernels used to refuse: importance
+    # against the column sums of the model's own eager attentions
+    from nexusquant_amd.scoring import real_importance
+    print(f"[gpu] scoring forward {kind} fused={fused}", flush=True)
+    model = _tiny_window_model(kind)
+    ids = torch.randint(0, 256, (1, 200), generator=torch.Generator().manual_seed(8)).to(DEV)
+    with torch.no_grad():
+        out = model(ids, use_cache=False, output_attentions=True)
+        ref = torch.zeros(1, 200, device=DEV)
+        for a in out.attentions:
+            ref += a.float().sum(dim=2).mean(dim=1)
+        ref /= len(out.attentions)
+        imp = real_importance(model, ids, fused_attention=fused)
+    assert torch.allclose(imp, ref, rtol=2e-3, atol=1e-5), (imp - ref).abs().max()

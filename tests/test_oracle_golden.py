@@ -136,3 +136,21 @@ def test_real_scorer_matches_transformers_eager(golden):
     imp = T.score_real_from_qk(q, k, float(g["scaling"]))
     assert np.allclose(imp.numpy(), g["importance"], rtol=0, atol=1e-6)
     assert np.array_equal(imp.numpy(), g["importance"])
+
+
+@pytest.mark.parametrize("name", ["real_scorer_mistral", "real_scorer_gemma2"])
+def test_real_scorer_window_and_softcap_match_transformers_eager(golden, name):
+    # the reference's _score_importance_real on a tiny Mistral (sliding window
+    # 48 < seq 160) and a tiny Gemma-2 (soft-cap 50, a sliding layer of 40 and a
+    # full layer), fp16: the oracle's eager restatement gives the same importance
+    g = golden(name)
+    q = [_t(x) for x in g["q"]]
+    k = [_t(x) for x in g["k"]]
+    win = [int(w) or None for w in g["window"]]
+    cap = [float(c) or None for c in g["softcap"]]
+    assert len(set(float(x) for x in g["scaling"])) == 1
+    imp = T.score_real_from_qk(q, k, float(g["scaling"][0]), windows=win, softcaps=cap)
+    assert np.array_equal(imp.numpy(), g["importance"])
+    # the window and the cap change the result: without them it differs
+    plain = T.score_real_from_qk(q, k, float(g["scaling"][0]))
+    assert not np.allclose(plain.numpy(), g["importance"], rtol=0, atol=1e-4)

@@ -148,3 +148,22 @@ def test_decode_rechecks_a_stream_changed_after_its_check(change):
     assert st._checked != st._layout_key()
     with pytest.raises(ValueError):
         rans_decode(st)
+
+
+def test_single_chain_limit_is_stated_and_checked_on_the_host():
+    # chunks (and so encode_e8 / decode_e8 containers) take up to 2^31 - 1
+    # symbols; larger requests are refused before any device work
+    import struct
+    from nexusquant_amd import entropy as E
+    E.check_stream_header(8, True, 17, (1 << 31) - 1, (1 << 31) - 1, 1)
+    with pytest.raises(ValueError, match="2\\^31 - 1"):
+        E.check_stream_header(8, True, 17, 1 << 31, 1 << 31, 1)
+    big = torch.zeros(1).expand((1 << 31) + 8)         # no memory behind the view
+    with pytest.raises(ValueError, match="2\\^31 - 1"):
+        E.encode_e8(big, torch.ones(1))
+    n_groups = 1 << 28                                 # 2^31 symbols
+    freq = struct.pack("<H", 9) + b"\x00\x02" * 9
+    blob = (E.E8_HEADER.pack(n_groups, 8, 0, 8 * n_groups) + E.E8_LENGTHS.pack(len(freq), 2, 4)
+            + freq + b"\x00" * 6)
+    with pytest.raises(ValueError, match="2\\^31 - 1"):
+        E.decode_e8(blob)

@@ -101,20 +101,3 @@ def test_model_config_detection_reads_transformers5_rope_parameters():
                              num_attention_heads=8, num_hidden_layers=2)
     mc = _detect_model_config(M())
     assert mc["rope_base"] == 500000.0 and mc["head_dim"] == 128 and mc["num_layers"] == 2
-
-
-def test_real_scorer_refuses_logit_softcapping():
-    # Gemma-2 soft-caps its logits (tanh(x / 50) * 50) before the softmax the
-    # reference column-sums; the kernel computes plain causal softmax, so the
-    # wrapper must refuse before any score is accumulated (no GPU reached)
-    from transformers import Gemma2Config, Gemma2ForCausalLM
-    from nexusquant_amd.scoring import real_importance
-    cfg = Gemma2Config(vocab_size=128, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
-                       num_attention_heads=4, num_key_value_heads=2, head_dim=16, max_position_embeddings=256,
-                       attn_logit_softcapping=50.0, sliding_window=64)
-    cfg._attn_implementation = "eager"
-    torch.manual_seed(0)
-    model = Gemma2ForCausalLM(cfg).eval()
-    with pytest.raises(NotImplementedError, match="soft-capping"):
-        real_importance(model, torch.randint(0, 128, (1, 20)))
-    assert model.config._attn_implementation == "eager"
