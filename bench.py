@@ -49,6 +49,24 @@ def synth_layer(gen, device, torch):
     return k, v
 
 
+QUANTIZER_SOURCES = ("nexusquant_amd/csrc/nq_quant.hip", "nexusquant_amd/csrc/nq_quant_kernel.h",
+                     "nexusquant_amd/csrc/nq_rowmath.h", "nexusquant_amd/csrc/nq_common.h",
+                     "include/nexusquant_amd.h")
+
+
+def quantizer_source_hash():
+    """sha256 (16 hex digits) of the quantizer translation unit's sources and the
+    compiler flags: the counter pass's stamp (profiles/quant_c2_traffic.json)."""
+    import hashlib
+    from nexusquant_amd.build import HIPCC_FLAGS
+    h = hashlib.sha256()
+    for rel in QUANTIZER_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(rel.encode() + b"\0" + f.read() + b"\0")
+    h.update(" ".join(HIPCC_FLAGS).encode())
+    return h.hexdigest()[:16]
+
+
 def algorithmic_bytes(levels, is_key, n_tensors):
     """Bytes each launch must move: read bf16, write fp16 recon + syms + cosets + scales."""
     rows = HEADS * SEQ
@@ -108,6 +126,54 @@ def _aux_cache(torch, gen, dev, layers, b, h, s, d, base, sink):
     return ks, vs
 
 
+def _cpu_threads(torch):
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    return torch.get_num_threads()
+
+
+def cpu_leg_evict(ks, vs, rate, key_levels, value_levels, scale_layers, sample_layers=1, importance=None,
+                  protect_boundary=0, label=""):
+    """Tier-A oracle (torch CPU restatement of NexusQuantEvict.compress) on a
+    bounded sample: the key-key scorer on layer 0 (unless importance is given),
+    then mask eviction + quantization of `sample_layers` layers, scaled to the
+    config's layer count (layers are independent given the mask)."""
+    import torch
+    from oracle import torch_ref as T
+    threads = _cpu_threads(torch)
+
+    class Cache:
+        pass
+
+    t_score = 0.0
+    if importance is None:
+        k0 = ks[0].cpu().float()
+        t0 = time.perf_counter()
+        importance = T.score_keykey(k0, 32)
+        t_score = time.perf_counter() - t0
+        del k0
+    c = Cache()
+    c.key_cache = [k.cpu() for k in ks[:sample_layers]]
+    c.value_cache = [v.cpu() for v in vs[:sample_layers]]
+    d = c.key_cache[0].shape[-1]
+    pad = ""
+    if d & (d - 1):
+        # the reference's Hadamard raises for head_dim 96 (hadamard.py:35-36);
+        # time the same work on rows zero-padded to the next power of two, as
+        # the kernel quantizes them
+        D = 1 << (d - 1).bit_length()
+        c.key_cache = [torch.nn.functional.pad(k, (0, D - d)) for k in c.key_cache]
+        c.value_cache = [torch.nn.functional.pad(v, (0, D - d)) for v in c.value_cache]
+        pad = f" (rows zero-padded from {d} to {D}: the reference raises at head_dim {d})"
+    t0 = time.perf_counter()
+    T.evict_compress(c, key_levels, value_levels, rate, importance=importance.cpu())
+    t_evict = time.perf_counter() - t0
+    ms = (t_score + t_evict * scale_layers / sample_layers) * 1e3
+    return {"value": round(ms, 1), "unit": "ms per step", "cores": threads, "kind": "port",
+            "sample": f"{label}key-key scores of layer 0 ({t_score:.2f} s) + mask eviction and quantization of "
+                      f"{sample_layers} layer(s) ({t_evict:.2f} s){pad}, scaled to {scale_layers} layers; Tier-A "
+                      "torch restatement of the reference, same inputs"}
+
+
 def _timed(torch, fn, steps, warmup):
     for _ in range(warmup):
         fn()
@@ -119,9 +185,10 @@ def _timed(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
-def aux_workload(name, steps, warmup, emit=True):
-    """Secondary configs (BASELINE.json configs[2..4]); one JSON line each
-    (emit=False: return the record instead of printing it)."""
+def aux_workload(name, steps, warmup, emit=True, cpu=True):
+    """Secondary configs ([2..4]) and the path's other
+    stages; one JSON line each (emit=False: return the record instead of
+    printing it; cpu=False: skip the bounded Tier-A CPU legs)."""
     import torch
     import nexusquant_amd as nq
     from nexusquant_amd.scoring import score_real_accumulate
@@ -143,6 +210,82 @@ def aux_workload(name, steps, warmup, emit=True):
         out.update(config={"workload": f"device copy of {n} bytes (read {n}, write {n})"},
                    ms_per_step=round(ms, 3), value=round(ms, 3), bytes_read=n, bytes_written=n,
                    copy_gbs=round(2 * n / (ms * 1e-3) / 1e9, 1))
+    elif name == "c1":
+        # one Mistral-7B-shaped layer, quant_only K3V2,
+        # the config the reference runs on its CPU path; here on the GPU and the
+        # Tier-A CPU restatement beside it, same inputs
+        from oracle import torch_ref as T
+        ks, vs = _aux_cache(torch, gen, dev, 1, 1, 8, 2048, 128, 10000.0, False)
+
+        def c1_step():
+            nq.compress_kv_cache(Cache(ks, vs), mode="quant_only", rope_base=10000.0, key_bits=3, value_bits=2)
+        ms = _timed(torch, c1_step, max(steps, 20), warmup) * 1e3
+        threads = _cpu_threads(torch)
+        kc, vc = ks[0].cpu(), vs[0].cpu()
+        reps, t0 = 0, time.perf_counter()
+        while reps < 3 or time.perf_counter() - t0 < 2.0:
+            T.quant_only_compress(Cache([kc], [vc]), 8, 4, rope_base=10000.0)
+            reps += 1
+        cpu_ms = (time.perf_counter() - t0) / reps * 1e3
+        elems = 2 * 8 * 2048 * 128
+        out.update(config={"workload": "quant_only K3V2, one Mistral-7B-shaped layer: K,V fp16 [1, 8, 2048, 128], "
+                           "RoPE base 1e4, no eviction"},
+                   ms_per_step=round(ms, 4), value=round(ms, 4),
+                   gbs_fp16_compressed=round(2 * elems / (ms * 1e-3) / 1e9, 1),
+                   cpu_baseline={"value": round(cpu_ms, 2), "unit": "ms per step", "cores": threads, "kind": "port",
+                                 "gbs_fp16_compressed": round(2 * elems / (cpu_ms * 1e-3) / 1e9, 3),
+                                 "sample": f"the whole config ({reps} runs); Tier-A torch restatement of the "
+                                           "reference, same inputs"},
+                   note="the GPU step is launch-bound at this size (8 MiB of K,V): two fused launches plus host "
+                        "set-up")
+    elif name == "trunc":
+        # truncation (NexusQuantEvictTruncate, pipeline.py:1270-1406): key-key
+        # scores, keep list, then kept rows gathered inside the quantizer with
+        # keys re-rotated at 0..n_kept-1; roofline on the key gather launch
+        from nexusquant_amd.ops import keep_mask, quantize_tensors
+        layers, s = 32, 8192
+        ks, vs = _aux_cache(torch, gen, dev, layers, 1, 8, s, 128, 10000.0, True)
+        comp = nq.NexusQuantEvictTruncate(key_bits=3, value_bits=2, eviction_rate=0.25, sliding_window=32,
+                                          rope_base=10000.0)
+        step_ms = _timed(torch, lambda: comp.compress(Cache(ks, vs)), steps, warmup) * 1e3
+        imp = comp._score_importance(ks[0])
+        _, kept, n_kept_t = keep_mask(imp, 0.25, 32)
+        n_kept = int(n_kept_t[0].item())
+        g = kept[:, :n_kept]
+        stream = torch.cuda.current_stream(dev)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for _ in range(warmup + 1):
+            quantize_tensors(ks, is_key=True, levels=8, rope_base=10000.0, gather=g)
+        for e in evs:
+            quantize_tensors(ks, is_key=True, levels=8, rope_base=10000.0, gather=g, launch_events=e)
+        torch.cuda.synchronize()
+        k_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        rows = layers * 8 * n_kept
+        # read and write each kept row once (fp16), the gather list, and the
+        # merged RoPE table rows (fl(sin - cos), fl(cos + sin); 512 B a position)
+        # of the source and the destination positions, once
+        kbytes = rows * (256 + 256) + 4 * n_kept + 2 * n_kept * 512
+        gbs = kbytes / (k_ms * 1e-3) / 1e9
+        elems = 2 * layers * 8 * s * 128
+        out.update(config={"workload": "truncation, key-key scorer: 32 layers x K,V fp16 [1, 8, 8192, 128], 25% "
+                           "eviction, BOS + last 32 kept, K3V2 on the gathered rows, keys re-rotated at 0..n_kept-1"},
+                   ms_per_step=round(step_ms, 3), value=round(step_ms, 3), n_kept=n_kept,
+                   gbs_fp16_compressed=round(2 * elems / (step_ms * 1e-3) / 1e9, 1),
+                   roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                             "kernel": "quant_rows_kernel<128, 8, key, f16> with a gather list (32 key tensors)",
+                             "algorithmic_bytes_per_launch": kbytes, "launch_ms": round(k_ms, 4)},
+                   note="the step includes one device-to-host read of n_kept (the reference's int return value)")
+        if cpu:
+            from oracle import torch_ref as T
+            threads = _cpu_threads(torch)
+            kc, vc = ks[0].cpu(), vs[0].cpu()
+            t0 = time.perf_counter()
+            T.evict_truncate_compress(Cache([kc], [vc]), 8, 4, 0.25, sliding_window=32, rope_base=10000.0)
+            t1 = time.perf_counter() - t0
+            out["cpu_baseline"] = {"value": round(t1 * layers * 1e3, 1), "unit": "ms per step", "cores": threads,
+                                   "kind": "port", "sample": f"one layer ({t1:.2f} s, scoring included), scaled to "
+                                                             f"{layers} layers; Tier-A torch restatement"}
     elif name == "c3":
         ks, vs = _aux_cache(torch, gen, dev, 32, 4, 8, 8192, 128, 10000.0, True)
         comp = nq.NexusQuantEvict(key_bits=3, value_bits=2, eviction_rate=0.25, sliding_window=32,
@@ -170,6 +313,8 @@ def aux_workload(name, steps, warmup, emit=True):
                    keykey_device_ms=round(kk_dev_ms, 4),
                    keykey_score_gbs=round(4 * 8 * 8192 * 128 * 2 / (kk_dev_ms * 1e-3) / 1e9, 1),
                    gbs_fp16_compressed=round(2 * elems / (step_ms * 1e-3) / 1e9, 1))
+        if cpu:
+            out["cpu_baseline"] = cpu_leg_evict(ks, vs, 0.25, 8, 4, 32, sample_layers=2)
     elif name == "c4":
         s, hq, hkv, d, layers = 8192, 32, 8, 128, 32
         qs = [torch.randn(1, hq, s, d, device=dev, generator=gen).half() for _ in range(layers)]
@@ -208,6 +353,24 @@ def aux_workload(name, steps, warmup, emit=True):
                              "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                              "algorithmic_flops": flops,
                              "note": "two causal QK^T passes per layer, as the kernels run them"})
+        if cpu:
+            # the eager oracle on one layer (per KV group, to bound host memory),
+            # scaled to 32 layers; then eviction of 2 of the 28 quantized layers
+            from oracle import torch_ref as T
+            threads = _cpu_threads(torch)
+            qc, kc = qs[0].cpu(), ks[0].cpu()
+            t0 = time.perf_counter()
+            imp_c = torch.zeros(1, s)
+            for kv in range(hkv):
+                probs = T.eager_attention_probs(qc[:, 4 * kv:4 * kv + 4], kc[:, kv:kv + 1], d ** -0.5)
+                imp_c += probs.float().sum(dim=2).sum(dim=1)
+                del probs
+            t_score = time.perf_counter() - t0
+            leg = cpu_leg_evict(ks[2:], vs[2:], 0.35, 8, 4, layers - 4, sample_layers=2, importance=imp)
+            total = t_score * layers * 1e3 + leg["value"]
+            out["cpu_baseline"] = {"value": round(total, 1), "unit": "ms per step", "cores": threads, "kind": "port",
+                                   "sample": f"eager real-attention oracle on one layer ({t_score:.2f} s) scaled to "
+                                             f"{layers} layers, plus {leg['sample']}"}
     elif name == "c4hook":
         # the whole scoring forward (real_importance) of a 2-layer Llama-shaped
         # model at C4's attention shape, with the model's eager attention and
@@ -241,6 +404,8 @@ def aux_workload(name, steps, warmup, emit=True):
         out.update(config={"workload": f"{desc}, K2V2, {int(rate * 100)}% key-key eviction"},
                    ms_per_step=round(step_ms, 3), value=round(step_ms, 3),
                    gbs_fp16_compressed=round(2 * elems / (step_ms * 1e-3) / 1e9, 1))
+        if cpu:
+            out["cpu_baseline"] = cpu_leg_evict(ks, vs, rate, 4, 4, layers, sample_layers=1)
     elif name in ("decode70b", "decode7b"):
         out.update(decode_workload(name, steps, warmup))
     elif name == "rans":
@@ -442,12 +607,65 @@ def decode_workload(name, steps, warmup):
     gbs = page_bytes / (ev_ms * 1e-3) / 1e9
     shape = (f"batch {batch}, {hq} query heads over {hkv} kv heads, head_dim {d}, {ctx}-token context in "
              f"{block}-token pages, bits {bits}")
+    del plans, outs, ws
+    torch.cuda.empty_cache()
+    fp16 = fp16_decode_comparator(torch, batch, hq, hkv, ctx, d, pools, gen, steps, warmup)
     return dict(config={"workload": f"paged decode attention from compressed pages: {shape}"},
                 ms_per_step=round(ms, 4), value=round(ms, 4), ms_per_layer_events=round(ev_ms, 4),
                 page_bytes_per_layer=page_bytes, fp16_kv_bytes_per_layer=fp16_bytes,
                 roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
-                fp16_equivalent_gbs=round(fp16_bytes / (ev_ms * 1e-3) / 1e9, 1))
+                fp16_equivalent_gbs=round(fp16_bytes / (ev_ms * 1e-3) / 1e9, 1),
+                fp16_sdpa=fp16, speedup_vs_fp16_sdpa=round(fp16["ms_per_layer_events"] / ev_ms, 3))
+
+
+def fp16_decode_comparator(torch, batch, hq, hkv, ctx, d, pools, gen, steps, warmup):
+    """Decode attention over the same context held as a plain fp16 cache: torch's
+    scaled_dot_product_attention with the G = hq / hkv query heads of a kv head
+    as its query length (no mask: a decode token sees the whole context), K and
+    V [batch, hkv, ctx, d]; `pools` layers' caches visited in turn, as for the
+    compressed pages.  The first SDPA backend that takes the shape is used."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    import torch.nn.functional as F
+    dev = torch.device("cuda:0")
+    g = hq // hkv
+    caches = [(torch.randn(batch, hkv, ctx, d, device=dev, generator=gen).half(),
+               (torch.randn(batch, hkv, ctx, d, device=dev, generator=gen) * 0.5).half()) for _ in range(pools)]
+    q = torch.randn(batch, hkv, g, d, device=dev, generator=gen).half()
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in caches]
+    nbytes = 2 * batch * hkv * ctx * d * 2
+    per_backend = {}
+    for backend in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION, SDPBackend.MATH):
+        name = str(backend).split(".")[-1]
+        try:
+            with sdpa_kernel([backend]):
+                F.scaled_dot_product_attention(q, caches[0][0], caches[0][1])
+            torch.cuda.synchronize()
+        except RuntimeError as e:
+            per_backend[name] = {"error": str(e).splitlines()[0][:120]}
+            continue
+
+        def step(events=False):
+            with sdpa_kernel([backend]):
+                for i, (k, v) in enumerate(caches):
+                    if events:
+                        evs[i][0].record(stream)
+                    F.scaled_dot_product_attention(q, k, v)
+                    if events:
+                        evs[i][1].record(stream)
+        _timed(torch, step, 1, warmup)
+        step(events=True)
+        torch.cuda.synchronize()
+        ev_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        per_backend[name] = {"ms_per_layer_events": round(ev_ms, 4), "gbs": round(nbytes / (ev_ms * 1e-3) / 1e9, 1)}
+    del caches
+    torch.cuda.empty_cache()
+    timed = {k: v for k, v in per_backend.items() if "ms_per_layer_events" in v}
+    best = min(timed, key=lambda k: timed[k]["ms_per_layer_events"])
+    return {"backend": best, "ms_per_layer_events": timed[best]["ms_per_layer_events"],
+            "fp16_kv_bytes_per_layer": nbytes, "gbs": timed[best]["gbs"], "backends": per_backend,
+            "note": "torch scaled_dot_product_attention over the fp16 cache of the same shape, fastest backend"}
 
 
 def entropy_stage(ck, cv, torch):
@@ -637,22 +855,26 @@ def temporal_codec_stage(code0, torch, reps=20):
     }
 
 
-def aux_summary(steps=2, warmup=1):
-    """C3, C4, C5a, C5b step times (no CPU leg) for the headline record."""
+def aux_summary(steps=5, warmup=1, cpu=True):
+    """C1, C3, C4, C5a, C5b and truncation step times, with their bounded
+    Tier-A CPU legs, and the fp16 decode comparator, for the headline record."""
     out = {}
-    for name in ("c3", "c4", "c5a", "c5b"):
-        r = aux_workload(name, steps, warmup, emit=False)
+    for name in ("c1", "c3", "c4", "c5a", "c5b", "trunc", "decode70b"):
+        r = aux_workload(name, steps, warmup, emit=False, cpu=cpu)
         out[f"{name}_ms_per_step"] = r["ms_per_step"]
         for k in ("keykey_score_ms", "keykey_device_ms", "keykey_score_gbs", "real_score_ms", "evict_quant_ms",
-                  "attention_with_scores_ms", "gbs_fp16_compressed"):
+                  "attention_with_scores_ms", "gbs_fp16_compressed", "n_kept", "ms_per_layer_events",
+                  "fp16_sdpa"):
             if k in r:
                 out[f"{name}_{k}"] = r[k]
-        if name == "c4":
-            out["c4_real_scorer_roofline"] = r["roofline"]
+        if "roofline" in r:
+            out[f"{name}_roofline"] = r["roofline"]
+        if "cpu_baseline" in r:
+            out[f"{name}_cpu_baseline"] = r["cpu_baseline"]
         import torch
         torch.cuda.empty_cache()
     out["note"] = (f"{steps} timed steps after {warmup} warmup each; workloads and units as "
-                   "bench.py --workload aux prints them")
+                   "bench.py --workload <name> prints them; cpu_baseline entries are bounded samples")
     return out
 
 
@@ -665,7 +887,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the delta + zstd stage and the C3-C5 step times after the headline")
     ap.add_argument("--workload", default="c2",
-                    help="c2 (headline, default), a secondary config: c3, c4, c5a, c5b, aux (all four), "
+                    help="c2 (headline, default), a secondary config: c1, c3, c4, c5a, c5b, trunc (truncation), "
+                         "aux (c1, c3, c4, c5a, c5b, trunc), "
                          "decode70b / decode7b (paged decode attention from compressed pages), rans (GPU "
                          "entropy stage), temporal (temporal_codec container), c4hook (the real scorer's whole scoring "
                          "forward on a 2-layer model), merge (merge eviction), e8mm (fused E8 dequant + matrix product), "
@@ -678,8 +901,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.workload != "c2":
-        for w in (["c3", "c4", "c5a", "c5b"] if args.workload == "aux" else [args.workload]):
-            aux_workload(w, args.steps, args.warmup)
+        for w in (["c1", "c3", "c4", "c5a", "c5b", "trunc"] if args.workload == "aux" else [args.workload]):
+            aux_workload(w, args.steps, args.warmup, cpu=not args.no_cpu_baseline)
         return
 
     import torch
@@ -742,11 +965,21 @@ def main():
     vb = algorithmic_bytes(4, False, LAYERS)
     k_gbs = kb / (k_ms * 1e-3) / 1e9
     v_gbs = vb / (v_ms * 1e-3) / 1e9
-    traffic = None
+    # HBM bytes of the key launch from the committed rocprofv3 counter pass
+    # (profiles/quant_c2_traffic.json), used only when that pass ran on a
+    # library built from the same sources as the one loaded now
+    traffic, traffic_note = None, "no counter pass recorded"
     tpath = os.path.join(ROOT, "profiles", "quant_c2_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("key_launch_bytes")
+            tr = json.load(f)
+        now = quantizer_source_hash()
+        if tr.get("quantizer_source_hash") == now:
+            traffic = tr.get("key_launch_bytes")
+            traffic_note = f"FETCH_SIZE + WRITE_SIZE counters of this quantizer build ({now}), copy-calibrated"
+        else:
+            traffic_note = (f"the committed counter pass ran on quantizer sources {tr.get('quantizer_source_hash')}, "
+                            f"not the current {now}")
 
     result = {
         "metric": METRIC,
@@ -775,6 +1008,7 @@ def main():
             "unit": "GB/s",
             "frac": round(k_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_note,
             "kernel": "quant_rows_kernel<128, 8, key, bf16> (80 key tensors per launch)",
             "algorithmic_bytes_per_launch": kb,
             "launch_ms": round(k_ms, 4),
@@ -792,7 +1026,7 @@ def main():
         gc.unfreeze()
         gc.collect()
         torch.cuda.empty_cache()
-        result["aux"] = aux_summary()
+        result["aux"] = aux_summary(cpu=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
 
 

@@ -570,13 +570,13 @@ __global__ __launch_bounds__(64 * W) void rans_decode_kernel(RansArgs a) {
     }
 }
 
-// exclusive scan of n_words into offset[0..n_chunks]: one block; per pass
-// every thread sums 32 consecutive counts, one block-wide scan of the 1024
-// sums, then every thread writes its 32 offsets
 // Chunk offsets = exclusive prefix sums of the word counts, in three launches
-// over segments of kScanSeg counts.  No workspace: a segment's total, and then
-// its base, live in offset[first chunk of the segment] until the last pass
-// reads that slot and overwrites it with the chunk's own offset.
+// over segments of kScanSeg = 1024 x kScanPer counts (one 1024-thread block
+// each, every thread owning kScanPer consecutive counts): pass 1 sums each
+// segment, pass 2 (one block) scans the segment sums into segment bases, and
+// pass 3 scans within each segment from its base.  No workspace: a segment's
+// total, and then its base, live in offset[first chunk of the segment] until
+// the last pass reads that slot and overwrites it with the chunk's own offset.
 constexpr int kScanPer = 4;                                   // counts per thread
 constexpr int64_t kScanSeg = 1024 * (int64_t)kScanPer;        // counts per segment (one block)
 
@@ -643,7 +643,7 @@ __global__ __launch_bounds__(1024) void rans_seg_base_kernel(int64_t n_chunks, u
     if (threadIdx.x == 0) offset[n_chunks] = carry;
 }
 
-// pass 3: thread t of segment b writes the offsets of its 32 consecutive chunks
+// pass 3: thread t of segment b writes the offsets of its kScanPer consecutive chunks
 __global__ __launch_bounds__(1024) void rans_seg_scan_kernel(const uint32_t* n_words, int64_t n_chunks,
                                                              uint64_t* offset) {
     __shared__ uint64_t lds[33];
