@@ -61,12 +61,15 @@ extern "C" int nq_quantize(const nq_quant_desc* d, void* stream) {
     a.keep_mode = d->keep_mode;
     a.n_tensors = (uint32_t)d->n_tensors;
     a.batch = (uint32_t)d->batch;
-    const uint64_t work = plan_work(a, (uint64_t)(d->seq_out + 63) / 64, d->is_key ? kKeyGroup : kMaxGroup);
+    const uint64_t work = plan_work(a, (uint64_t)(d->seq_out + 63) / 64, d->is_key ? kKeyGroup : kMaxGroup,
+                                    d->is_key && d->gather ? kGatherKeyMinBlocks : kMinBlocks);
     NQ_CHECK_ARG(work + 8 <= max_blocks(256), "nq_quantize: %llu work items exceed the grid limit",
                  (unsigned long long)work);
     hipStream_t s = (hipStream_t)stream;
-    const hipError_t e = a.order ? dispatch_quant_list(d->head_dim, d->levels, d->is_key != 0, d->dtype, a, t, s)
-                                 : dispatch_quant<false>(d->head_dim, d->levels, d->is_key != 0, d->dtype, a, t, s);
+    const bool key = d->is_key != 0;
+    const hipError_t e = a.order    ? dispatch_quant_list(d->head_dim, d->levels, key, d->dtype, a, t, s)
+                         : a.gather ? dispatch_quant_gather(d->head_dim, d->levels, key, d->dtype, a, t, s)
+                                    : dispatch_quant<kSelNone>(d->head_dim, d->levels, key, d->dtype, a, t, s);
     NQ_CHECK_HIP(e);
     return NQ_OK;
 }

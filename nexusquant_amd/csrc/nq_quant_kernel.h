@@ -1,6 +1,6 @@
 // Fused row quantizer for gfx950, the kernel template shared by nq_quant.hip
-// (entry points, plain instantiations) and nq_quant_list.hip (row-list
-// instantiations): inverse RoPE -> Walsh-Hadamard -> per-row
+// (entry points, plain instantiations), nq_quant_list.hip (row-list
+// instantiations) and nq_quant_gather.hip (gather instantiations): inverse RoPE -> Walsh-Hadamard -> per-row
 // scale -> relaxed E8 -> packed codes, and the drop-in reconstruction
 // (inverse Hadamard -> rescale -> forward RoPE -> fp16) in the same pass.
 //
@@ -340,12 +340,14 @@ struct RowOut {
 
 // The row computation of one sub-item: x holds the source row (zero padded,
 // zeroed for evicted rows); cs / sn the source position's RoPE rows for keys.
-// With a gather list, keys load the output position's RoPE rows into cs / sn
-// before the forward rotation.
-template <int D, int L, bool IS_KEY, int DR, bool PAGE>
+// With a gather list the forward rotation takes the output position's rows:
+// co / so for the merged layout, loaded per sub-item for the padded one.
+template <int D, int L, bool IS_KEY, int DR, bool PAGE, bool GATHER>
 __device__ __forceinline__ void quant_row_body(const QuantArgs& a, float (&x)[D / 32][8],
                                                float (&cs)[RopeChunks<D, DR>::value][8],
-                                               float (&sn)[RopeChunks<D, DR>::value][8], int q, const RowOut& o,
+                                               float (&sn)[RopeChunks<D, DR>::value][8],
+                                               const float (&co)[RopeChunks<D, DR>::value][8],
+                                               const float (&so)[RopeChunks<D, DR>::value][8], int q, const RowOut& o,
                                                uint32_t bh, uint32_t t_in, uint32_t t_out, bool active,
                                                const float* lds_rope = nullptr) {
     constexpr int C = D / 32;
@@ -526,14 +528,24 @@ __device__ __forceinline__ void quant_row_body(const QuantArgs& a, float (&x)[D 
     if constexpr (MERGED) {
         // the top inverse Hadamard stage and forward RoPE in one step.  The tables
         // stay live through the quantizer: reloading them here cuts 8 VGPRs but
-        // not the occupancy, and the extra loads cost more than they save.
-        if (a.gather && t_out != t_in)
-            load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, t_out, q, cs, sn);
-        rope_stage_merged<C>(x, cs, sn);
+        // not the occupancy, and the extra loads cost more than they save.  With a
+        // gather list, co / so hold the output position's rows.
+        if constexpr (GATHER) {
+            rope_stage_merged<C>(x, co, so);
+        } else {
+            rope_stage_merged<C>(x, cs, sn);
+        }
     } else if constexpr (IS_KEY) {
-        if (a.gather && t_out != t_in) load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t_out, q, cs, sn);
-        else if constexpr (!PAGE && DR != D) load_rope_row<D, DR, RC>(lds_rope, q, cs, sn);
-        apply_rope<D, DR, RC, false>(x, q, cs, sn);
+        if constexpr (GATHER) {
+            // the padded layout loads the output position's rows here (holding
+            // them for the work item would cost a wave of occupancy)
+            float cg[RC][8], sg[RC][8];
+            load_rope<D, DR, RC>(a.rope_cos, a.rope_sin, t_out, q, cg, sg);
+            apply_rope<D, DR, RC, false>(x, q, cg, sg);
+        } else {
+            if constexpr (!PAGE && DR != D) load_rope_row<D, DR, RC>(lds_rope, q, cs, sn);
+            apply_rope<D, DR, RC, false>(x, q, cs, sn);
+        }
     }
     if (!active) return;
     uint16_t* dst = o.recon + out_row * DR;
@@ -601,13 +613,21 @@ __device__ __forceinline__ void store_evicted_row(const RowOut& o, size_t out_ro
 constexpr int kWaitLgkm0 = 0xc07f;
 constexpr int kWaitVm0 = 0x0f70;
 
-// Keys with the padded RoPE layout (head_dim 96) run 4 waves per SIMD: with
-// fp16 / bf16 input that spills 28-32 bytes and measured 1 % faster on the
-// Phi-3 workload than 3 waves without spills.
-// LIST instantiations take the row list (QuantArgs::order) and no gather list;
-// keeping them apart leaves the other instantiations' registers as they were.
-template <int D, int L, bool IS_KEY, int DT, int DR, bool PAGE = false, bool LIST = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((IS_KEY && !PAGE && DR != D) ? 4 : 1))) void
+// Row selection, one set of instantiations each, so that every path keeps its
+// own register budget: kSelNone (output row t reads source row t, optionally
+// zeroed or filtered by a keep list), kSelList (QuantArgs::order, mask
+// eviction without work on evicted rows) and kSelGather (QuantArgs::gather,
+// truncation: keys hold the source position's RoPE rows for the work item and
+// load the output position's per row).
+constexpr int kSelNone = 0;
+constexpr int kSelList = 1;
+constexpr int kSelGather = 2;
+
+// Keys with the padded RoPE layout (head_dim 96): the row-list instantiation
+// (mask eviction, the Phi-3 workload) fits 4 waves per SIMD without spills
+// (126 VGPRs); the others keep their natural 3 waves rather than spill at 4.
+template <int D, int L, bool IS_KEY, int DT, int DR, bool PAGE = false, int SEL = kSelNone>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((IS_KEY && !PAGE && DR != D && SEL == kSelList) ? 4 : 1))) void
 quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
                                                          const uint64_t* __restrict__ tab_recon,
                                                          const uint64_t* __restrict__ tab_syms,
@@ -617,7 +637,9 @@ quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
                                                          const uint64_t* __restrict__ tab_codes8,
                                                          const uint64_t* __restrict__ tab_scales16) {
     static_assert(!PAGE || DR == D, "page encoding takes power-of-two head dims");
-    static_assert(!(PAGE && LIST), "pages take no row list");
+    static_assert(!PAGE || SEL == kSelNone, "pages take no row selection");
+    constexpr bool LIST = SEL == kSelList;
+    constexpr bool GATHER = SEL == kSelGather;
     constexpr int C = D / 32;
     constexpr int RC = RopeChunks<D, DR>::value;
     constexpr bool MERGED = IS_KEY && DR == D;
@@ -672,7 +694,7 @@ quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
             return;
         }
     } else {
-        if (a.gather) {
+        if constexpr (GATHER) {
             // the host validates the list; clamp anyway so a bad index cannot read out of bounds
             const int32_t gi = a.gather[(size_t)b * a.seq_out + t_out];
             t_in = gi < 0 ? 0u : ((uint32_t)gi >= a.seq_in ? a.seq_in - 1u : (uint32_t)gi);
@@ -684,8 +706,7 @@ quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
     if (a.keep_mode != NQ_KEEP_ZERO) keep = true;  // selected rows are quantized as they are
 
     // Keys: the RoPE rows of the source position, loaded once for the work item
-    // unless each sub-item loads its own (a gather list reloads the output
-    // position's rows after the quantizer; pages rotate at per-page positions).
+    // (pages rotate at per-page positions, loaded per sub-item).
     float cs[RC][8], sn[RC][8];  // cos / sin, or fl(sin - cos) / fl(cos + sin) when MERGED
     auto load_tables = [&](uint32_t pos) {
         if constexpr (MERGED) load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, pos, q, cs, sn);
@@ -731,8 +752,13 @@ quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
         __syncthreads();
         my_rope = s_rope + r * H;
     } else if constexpr (IS_KEY && !PAGE) {
-        if (!a.gather) load_tables(t_in);
+        load_tables(t_in);
     }
+    // With a gather list, merged-layout keys also hold the output position's
+    // rows for the work item (loading them per sub-item measured 11% slower).
+    constexpr bool HOLD_OUT = GATHER && MERGED;
+    float co[HOLD_OUT ? RC : 1][8], so[HOLD_OUT ? RC : 1][8];
+    if constexpr (HOLD_OUT) load_rope_merged<D>(a.rope_cos, a.rope_sin, a.rope_dm, a.rope_dp, t_out, q, co, so);
     if constexpr (ST::pipe) stage_rows(j0);
     for (uint32_t j = j0; j < j1; ++j) {
         const uint32_t tensor = j % a.n_tensors;
@@ -771,8 +797,6 @@ quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
             // position cannot read outside it
             const int32_t pp = gptr<const int32_t>(tab_positions[tensor])[t_in % a.page_tokens];
             load_tables(pp < 0 ? 0u : ((uint32_t)pp >= a.rope_n_pos ? a.rope_n_pos - 1u : (uint32_t)pp));
-        } else if constexpr (IS_KEY && !LDS_ROPE) {
-            if (a.gather) load_tables(t_in);
         }
         RowOut o;
         o.recon = tab_recon ? gptr<uint16_t>(tab_recon[tensor]) : nullptr;
@@ -786,26 +810,35 @@ quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
             o.codes8 = nullptr;
             o.scales16 = nullptr;
         }
-        quant_row_body<D, L, IS_KEY, DR, PAGE>(a, x, cs, sn, q, o, bh, t_in, t_out, active, my_rope);
+        if constexpr (HOLD_OUT)
+            quant_row_body<D, L, IS_KEY, DR, PAGE, GATHER>(a, x, cs, sn, co, so, q, o, bh, t_in, t_out, active, my_rope);
+        else
+            quant_row_body<D, L, IS_KEY, DR, PAGE, GATHER>(a, x, cs, sn, cs, sn, q, o, bh, t_in, t_out, active, my_rope);
     }
 }
 
 // ---------------------------------------------------------------- host ----
 
 // Sub-items per work item, at most max_group, fewer while the grid would fall
-// below 8192 blocks (32 per CU).  Values take 8 (16 and 1 measured slower).
-// Keys take 64: a work item loads its tile's RoPE rows once, so with the
-// tile-fastest order the rows are fetched once per group, 10 times per tile on
-// an 80-layer cache instead of 80.  Sets group, n_groups, hn, n_tiles, work and
-// per_xcd from heads, n_tensors and batch; returns the work item count (the
-// caller rejects counts beyond the grid limit before launching).
+// below min_blocks (8192 = 32 per CU by default).  Values take 8 (16 and 1
+// measured slower).  Keys take 64: a work item loads its tile's RoPE rows
+// once, so with the tile-fastest order the rows are fetched once per group, 10
+// times per tile on an 80-layer cache instead of 80.  Keys with a gather list
+// load two positions' rows per work item and keep larger groups on small
+// caches (4096 blocks: 8% faster on a 32-layer truncation than 8192, 2048 the
+// same; plain and row-list launches measured slower at 4096).  Sets group,
+// n_groups, hn, n_tiles, work and per_xcd from heads, n_tensors and batch;
+// returns the work item count (the caller rejects counts beyond the grid limit
+// before launching).
 constexpr uint32_t kMaxGroup = 8;
 constexpr uint32_t kKeyGroup = 64;
+constexpr uint64_t kMinBlocks = 8192;
+constexpr uint64_t kGatherKeyMinBlocks = 4096;
 
-static uint64_t plan_work(QuantArgs& a, uint64_t tiles, uint32_t max_group) {
+static uint64_t plan_work(QuantArgs& a, uint64_t tiles, uint32_t max_group, uint64_t min_blocks = kMinBlocks) {
     a.hn = a.heads * a.n_tensors;
     uint32_t g = a.hn < max_group ? a.hn : max_group;
-    while (g > 1 && tiles * a.batch * ((a.hn + g - 1) / g) < 8192) g >>= 1;
+    while (g > 1 && tiles * a.batch * ((a.hn + g - 1) / g) < min_blocks) g >>= 1;
     a.group = g;
     a.n_groups = (a.hn + g - 1) / g;
     a.n_tiles = (uint32_t)tiles;
@@ -815,52 +848,55 @@ static uint64_t plan_work(QuantArgs& a, uint64_t tiles, uint32_t max_group) {
     return work;
 }
 
-template <int D, int L, bool K, int DT, int DR, bool PAGE = false, bool LIST = false>
+template <int D, int L, bool K, int DT, int DR, bool PAGE = false, int SEL = kSelNone>
 static hipError_t launch_quant(const QuantArgs& a, const QuantTables& t, hipStream_t s) {
-    hipLaunchKernelGGL((quant_rows_kernel<D, L, K, DT, DR, PAGE, LIST>), dim3(a.per_xcd * 8u), dim3(256), 0, s, a,
+    hipLaunchKernelGGL((quant_rows_kernel<D, L, K, DT, DR, PAGE, SEL>), dim3(a.per_xcd * 8u), dim3(256), 0, s, a,
                        t.src, t.recon, t.syms, t.cosets, t.scales, t.positions, t.codes8, t.scales16);
     return hipGetLastError();
 }
 
-template <int D, int L, bool K, int DR, bool LIST>
+template <int D, int L, bool K, int DR, int SEL>
 static hipError_t dispatch_dtype(int dt, const QuantArgs& a, const QuantTables& t, hipStream_t s) {
     switch (dt) {
-        case NQ_F16: return launch_quant<D, L, K, NQ_F16, DR, false, LIST>(a, t, s);
-        case NQ_BF16: return launch_quant<D, L, K, NQ_BF16, DR, false, LIST>(a, t, s);
-        default: return launch_quant<D, L, K, NQ_F32, DR, false, LIST>(a, t, s);
+        case NQ_F16: return launch_quant<D, L, K, NQ_F16, DR, false, SEL>(a, t, s);
+        case NQ_BF16: return launch_quant<D, L, K, NQ_BF16, DR, false, SEL>(a, t, s);
+        default: return launch_quant<D, L, K, NQ_F32, DR, false, SEL>(a, t, s);
     }
 }
 
-template <int D, int L, int DR, bool LIST>
+template <int D, int L, int DR, int SEL>
 static hipError_t dispatch_key(bool key, int dt, const QuantArgs& a, const QuantTables& t, hipStream_t s) {
-    return key ? dispatch_dtype<D, L, true, DR, LIST>(dt, a, t, s) : dispatch_dtype<D, L, false, DR, LIST>(dt, a, t, s);
+    return key ? dispatch_dtype<D, L, true, DR, SEL>(dt, a, t, s) : dispatch_dtype<D, L, false, DR, SEL>(dt, a, t, s);
 }
 
-template <int D, int DR, bool LIST>
+template <int D, int DR, int SEL>
 static hipError_t dispatch_levels(int L, bool key, int dt, const QuantArgs& a, const QuantTables& t, hipStream_t s) {
     switch (L) {
-        case 2: return dispatch_key<D, 2, DR, LIST>(key, dt, a, t, s);
-        case 4: return dispatch_key<D, 4, DR, LIST>(key, dt, a, t, s);
-        case 8: return dispatch_key<D, 8, DR, LIST>(key, dt, a, t, s);
-        default: return dispatch_key<D, 16, DR, LIST>(key, dt, a, t, s);
+        case 2: return dispatch_key<D, 2, DR, SEL>(key, dt, a, t, s);
+        case 4: return dispatch_key<D, 4, DR, SEL>(key, dt, a, t, s);
+        case 8: return dispatch_key<D, 8, DR, SEL>(key, dt, a, t, s);
+        default: return dispatch_key<D, 16, DR, SEL>(key, dt, a, t, s);
     }
 }
 
 // Launch of one nq_quantize call on the already planned arguments, by head_dim.
-template <bool LIST>
+template <int SEL>
 static hipError_t dispatch_quant(int head_dim, int L, bool key, int dt, const QuantArgs& a, const QuantTables& t,
                                  hipStream_t s) {
     switch (head_dim) {
-        case 64: return dispatch_levels<64, 64, LIST>(L, key, dt, a, t, s);
-        case 96: return dispatch_levels<128, 96, LIST>(L, key, dt, a, t, s);
-        case 128: return dispatch_levels<128, 128, LIST>(L, key, dt, a, t, s);
-        default: return dispatch_levels<256, 256, LIST>(L, key, dt, a, t, s);
+        case 64: return dispatch_levels<64, 64, SEL>(L, key, dt, a, t, s);
+        case 96: return dispatch_levels<128, 96, SEL>(L, key, dt, a, t, s);
+        case 128: return dispatch_levels<128, 128, SEL>(L, key, dt, a, t, s);
+        default: return dispatch_levels<256, 256, SEL>(L, key, dt, a, t, s);
     }
 }
 
-// The row-list instantiations, compiled in their own translation unit
-// (nq_quant_list.hip) so that the two sets build in parallel.
+// The row-list and gather instantiations, each compiled in a translation unit
+// of its own (nq_quant_list.hip, nq_quant_gather.hip) so the sets build in
+// parallel.
 hipError_t dispatch_quant_list(int head_dim, int L, bool key, int dt, const QuantArgs& a, const QuantTables& t,
                                hipStream_t s);
+hipError_t dispatch_quant_gather(int head_dim, int L, bool key, int dt, const QuantArgs& a, const QuantTables& t,
+                                 hipStream_t s);
 
 }  // namespace nq

@@ -6,7 +6,7 @@ namespace nq {
 
 hipError_t dispatch_quant_list(int head_dim, int L, bool key, int dt, const QuantArgs& a, const QuantTables& t,
                                hipStream_t s) {
-    return dispatch_quant<true>(head_dim, L, key, dt, a, t, s);
+    return dispatch_quant<kSelList>(head_dim, L, key, dt, a, t, s);
 }
 
 }  // namespace nq
