@@ -654,12 +654,22 @@ quant_rows_kernel(QuantArgs a, const uint64_t* __restrict__ tab_src,
     // at a time cover consecutive tiles of one group, so they stream a few
     // contiguous regions of the group's tensors instead of one small piece of
     // every tensor (measured: 6% faster on the 80-layer 128K cache, and less
-    // sensitive to where the buffers land in physical memory).  The whole block
-    // exits together.
+    // sensitive to where the buffers land in physical memory).  Keys with a
+    // gather list take the group fastest instead: their groups are small and
+    // each work item loads two positions' RoPE rows, which the blocks of one
+    // tile then share in the XCD's L2 (the tile-fastest order re-fetched them
+    // per group, 0.3 GB of a truncation launch's 0.7 GB of reads; 5% faster).
+    // The whole block exits together.
     const uint32_t w = (blockIdx.x & 7u) * a.per_xcd + (blockIdx.x >> 3);
     if (w >= a.work) return;
-    const uint32_t tile = w % a.n_tiles;
-    const uint32_t rest = w / a.n_tiles;
+    uint32_t tile, rest;
+    if constexpr (GATHER && IS_KEY) {
+        tile = w / (a.batch * a.n_groups);
+        rest = w - tile * (a.batch * a.n_groups);
+    } else {
+        tile = w % a.n_tiles;
+        rest = w / a.n_tiles;
+    }
     const uint32_t b = rest % a.batch;
     const uint32_t grp = rest / a.batch;
     const uint32_t j0 = grp * a.group;
