@@ -125,25 +125,26 @@ def test_gather_truncation_path_bitexact(d):
         assert_bitexact(rec, cd, ref, L)
 
 
-@pytest.mark.parametrize("d", [128, 64, 256, 96])
-def test_gather_multi_tensor_groups_bitexact(d):
+@pytest.mark.parametrize("d,dt,L", [(128, torch.float16, 8), (64, torch.float16, 8), (256, torch.float16, 8),
+                                    (96, torch.float16, 8), (128, torch.bfloat16, 16), (128, torch.float32, 4)])
+def test_gather_multi_tensor_groups_bitexact(d, dt, L):
     # 52 key tensors [2, 8, 700, d] with a different gather list per batch row:
     # enough work that each work item takes two (head, tensor) sub-items, so
     # keys reuse both positions' RoPE rows across sub-items
-    print(f"[gpu] gather groups d={d}", flush=True)
+    print(f"[gpu] gather groups d={d} {dt} L={L}", flush=True)
     ops = _ops()
     n_t, b, h, s, s_out = 52, 2, 8, 700, 640
-    xs = [_inputs((b, h, s, d), torch.float16, seed=100 + i) for i in range(n_t)]
+    xs = [_inputs((b, h, s, d), dt, seed=100 + i) for i in range(n_t)]
     kept = np.stack([np.sort(np.random.default_rng(7 + i).choice(s, s_out, replace=False))
                      for i in range(b)]).astype(np.int32)
     g = torch.from_numpy(kept).to(DEV)
-    rec, cds = ops.quantize_tensors([x.to(DEV) for x in xs], is_key=True, levels=8, codes=True, gather=g)
+    rec, cds = ops.quantize_tensors([x.to(DEV) for x in xs], is_key=True, levels=L, codes=True, gather=g)
     torch.cuda.synchronize()
-    ref = spec_tensor(torch.cat(xs, 1).float().numpy(), 8, True, 10000.0, gather=kept)
+    ref = spec_tensor(torch.cat(xs, 1).float().numpy(), L, True, 10000.0, gather=kept)
     D = cds[0].padded_dim
     assert_same_fp16(torch.cat(rec, 1).cpu().numpy().reshape(-1, d), ref["recon"])
-    syms = torch.cat([c.syms for c in cds], 1).cpu().numpy().reshape(-1, D // 8 * C.bits_for(8))
-    assert np.array_equal(syms, C.pack_symbols(ref["sym"], 8))
+    syms = torch.cat([c.syms for c in cds], 1).cpu().numpy().reshape(-1, D // 8 * C.bits_for(L))
+    assert np.array_equal(syms, C.pack_symbols(ref["sym"], L))
     cos = torch.cat([c.cosets for c in cds], 1).cpu().numpy().reshape(-1, D // 64)
     assert np.array_equal(cos, C.pack_cosets(ref["coset"]))
     assert np.array_equal(torch.cat([c.scales for c in cds], 1).cpu().numpy().reshape(-1), ref["scale"])
