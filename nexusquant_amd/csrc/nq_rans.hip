@@ -150,25 +150,35 @@ struct RansArgs {
 __host__ __device__ __forceinline__ int64_t rans_stride(int chunk) { return ((int64_t)chunk + 2 + 3) & ~(int64_t)3; }
 
 // One lane per chunk, one wave per block (so the chunks spread over every CU).
-// A chunk is a chain of dependent state updates, so its time is the chain's
-// latency per symbol: nothing but the update itself may sit on it.
-//  - The codes of a whole chunk whose length is a multiple of 128 are read
-//    128 at a time (eight 16-byte loads per lane), one group ahead, from the
+// A chunk is a chain of dependent state updates: with few chunks the time is
+// the chain's latency per symbol, with many (a whole role's codes as one
+// stream) the instructions per symbol, so both the chain and the count are
+// kept short.
+//  - The codes of a whole chunk whose length is a multiple of 64 are read
+//    64 at a time (four 16-byte loads per lane), one group ahead, from the
 //    chunk's end backwards; other chunks read 16 at a time.
-//  - For every 16 codes, all 16 table entries (f, cf, 1/f, and the renorm
-//    bound f * 2^20 - 1) are looked up before the first of them is coded, so
-//    no LDS latency lies on the chain.
-//  - Emitted words collect in a 64-bit buffer and leave in 8-byte stores;
-//    nothing inside a group of 128 waits on memory.
+//  - The table is indexed by the raw code byte (256 entries, the symbol
+//    mapping and its clamp folded in), so a lookup is one byte select and the
+//    LDS reads; entries (f, cf, 1/f, and the renorm bound f * 2^20 - 1) are
+//    looked up 8 codes ahead of the chain, so no LDS latency lies on it and
+//    the lookahead costs 40 VGPRs (16 codes ahead took 80 and a wave of
+//    occupancy).
+//  - Emitted words go to a per-lane LDS ring (below) and leave in 32-byte
+//    blocks; nothing inside a group of 64 waits on memory.
 // Per-symbol encoder constants.  rcp is 1/f rounded up in fp64: for x < f 2^20
 // it gives q = trunc(x * rcp) = floor(x / f) exactly (x * rcp exceeds x / f by
 // at most 2^-32, less than the 1/f gap to the next integer, and the rounded
 // product stays below it), so the update q M + (x - q f) + cf is
 // q (M - f) + x + cf with a 24-bit multiply and no correction.
-struct __attribute__((aligned(16))) RansEnc {
-    uint32_t xmax, mmf, cf, pad;  // renorm bound f 2^20 - 1, M - f, cumulative frequency
+struct RansEnc {
+    uint32_t xmax, mmf, cf;  // renorm bound f 2^20 - 1, M - f, cumulative frequency
     double rcp;
-    double pad2;
+};
+// In LDS the integer fields and 1/f sit in two arrays (16- and 8-byte
+// entries): the code bytes in use (around 0 and 255) then fall in distinct
+// banks, where 32-byte entries put bytes 8 apart on the same banks.
+struct __attribute__((aligned(16))) RansEncInt {
+    uint32_t xmax, mmf, cf, pad;
 };
 
 __device__ __forceinline__ double rcp_up(uint32_t f) {
@@ -177,109 +187,148 @@ __device__ __forceinline__ double rcp_up(uint32_t f) {
     return r;
 }
 
-__global__ __launch_bounds__(64) void rans_encode_kernel(RansArgs a) {
-    __shared__ RansEnc tab[kRansMaxAlpha];
-    if (threadIdx.x == 0) {
-        uint32_t acc = 0;
-        for (int s = 0; s < a.alphabet; ++s) {
-            const uint32_t f = a.freq[s];
-            RansEnc e;
-            // state >= f * 2^20 as a 32-bit test: f * 2^20 - 1 wraps to 2^32 - 1
-            // at f = 4096 (never renormalise); f = 0 (not valid input) gives 0
-            e.xmax = f ? (f << 20) - 1u : 0u;
-            e.mmf = kRansM - f;
-            e.cf = acc;
-            e.pad = 0;
-            e.rcp = f ? rcp_up(f) : 0.0;
-            e.pad2 = 0.0;
-            tab[s] = e;
-            acc += f;
+// Emitted words go to a per-lane ring of 32 words in LDS, written at the
+// lane's current slot on every symbol and kept (the slot moves down) only when
+// the step emitted one: no branch and no buffer shuffling per symbol.  After
+// every 16 symbols a lane with 16 or more words pending stores the oldest 16
+// (32 bytes, already in stream order) below its previous ones; at most 31 are
+// ever pending, so the slot written next never holds an unstored word.
+constexpr int kEncRingStride = 18;  // dwords per lane: 32 words + 8 bytes, 8-byte aligned rows
+constexpr int64_t kEncWideChunks = 256 * 2 * 4 * 64;  // two 4-wave blocks per CU
+constexpr int kEncGroup = 64;  // codes per load group of a whole chunk (read one group ahead)
+
+// W waves per block share the byte table: one wave for streams of few chunks
+// (so they spread over every CU), four when there are chunks for at least two
+// such blocks per CU (LDS then holds more waves per CU).
+template <int W>
+__global__ __launch_bounds__(64 * W) void rans_encode_kernel(RansArgs a) {
+    // the encoder constants of every code byte value: byte b (a signed code c)
+    // codes symbol c + L, or c / 2 + L / 2 without half-integer points; bytes
+    // outside [-L, L] (not valid input) take the nearest valid symbol, so any
+    // byte stays inside the table
+    __shared__ RansEncInt tab_i[256];
+    __shared__ double tab_r[256];
+    __shared__ uint32_t fcf[kRansMaxAlpha];  // f | cf << 16 per symbol
+    __shared__ __align__(16) uint32_t ring_all[64 * W * kEncRingStride];
+    if (threadIdx.x < 64) {
+        // cumulative frequencies: an exclusive scan over the first wave (alphabet <= 64)
+        const int t = threadIdx.x;
+        const uint32_t f = t < a.alphabet ? a.freq[t] : 0u;
+        uint32_t inc = f;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t v = __shfl_up(inc, o, 64);
+            inc += t >= o ? v : 0u;
         }
+        if (t < a.alphabet) fcf[t] = f | (inc - f) << 16;
     }
     __syncthreads();
-    const int64_t ch = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    for (int b = threadIdx.x; b < 256; b += 64 * W) {
+        const int c = (int)(int8_t)(uint8_t)b;
+        const int sym = min(max(a.has_half ? c + a.L : (c >> 1) + a.L / 2, 0), a.alphabet - 1);
+        const uint32_t f = fcf[sym] & 0xffffu, cf = fcf[sym] >> 16;
+        RansEncInt e;
+        // state >= f * 2^20 as a 32-bit test: f * 2^20 - 1 wraps to 2^32 - 1
+        // at f = 4096 (never renormalise); f = 0 (not valid input) gives 0
+        e.xmax = f ? (f << 20) - 1u : 0u;
+        e.mmf = kRansM - f;
+        e.cf = cf;
+        e.pad = 0;
+        tab_i[b] = e;
+        tab_r[b] = f ? rcp_up(f) : 0.0;
+    }
+    __syncthreads();
+    const int64_t ch = (int64_t)blockIdx.x * (64 * W) + threadIdx.x;
     if (ch >= a.n_chunks) return;
     const int64_t c0 = ch * a.chunk;
     const int64_t c1 = c0 + a.chunk < a.n ? c0 + a.chunk : a.n;
     uint16_t* const end = a.scratch + (ch + 1) * rans_stride(a.chunk);
-    uint16_t* out = end;  // next 4-word group goes just below
-    uint64_t buf = 0;
-    uint32_t nbuf = 0;
+    uint16_t* out = end;  // next 16-word block goes just below
+    uint16_t* const ring = reinterpret_cast<uint16_t*>(ring_all + threadIdx.x * kEncRingStride);
+    int wp = -1;  // the lane's next free slot (mod 32); counts down as words are emitted
+    int fl = 0;   // slot one above the oldest pending word: slots wp + 1 .. fl - 1 are pending
     uint32_t state = kRansL;
-    // the symbol of code byte k without a branch: the byte arithmetically
-    // shifted right by 1 when there are no half-integer points (c / 2, c even),
-    // plus L or L / 2
-    const int sym_shift = a.has_half ? 24 : 25;
-    const int sym_off = a.has_half ? a.L : a.L / 2;
     auto lookup = [&](uint32_t word, int k) -> RansEnc {
-        int s = ((int)(word << (24 - 8 * k)) >> sym_shift) + sym_off;
-        s = min(max(s, 0), a.alphabet - 1);  // codes outside [-L, L] are not valid input
-        return tab[s];
+        const uint32_t b = (word >> (8 * k)) & 255u;
+        const RansEncInt t = tab_i[b];
+        return RansEnc{t.xmax, t.mmf, t.cf, tab_r[b]};
     };
     auto code_one = [&](const RansEnc& e) {
         // at most one word: state >> 16 < 2^16 <= f << 20
         const bool ren = state > e.xmax;
-        const uint32_t wd = state & 0xffffu;
+        // off the chain: the low word goes to the current slot, kept if emitted
+        ring[wp & 31] = (uint16_t)state;
+        wp -= ren ? 1 : 0;
         state = ren ? state >> 16 : state;
         const uint32_t q = (uint32_t)((double)state * e.rcp);  // floor(state / f), q < 2^20
         state = __umul24(q, e.mmf) + state + e.cf;             // q (M - f) < 2^32
-        // off the chain: the word joins the buffer, a full buffer leaves
-        buf = ren ? (buf << 16) | wd : buf;
-        nbuf += ren ? 1u : 0u;
-        if (nbuf == 4) {
-            out -= 4;
-            *reinterpret_cast<uint64_t*>(out) = buf;
-            nbuf = 0;
+    };
+    // after 16 symbols: store the oldest 16 pending words (slots fl - 16 .. fl - 1,
+    // ascending = stream order) below the stored ones
+    auto flush16 = [&]() {
+        if (fl - wp > 16) {
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(ring + ((fl - 16) & 31));
+            uint2 w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) w[k] = *reinterpret_cast<const uint2*>(src + 2 * k);
+            out -= 16;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) *reinterpret_cast<uint2*>(out + 4 * k) = w[k];
+            fl -= 16;
         }
     };
-    // the 16 codes of one 16-byte block, highest first
+    // the 16 codes of one 16-byte block, highest first, 8 table entries at a time
     auto code16 = [&](uint4 v) {
         const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-        RansEnc e[16];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) e[k] = lookup(wv[k >> 2], k & 3);
+        for (int h = 1; h >= 0; --h) {
+            RansEnc e[8];
 #pragma unroll
-        for (int k = 15; k >= 0; --k) code_one(e[k]);
+            for (int k = 0; k < 8; ++k) e[k] = lookup(wv[2 * h + (k >> 2)], k & 3);
+#pragma unroll
+            for (int k = 7; k >= 0; --k) code_one(e[k]);
+        }
     };
-    if (a.chunk % 128 == 0 && c1 - c0 == a.chunk) {
+    if (a.chunk % kEncGroup == 0 && c1 - c0 == a.chunk) {
+        constexpr int G = kEncGroup / 16;  // 16-byte loads per group
         const uint4* p = reinterpret_cast<const uint4*>(a.codes + c0);
-        int sb = a.chunk / 128 - 1;
-        uint4 cur[8];
+        int sb = a.chunk / kEncGroup - 1;
+        uint4 cur[G];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            cur[j] = p[8 * sb + j];
+        for (int j = 0; j < G; ++j) {
+            cur[j] = p[G * sb + j];
             // keeps the first group's loads apart from the loop's, so they are not
             // merged into one load at the loop top
             asm("" : "+v"(cur[j].x), "+v"(cur[j].y), "+v"(cur[j].z), "+v"(cur[j].w));
         }
-        // the table entries of the next 16 codes are looked up between the
-        // current 16 codes' chain steps, where they fill its dependency stalls
-        RansEnc e[16];
+        // table entries run 8 codes ahead of the chain: the entry of the code
+        // 8 places later is looked up right after each code, where it fills the
+        // chain's dependency stalls (e[k & 7] holds code k's entry when it is coded)
+        RansEnc e[8];
         {
-            const uint32_t wv[4] = {cur[7].x, cur[7].y, cur[7].z, cur[7].w};
+            const uint32_t wv[4] = {cur[G - 1].x, cur[G - 1].y, cur[G - 1].z, cur[G - 1].w};
 #pragma unroll
-            for (int k = 0; k < 16; ++k) e[k] = lookup(wv[k >> 2], k & 3);
+            for (int k = 8; k < 16; ++k) e[k & 7] = lookup(wv[k >> 2], k & 3);
         }
         for (; sb >= 0; --sb) {
             const int nb = sb > 0 ? sb - 1 : 0;  // the last pass reloads group 0 (in bounds, unused)
-            uint4 nxt[8];
+            uint4 nxt[G];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) nxt[j] = p[8 * nb + j];
+            for (int j = 0; j < G; ++j) nxt[j] = p[G * nb + j];
 #pragma unroll
-            for (int j = 7; j >= 0; --j) {
-                const uint4 nv = j > 0 ? cur[j - 1] : nxt[7];
+            for (int j = G - 1; j >= 0; --j) {
+                const uint32_t cw[4] = {cur[j].x, cur[j].y, cur[j].z, cur[j].w};
+                const uint4 nv = j > 0 ? cur[j - 1] : nxt[G - 1];
                 const uint32_t nw[4] = {nv.x, nv.y, nv.z, nv.w};
-                RansEnc en[16];
 #pragma unroll
                 for (int k = 15; k >= 0; --k) {
-                    code_one(e[k]);
-                    en[k] = lookup(nw[k >> 2], k & 3);
+                    code_one(e[k & 7]);
+                    e[k & 7] = k >= 8 ? lookup(cw[(k - 8) >> 2], (k - 8) & 3) : lookup(nw[(k + 8) >> 2], (k + 8) & 3);
                 }
-#pragma unroll
-                for (int k = 0; k < 16; ++k) e[k] = en[k];
+                flush16();
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
+            for (int j = 0; j < G; ++j) cur[j] = nxt[j];
         }
     } else {
         // 16-byte blocks [b, b + 16) from the one holding c1 - 1 down to the one holding c0
@@ -306,22 +355,19 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(RansArgs a) {
                 const uint32_t wv[4] = {cur.x, cur.y, cur.z, cur.w};
                 for (int k = k_hi; k >= k_lo; --k) code_one(lookup(wv[k >> 2], k & 3));
             }
+            flush16();
             cur = nxt;
         }
     }
     // the final state, high word last (the decoder reads it first)
-    for (int k = 0; k < 2; ++k) {
-        buf = (buf << 16) | (k ? state >> 16 : state & 0xffffu);
-        if (++nbuf == 4) {
-            out -= 4;
-            *reinterpret_cast<uint64_t*>(out) = buf;
-            nbuf = 0;
-        }
-    }
-    // the last 0..3 words, just below the stored groups: the earliest emitted
-    // (the buffer's highest) at the highest address
-    for (uint32_t k = 0; k < nbuf; ++k) out[-1 - (int)k] = (uint16_t)(buf >> (16 * (nbuf - 1 - k)));
-    a.n_words[ch] = (uint32_t)(end - out) + nbuf;
+    ring[wp & 31] = (uint16_t)state;
+    --wp;
+    ring[wp & 31] = (uint16_t)(state >> 16);
+    --wp;
+    // the 0..17 pending words, just below the stored blocks in stream order
+    const int pend = fl - wp - 1;
+    for (int k = 0; k < pend; ++k) out[-1 - k] = ring[(fl - 1 - k) & 31];
+    a.n_words[ch] = (uint32_t)(end - out) + (uint32_t)pend;
 }
 
 // copy each chunk's right-aligned words to its compacted offset.
@@ -744,7 +790,10 @@ extern "C" int nq_rans_encode(const int8_t* codes, int64_t n, int32_t levels, in
         a.L = levels;
         a.has_half = has_half;
         a.alphabet = alphabet;
-        hipLaunchKernelGGL(rans_encode_kernel, dim3((uint32_t)((n_chunks + 63) / 64)), dim3(64), 0, s, a);
+        if (n_chunks >= kEncWideChunks)
+            hipLaunchKernelGGL(rans_encode_kernel<4>, dim3((uint32_t)((n_chunks + 255) / 256)), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(rans_encode_kernel<1>, dim3((uint32_t)((n_chunks + 63) / 64)), dim3(64), 0, s, a);
         const uint32_t n_seg = (uint32_t)((n_chunks + kScanSeg - 1) / kScanSeg);
         hipLaunchKernelGGL(rans_seg_sum_kernel, dim3(n_seg), dim3(1024), 0, s, n_words, n_chunks, offset);
         hipLaunchKernelGGL(rans_seg_base_kernel, dim3(1), dim3(1024), 0, s, n_chunks, offset);
