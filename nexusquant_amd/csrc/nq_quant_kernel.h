@@ -1,8 +1,9 @@
 // Fused row quantizer for gfx950, the kernel template shared by nq_quant.hip
 // (entry points, plain instantiations), nq_quant_list.hip (row-list
-// instantiations) and nq_quant_gather.hip (gather instantiations): inverse RoPE -> Walsh-Hadamard -> per-row
-// scale -> relaxed E8 -> packed codes, and the drop-in reconstruction
-// (inverse Hadamard -> rescale -> forward RoPE -> fp16) in the same pass.
+// instantiations) and nq_quant_gather.hip (gather instantiations): inverse
+// RoPE -> Walsh-Hadamard -> per-row scale -> relaxed E8 -> packed codes, and
+// the drop-in reconstruction (inverse Hadamard -> rescale -> forward RoPE ->
+// fp16) in the same pass.
 //
 // Layout: one row (one head vector of one token, D <= 256 padded coordinates)
 // is owned by a quad of 4 lanes.  Lane q of the quad holds C = D/32 chunks of 8
@@ -617,8 +618,9 @@ constexpr int kWaitVm0 = 0x0f70;
 // own register budget: kSelNone (output row t reads source row t, optionally
 // zeroed or filtered by a keep list), kSelList (QuantArgs::order, mask
 // eviction without work on evicted rows) and kSelGather (QuantArgs::gather,
-// truncation: keys hold the source position's RoPE rows for the work item and
-// load the output position's per row).
+// truncation: keys hold the source position's RoPE rows for the work item, and
+// the output position's too where the merged layout applies; the padded layout
+// loads the output rows per sub-item).
 constexpr int kSelNone = 0;
 constexpr int kSelList = 1;
 constexpr int kSelGather = 2;
