@@ -154,3 +154,14 @@ def test_real_scorer_window_and_softcap_match_transformers_eager(golden, name):
     # the window and the cap change the result: without them it differs
     plain = T.score_real_from_qk(q, k, float(g["scaling"][0]))
     assert not np.allclose(plain.numpy(), g["importance"], rtol=0, atol=1e-4)
+    # the window's edge is pinned: one key more (j >= i - W, a window of W + 1)
+    # does not reproduce the fixture
+    if any(w is not None for w in win):
+        wider = [w + 1 if w is not None else None for w in win]
+        off = T.score_real_from_qk(q, k, float(g["scaling"][0]), windows=wider, softcaps=cap)
+        assert not np.array_equal(off.numpy(), g["importance"])
+    # and so is the cap's value
+    if any(c is not None for c in cap):
+        other = [c * 1.01 if c is not None else None for c in cap]
+        off = T.score_real_from_qk(q, k, float(g["scaling"][0]), windows=win, softcaps=other)
+        assert not np.array_equal(off.numpy(), g["importance"])
