@@ -94,7 +94,8 @@ def test_offsets_across_scan_segments_and_compact_strides(has_half, n_chunks):
     second group; chunks on either side of segment boundaries and at both
     ends are checked against the restated encoder, and offsets against the
     cumulative sums of those per-chunk word counts.  At 197,609 chunks the
-    decoder runs six waves per block, the last block partly empty."""
+    decoder runs six waves per block and the encoder four, the last block of
+    each partly empty; 32-code chunks take the encoder's 16-code path."""
     from nexusquant_amd.entropy import rans_decode, rans_encode
     print(f"[gpu] rans offsets across scan segments has_half={has_half} n_chunks={n_chunks}", flush=True)
     chunk, levels = 32, 8
