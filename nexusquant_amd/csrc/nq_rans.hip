@@ -460,14 +460,18 @@ __global__ __launch_bounds__(256) void rans_compact_kernel(const uint16_t* scrat
 // The chain per symbol is one table read and a multiply-add; everything else
 // is kept off it:
 //  - each lane's stream words pass through a private 64-word ring in LDS.  At
-//    the start of every 16 symbols a lane writes the 16 words it loaded one
+//    the start of every 16 symbols a lane writes the words it loaded one
 //    step earlier and, if fewer than 32 unread words remain, loads the next
-//    16, so no load is waited on inside a step and the ring always holds the
-//    (at most 16) words a step reads;
+//    batch (16 words in one-wave blocks, 32 in the wide blocks, which then
+//    load half as often), so no load is waited on inside a step and the ring
+//    always holds the (at most 16) words a step reads.  A wave whose lanes can
+//    only reach words inside the stream loads without the end-of-stream test,
+//    on a branch the whole wave takes;
 //  - the word a renormalisation would take is read from the ring alongside
 //    the table entry, before it is known to be needed;
-//  - 16 decoded codes leave in one 16-byte store, issued a step late so that
-//    the next wait on loads does not also wait for it.
+//  - 16 decoded codes leave in one 16-byte store, issued a step late and after
+//    that step's loads, so that the next wait on loads does not also wait for
+//    it.
 constexpr int kRingStride = 34;  // dwords per lane: 64 words + 4 bytes, 8-byte aligned rows
 // the ring is written in 8-byte groups and read in 16-bit words: both through
 // may_alias types, so the compiler keeps every read after the writes it follows
@@ -526,6 +530,15 @@ __global__ __launch_bounds__(64 * W) void rans_decode_kernel(RansArgs a) {
         for (uint64_t j = 0; g + j < total; ++j) v |= (uint64_t)a.words[g + j] << (16 * j);
         return v;
     };
+    // Words this lane can load: rpos never passes the chunk's end (renormalising
+    // stops there) nor 2 + n_sym, and a batch is loaded only while fewer than 32
+    // words are unread, so every load stays below g0 + rmax + 32 + kBatch (and
+    // the first 32 words).  A wave all of whose lanes stay inside the stream
+    // skips the per-group end test.
+    constexpr uint32_t kBatch = W > 1 ? 32 : 16;  // words per prefetch
+    const uint32_t rmax = (uint32_t)(w0 & 3) + (len < n_sym + 2 ? len : n_sym + 2);
+    const uint64_t lane_end = g0 + (rmax + 32 + kBatch > 32 ? rmax + 32 + kBatch : 32);
+    const bool wave_inside = __builtin_amdgcn_ballot_w64(lane_end > total) == 0;
     auto put_group = [&](uint32_t k, uint64_t v) { *reinterpret_cast<ring_group_t*>(ring + 2 * (k & 15u)) = v; };
     uint32_t written = 8;  // groups in the ring: the first 8, all loads issued before the first write
     {
@@ -563,21 +576,28 @@ __global__ __launch_bounds__(64 * W) void rans_decode_kernel(RansArgs a) {
         nw = ring16[rpos & 63u];
         return code;
     };
-    uint64_t pf[4];        // groups loaded for the next step
+    constexpr int PG = kBatch / 4;
+    uint64_t pf[PG];       // groups loaded for the next step
     bool inflight = false;
     auto refill = [&]() {
         if (inflight) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) put_group(written + j, pf[j]);
-            written += 4;
+            for (int j = 0; j < PG; ++j) put_group(written + j, pf[j]);
+            written += PG;
             inflight = false;
             nw = ring16[rpos & 63u];  // its slot may have just been written
         }
     };
     auto prefetch = [&]() {
         if (4 * written - rpos < 32) {
+            if (wave_inside) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) pf[j] = load_group(written + j);
+                for (int j = 0; j < PG; ++j)
+                    pf[j] = *reinterpret_cast<const uint64_t*>(a.words + g0 + 4ull * (written + j));
+            } else {
+#pragma unroll
+                for (int j = 0; j < PG; ++j) pf[j] = load_group(written + j);
+            }
             inflight = true;
         }
     };
@@ -587,8 +607,8 @@ __global__ __launch_bounds__(64 * W) void rans_decode_kernel(RansArgs a) {
         uint4 prev = make_uint4(0u, 0u, 0u, 0u);
         for (; i + 16 <= n_sym; i += 16) {
             refill();
-            if (i) *reinterpret_cast<uint4*>(out + i - 16) = prev;
             prefetch();
+            if (i) *reinterpret_cast<uint4*>(out + i - 16) = prev;
             uint32_t ob[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
