@@ -31,9 +31,12 @@ __device__ __forceinline__ int hist_bin(int8_t c, int L) {
 // histogram of c + L over [0, 2L] (the host folds it when no code is odd).
 // Lattice codes are peaked around 0, so a wave's 64 lanes mostly hit a few
 // bins: each of 16 lane groups (lane % 16) counts into its own copy of the
-// bins, so at most 4 lanes of a wave meet on one address, and the copies are
-// 65 words apart so that equal bins of different copies sit in different banks.
-// (One copy per lane measured the same.)
+// bins, so at most 4 lanes of a wave meet on one address.  Copy c's bin b is
+// word c * hs + b, in bank (c * hs + b) mod 64.  With hs = 17 (17 bins, levels
+// 8) the busy central bins of different copies fall in different banks; with
+// hs = 65 (the earlier layout) copy c + 1's bin b - 1 shared copy c's bin b's
+// bank, and one instruction's busiest bank held about 7 lanes instead of 4.
+// Levels 16 (33 bins) keep hs = 65.  (One copy per lane measured the same.)
 constexpr int kHistCopies = 16;
 constexpr int kHistStride = kRansMaxAlpha + 1;
 
@@ -41,7 +44,8 @@ __global__ __launch_bounds__(256) void rans_hist_kernel(const int8_t* codes, int
     __shared__ uint32_t h_all[kHistCopies * kHistStride];
     for (int i = threadIdx.x; i < kHistCopies * kHistStride; i += 256) h_all[i] = 0;
     __syncthreads();
-    uint32_t* const h = h_all + (threadIdx.x & (kHistCopies - 1)) * kHistStride;
+    const int hs = 2 * L + 1 <= 17 ? 17 : kHistStride;  // words between copies
+    uint32_t* const h = h_all + (threadIdx.x & (kHistCopies - 1)) * hs;
     const int64_t stride = (int64_t)gridDim.x * 256 * 16;
     for (int64_t base = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16; base < n; base += stride) {
         if (base + 16 <= n) {
@@ -59,7 +63,7 @@ __global__ __launch_bounds__(256) void rans_hist_kernel(const int8_t* codes, int
     if (threadIdx.x <= 2 * L) {
         uint32_t t = 0;
 #pragma unroll
-        for (int c = 0; c < kHistCopies; ++c) t += h_all[c * kHistStride + threadIdx.x];
+        for (int c = 0; c < kHistCopies; ++c) t += h_all[c * hs + threadIdx.x];
         if (t) atomicAdd(&hist[threadIdx.x], t);
     }
 }
