@@ -350,7 +350,11 @@ int nq_merge_values(const nq_merge_desc* desc, void* stream);
  *   nq_rans_compact: words[offset[k] ..] = chunk k's words; scratch 8-byte
  *     and words 4-byte aligned.
  *   nq_rans_decode: codes from the compacted words and offsets; words 8-byte
- *     and codes 16-byte aligned.
+ *     and codes 16-byte aligned.  offset must be a layout nq_rans_encode can
+ *     write: offset[0] = 0, non-decreasing, chunk k holding at most its symbol
+ *     count + 2 words, and words[0 .. offset[n_chunks]) readable (the kernel
+ *     reads ahead of a chunk's words up to that end).  A stream from elsewhere
+ *     is checked on the host first (entropy.check_stream_layout).
  * freq: uint16 [alphabet], summing to 4096, nonzero for every symbol present.
  *
  * Replaces: _build_freq_table / _rans_encode / _rans_decode use in
