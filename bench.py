@@ -749,22 +749,28 @@ def rans_full_stream(ck, cv, fp16_bytes, torch):
     NQR1 stream per layer and role (160 streams of 134M symbols, 65536 chains
     each), and one stream per role over all 80 layers (2 streams, 5.2M chains
     each, one frequency table per role).  Wall time over the calls, each
-    including its host-side frequency table."""
+    including its host-side frequency table.  The per-layer streams go through
+    the batched calls (rans_encode_many / rans_decode_many: the same streams,
+    with different tensors' launches overlapping on worker streams)."""
     from nexusquant_amd.codec import codes_int8
-    from nexusquant_amd.entropy import rans_decode, rans_encode
+    from nexusquant_amd.entropy import rans_decode, rans_decode_many, rans_encode, rans_encode_many
     ik, iv = codes_int8(ck), codes_int8(cv)
-    warm = rans_encode(ik[0], 8)
-    rans_decode(warm)
+    warm = rans_encode_many([ik[0], iv[0]], [8, 4])
+    rans_decode_many(warm)
+    rans_decode(rans_encode(ik[0], 8))
     del warm
 
-    def run(jobs):
+    def run(jobs, batched):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        streams = [rans_encode(c, lv) for c, lv in jobs]
+        if batched:
+            streams = rans_encode_many([c for c, _ in jobs], [lv for _, lv in jobs])
+        else:
+            streams = [rans_encode(c, lv) for c, lv in jobs]
         torch.cuda.synchronize()
         enc_s = time.perf_counter() - t0
         t0 = time.perf_counter()
-        back = [rans_decode(st) for st in streams]
+        back = rans_decode_many(streams) if batched else [rans_decode(st) for st in streams]
         torch.cuda.synchronize()
         dec_s = time.perf_counter() - t0
         lossless = all(torch.equal(b, c) for b, (c, _) in zip(back, jobs))
@@ -777,10 +783,10 @@ def rans_full_stream(ck, cv, fp16_bytes, torch):
                 "encode_gsym_s": round(n_sym / enc_s / 1e9, 1), "decode_gsym_s": round(n_sym / dec_s / 1e9, 1),
                 "lossless": lossless}
 
-    per_layer = run([(c, 8) for c in ik] + [(c, 4) for c in iv])
+    per_layer = run([(c, 8) for c in ik] + [(c, 4) for c in iv], batched=True)
     whole_k, whole_v = torch.cat([c.reshape(-1) for c in ik]), torch.cat([c.reshape(-1) for c in iv])
     del ik, iv
-    per_role = run([(whole_k, 8), (whole_v, 4)])
+    per_role = run([(whole_k, 8), (whole_v, 4)], batched=False)
     del whole_k, whole_v
     return {"per_layer": per_layer, "per_role": per_role,
             "note": "int8 2p codes; wall time including each call's host-side frequency table; sizes "

@@ -197,6 +197,174 @@ def rans_encode(codes: torch.Tensor, levels: int, chunk: int = DEFAULT_CHUNK,
     return st
 
 
+# Batched coding of many tensors (one stream each, e.g. one per layer and role).
+# One tensor's stream at the default chunk has 65536 chains, one wave per SIMD,
+# so a single launch leaves most of each SIMD idle and a loop of calls runs them
+# one after another.  The batched calls run the launches of different tensors on
+# a few worker streams at once, with two host round trips per group of tensors
+# (the histograms, then the word totals) instead of two per tensor.  The streams
+# are the ones rans_encode writes, word for word.
+_WORKER_STREAMS = 4   # hardware queues per process on these boxes
+_BATCH_GROUP = 16     # tensors in flight at once (bounds the scratch memory)
+_workers = {}
+
+
+def _worker_streams(dev) -> list:
+    key = torch.device(dev).index
+    if key not in _workers:
+        _workers[key] = [torch.cuda.Stream(device=dev) for _ in range(_WORKER_STREAMS)]
+    return _workers[key]
+
+
+def _prepare_codes(codes: torch.Tensor, levels: int) -> torch.Tensor:
+    _lib.require_device(codes, "codes")
+    if codes.dtype != torch.int8:
+        raise TypeError(f"codes must be int8 (2p), got {codes.dtype}")
+    if levels not in (2, 4, 8, 16):
+        raise ValueError(f"levels must be 2, 4, 8 or 16, got {levels}")
+    flat = codes.contiguous().reshape(-1)
+    if flat.data_ptr() % 16:
+        flat = flat.clone()
+    return flat
+
+
+def rans_encode_many(codes_list, levels, chunk: int = DEFAULT_CHUNK, has_half=None) -> list:
+    """rans_encode of each tensor of codes_list (levels / has_half: one value for
+    all, or one per tensor), the launches of different tensors overlapping on a
+    few worker streams.  Returns the RansStreams rans_encode would return."""
+    lib = _lib.load()
+    n_t = len(codes_list)
+    lv = list(levels) if isinstance(levels, (list, tuple)) else [levels] * n_t
+    hh = list(has_half) if isinstance(has_half, (list, tuple)) else [has_half] * n_t
+    if len(lv) != n_t or len(hh) != n_t:
+        raise ValueError("levels and has_half take one value or one per tensor")
+    out = []
+    for g0 in range(0, n_t, _BATCH_GROUP):
+        idx = range(g0, min(n_t, g0 + _BATCH_GROUP))
+        flats = [_prepare_codes(codes_list[i], lv[i]) for i in idx]
+        devs = {f.device for f in flats}
+        if len(devs) != 1:
+            raise ValueError("rans_encode_many: all tensors must be on one device")
+        dev = flats[0].device
+        with torch.cuda.device(dev):
+            cur = torch.cuda.current_stream(dev)
+            # histograms on the current stream, one device-to-host copy for the group
+            tot = torch.zeros(len(flats), 33, dtype=torch.int64, device=dev)
+            for r, (i, flat) in enumerate(zip(idx, flats)):
+                bins = 2 * lv[i] + 1
+                for start in range(0, flat.numel(), _HIST_PIECE):
+                    piece = flat[start:start + _HIST_PIECE]
+                    hist = torch.zeros(bins, dtype=torch.int32, device=dev)
+                    _lib.check(lib.nq_rans_histogram(_addr(piece), piece.numel(), lv[i], _addr(hist),
+                                                     ctypes.c_void_p(cur.cuda_stream)), "nq_rans_histogram")
+                    tot[r, :bins] += hist.to(torch.int64)
+            counts = tot.cpu().numpy()
+            plans = []
+            for r, (i, flat) in enumerate(zip(idx, flats)):
+                h = counts[r, :2 * lv[i] + 1]
+                half = hh[i]
+                if half is None:
+                    half = bool(h[1::2].sum() > 0)
+                elif not half and h[1::2].sum() > 0:
+                    raise ValueError("has_half=False but some codes are odd (half-integer points)")
+                freq = build_freq_table(h if half else h[0::2])
+                n = flat.numel()
+                n_chunks = (n + chunk - 1) // chunk
+                plans.append(dict(flat=flat, n=n, levels=lv[i], half=half, freq=freq, n_chunks=n_chunks,
+                                  shape=tuple(codes_list[i].shape)))
+            freq_all = torch.from_numpy(np.concatenate([p["freq"].view(np.int16) for p in plans]).copy()).to(dev)
+            base = 0
+            for p in plans:
+                p["freq_d"] = freq_all[base:base + len(p["freq"])]
+                base += len(p["freq"])
+                p["scratch"] = torch.empty(max(int(lib.nq_rans_scratch_words(p["n"], chunk)), 1), dtype=torch.int16,
+                                           device=dev)
+                p["n_words"] = torch.empty(max(p["n_chunks"], 1), dtype=torch.int32, device=dev)
+                p["offsets"] = torch.empty(p["n_chunks"] + 1, dtype=torch.int64, device=dev)
+            workers = _worker_streams(dev)
+            ready = cur.record_event()
+            for w in workers:
+                w.wait_event(ready)
+            for k, p in enumerate(plans):
+                s = workers[k % len(workers)]
+                _lib.check(lib.nq_rans_encode(_addr(p["flat"]), p["n"], p["levels"], int(p["half"]), _addr(p["freq_d"]),
+                                              len(p["freq"]), chunk, _addr(p["scratch"]), _addr(p["n_words"]),
+                                              _addr(p["offsets"]), ctypes.c_void_p(s.cuda_stream)), "nq_rans_encode")
+            for w in workers:
+                cur.wait_stream(w)
+            totals = torch.stack([p["offsets"][-1] for p in plans]).cpu().tolist()
+            for p, total in zip(plans, totals):
+                p["total"] = int(total)
+                p["words"] = torch.empty(max(p["total"], 1), dtype=torch.int16, device=dev)
+            ready = cur.record_event()
+            for w in workers:
+                w.wait_event(ready)
+            for k, p in enumerate(plans):
+                s = workers[k % len(workers)]
+                _lib.check(lib.nq_rans_compact(_addr(p["scratch"]), _addr(p["n_words"]), _addr(p["offsets"]), p["n"],
+                                               chunk, _addr(p["words"]), ctypes.c_void_p(s.cuda_stream)),
+                           "nq_rans_compact")
+            for w in workers:
+                cur.wait_stream(w)  # the scratch buffers go back to the allocator after this point
+        for p in plans:
+            st = RansStream(words=p["words"][:p["total"]], offsets=p["offsets"], freq=p["freq"], levels=p["levels"],
+                            has_half=p["half"], n=p["n"], chunk=chunk, shape=p["shape"])
+            st._checked = st._layout_key()
+            out.append(st)
+    return out
+
+
+def rans_decode_many(streams, device=None) -> list:
+    """rans_decode of each stream, the launches overlapping on a few worker
+    streams; returns the int8 codes in each stream's shape."""
+    lib = _lib.load()
+    outs, jobs = [], []
+    for stream in streams:
+        key = stream._layout_key()
+        if stream._checked != key:
+            check_stream_layout(stream.levels, stream.has_half, stream.alphabet, stream.n, stream.chunk,
+                                stream.offsets.numel() - 1, stream.freq, stream.offsets.cpu().numpy(),
+                                stream.words.numel())
+            stream._checked = key
+        if int(np.prod(stream.shape)) != stream.n:
+            raise ValueError(f"stream shape {stream.shape} does not hold {stream.n} symbols")
+        dev = stream.words.device if device is None else torch.device(device)
+        out = torch.empty(stream.n, dtype=torch.int8, device=dev)
+        outs.append(out.reshape(stream.shape))
+        if stream.n:
+            words = stream.words.to(dev)
+            if words.numel() == 0:
+                words = torch.zeros(1, dtype=torch.int16, device=dev)
+            if words.data_ptr() % 8:
+                words = words.clone()
+            jobs.append((dev, stream, words, stream.offsets.to(dev), out))
+    by_dev = {}
+    for job in jobs:
+        by_dev.setdefault(job[0], []).append(job)
+    for dev, dev_jobs in by_dev.items():
+        with torch.cuda.device(dev):
+            cur = torch.cuda.current_stream(dev)
+            freq_all = torch.from_numpy(np.concatenate([j[1].freq.view(np.int16) for j in dev_jobs]).copy()).to(dev)
+            workers = _worker_streams(dev)
+            ready = cur.record_event()
+            for w in workers:
+                w.wait_event(ready)
+            base = 0
+            keep = []
+            for k, (_, stream, words, offsets, out) in enumerate(dev_jobs):
+                freq_d = freq_all[base:base + stream.alphabet]
+                base += stream.alphabet
+                s = workers[k % len(workers)]
+                _lib.check(lib.nq_rans_decode(_addr(words), _addr(offsets), stream.n, stream.levels,
+                                              int(stream.has_half), _addr(freq_d), stream.alphabet, stream.chunk,
+                                              _addr(out), ctypes.c_void_p(s.cuda_stream)), "nq_rans_decode")
+                keep.append((words, offsets))
+            for w in workers:
+                cur.wait_stream(w)  # inputs copied or cloned above are released after this point
+            del keep
+    return outs
+
+
 def check_stream_header(levels: int, has_half: bool, alphabet: int, n: int, chunk: int, n_chunks: int) -> None:
     """Raise ValueError unless a stream header's counts agree with each other."""
     if levels not in (2, 4, 8, 16):

@@ -159,3 +159,40 @@ def test_stream_longer_than_2_31_codes_roundtrips():
     st = rans_encode(codes, levels)
     back = rans_decode(st)
     assert torch.equal(back, codes)
+
+
+def test_encode_many_and_decode_many_equal_the_single_calls():
+    """rans_encode_many / rans_decode_many run many tensors' launches on worker
+    streams at once: 20 tensors (two groups of at most 16), every level, an
+    empty and a one-code tensor, ragged and multi-chunk sizes, a view at an odd
+    byte offset (cloned to 16-byte alignment) and per-tensor has_half.  Every
+    stream's words, offsets, frequency table and alphabet equal rans_encode's
+    on the same tensor, and every stream decodes to its codes."""
+    from nexusquant_amd.entropy import rans_decode_many, rans_encode, rans_encode_many
+    print("[gpu] rans encode_many / decode_many against single calls", flush=True)
+    rng = np.random.default_rng(21)
+    sizes = [(0, 8), (1, 8), (4097, 4), (300_001, 8), (70_000, 2), (2048 * 40 + 5, 16), (131_072, 8)]
+    tensors, levels = [], []
+    for k in range(20):
+        n, lv = sizes[k % len(sizes)]
+        half = k % 3 != 0
+        vals = np.arange(-lv, lv + 1) if half else np.arange(-lv, lv + 1, 2)
+        p = np.exp(-0.5 * (vals / (1.0 + lv / 4)) ** 2)
+        c = rng.choice(vals, n, p=p / p.sum()).astype(np.int8)
+        if k == 5:  # a view 1 byte into its buffer
+            t = torch.from_numpy(np.concatenate([np.zeros(1, np.int8), c])).to(DEV)[1:]
+        else:
+            t = torch.from_numpy(c).to(DEV)
+        tensors.append(t)
+        levels.append(lv)
+    many = rans_encode_many(tensors, levels)
+    assert len(many) == len(tensors)
+    for t, lv, st in zip(tensors, levels, many):
+        one = rans_encode(t, lv)
+        assert st.has_half == one.has_half and st.n == one.n and st.shape == one.shape
+        assert np.array_equal(st.freq, one.freq)
+        assert torch.equal(st.offsets, one.offsets)
+        assert torch.equal(st.words, one.words)
+    back = rans_decode_many(many)
+    for t, b in zip(tensors, back):
+        assert torch.equal(b, t)
