@@ -200,12 +200,14 @@ def rans_encode(codes: torch.Tensor, levels: int, chunk: int = DEFAULT_CHUNK,
 # Batched coding of many tensors (one stream each, e.g. one per layer and role).
 # One tensor's stream at the default chunk has 65536 chains, one wave per SIMD,
 # so a single launch leaves most of each SIMD idle and a loop of calls runs them
-# one after another.  The batched calls run the launches of different tensors on
-# a few worker streams at once, with two host round trips per group of tensors
-# (the histograms, then the word totals) instead of two per tensor.  The streams
+# one after another with two host round trips each.  The batched calls run the
+# launches of different tensors on worker streams at once and pipeline groups
+# of tensors: while a group's encoder launches run on the workers, the next
+# group's histograms run on the caller's stream, and one host round trip reads
+# both the group's word totals and the next group's histograms.  The streams
 # are the ones rans_encode writes, word for word.
-_WORKER_STREAMS = 4   # hardware queues per process on these boxes
-_BATCH_GROUP = 16     # tensors in flight at once (bounds the scratch memory)
+_WORKER_STREAMS = 3   # with the caller's stream, the 4 hardware queues a process gets here
+_BATCH_GROUP = 16     # tensors per group (bounds the scratch memory in flight)
 _workers = {}
 
 
@@ -231,36 +233,44 @@ def _prepare_codes(codes: torch.Tensor, levels: int) -> torch.Tensor:
 def rans_encode_many(codes_list, levels, chunk: int = DEFAULT_CHUNK, has_half=None) -> list:
     """rans_encode of each tensor of codes_list (levels / has_half: one value for
     all, or one per tensor), the launches of different tensors overlapping on a
-    few worker streams.  Returns the RansStreams rans_encode would return."""
+    few worker streams.  Returns the RansStreams rans_encode would return; the
+    words and offsets of the streams of one group of tensors are views of one
+    buffer each, which lives while any of them does."""
     lib = _lib.load()
     n_t = len(codes_list)
     lv = list(levels) if isinstance(levels, (list, tuple)) else [levels] * n_t
     hh = list(has_half) if isinstance(has_half, (list, tuple)) else [has_half] * n_t
     if len(lv) != n_t or len(hh) != n_t:
         raise ValueError("levels and has_half take one value or one per tensor")
+    if n_t == 0:
+        return []
+    flats = [_prepare_codes(c, l) for c, l in zip(codes_list, lv)]
+    if len({f.device for f in flats}) != 1:
+        raise ValueError("rans_encode_many: all tensors must be on one device")
+    dev = flats[0].device
+    groups = [list(range(g, min(n_t, g + _BATCH_GROUP))) for g in range(0, n_t, _BATCH_GROUP)]
     out = []
-    for g0 in range(0, n_t, _BATCH_GROUP):
-        idx = range(g0, min(n_t, g0 + _BATCH_GROUP))
-        flats = [_prepare_codes(codes_list[i], lv[i]) for i in idx]
-        devs = {f.device for f in flats}
-        if len(devs) != 1:
-            raise ValueError("rans_encode_many: all tensors must be on one device")
-        dev = flats[0].device
-        with torch.cuda.device(dev):
-            cur = torch.cuda.current_stream(dev)
-            # histograms on the current stream, one device-to-host copy for the group
-            tot = torch.zeros(len(flats), 33, dtype=torch.int64, device=dev)
-            for r, (i, flat) in enumerate(zip(idx, flats)):
+    with torch.cuda.device(dev):
+        cur = torch.cuda.current_stream(dev)
+        h_cur = ctypes.c_void_p(cur.cuda_stream)
+        workers = _worker_streams(dev)
+
+        def launch_hists(idx):  # int64 [len(idx), 33] on the caller's stream
+            tot = torch.zeros(len(idx), 33, dtype=torch.int64, device=dev)
+            for r, i in enumerate(idx):
                 bins = 2 * lv[i] + 1
-                for start in range(0, flat.numel(), _HIST_PIECE):
-                    piece = flat[start:start + _HIST_PIECE]
+                for start in range(0, flats[i].numel(), _HIST_PIECE):
+                    piece = flats[i][start:start + _HIST_PIECE]
                     hist = torch.zeros(bins, dtype=torch.int32, device=dev)
-                    _lib.check(lib.nq_rans_histogram(_addr(piece), piece.numel(), lv[i], _addr(hist),
-                                                     ctypes.c_void_p(cur.cuda_stream)), "nq_rans_histogram")
+                    _lib.check(lib.nq_rans_histogram(_addr(piece), piece.numel(), lv[i], _addr(hist), h_cur),
+                               "nq_rans_histogram")
                     tot[r, :bins] += hist.to(torch.int64)
-            counts = tot.cpu().numpy()
+            return tot
+
+        counts = launch_hists(groups[0]).cpu().numpy()
+        for gi, idx in enumerate(groups):
             plans = []
-            for r, (i, flat) in enumerate(zip(idx, flats)):
+            for r, i in enumerate(idx):
                 h = counts[r, :2 * lv[i] + 1]
                 half = hh[i]
                 if half is None:
@@ -268,20 +278,26 @@ def rans_encode_many(codes_list, levels, chunk: int = DEFAULT_CHUNK, has_half=No
                 elif not half and h[1::2].sum() > 0:
                     raise ValueError("has_half=False but some codes are odd (half-integer points)")
                 freq = build_freq_table(h if half else h[0::2])
-                n = flat.numel()
-                n_chunks = (n + chunk - 1) // chunk
-                plans.append(dict(flat=flat, n=n, levels=lv[i], half=half, freq=freq, n_chunks=n_chunks,
-                                  shape=tuple(codes_list[i].shape)))
+                n = flats[i].numel()
+                plans.append(dict(flat=flats[i], n=n, levels=lv[i], half=half, freq=freq,
+                                  n_chunks=(n + chunk - 1) // chunk, shape=tuple(codes_list[i].shape)))
             freq_all = torch.from_numpy(np.concatenate([p["freq"].view(np.int16) for p in plans]).copy()).to(dev)
-            base = 0
-            for p in plans:
+            # one allocation per group for each kind of buffer, sliced per tensor;
+            # scratch slices start on 8-byte boundaries (4-word multiples)
+            sw = [(max(int(lib.nq_rans_scratch_words(p["n"], chunk)), 1) + 3) // 4 * 4 for p in plans]
+            scratch_all = torch.empty(sum(sw), dtype=torch.int16, device=dev)
+            nw_all = torch.empty(sum(max(p["n_chunks"], 1) for p in plans), dtype=torch.int32, device=dev)
+            off_all = torch.empty(sum(p["n_chunks"] + 1 for p in plans), dtype=torch.int64, device=dev)
+            base = bs = bn = bo = 0
+            for p, w in zip(plans, sw):
                 p["freq_d"] = freq_all[base:base + len(p["freq"])]
                 base += len(p["freq"])
-                p["scratch"] = torch.empty(max(int(lib.nq_rans_scratch_words(p["n"], chunk)), 1), dtype=torch.int16,
-                                           device=dev)
-                p["n_words"] = torch.empty(max(p["n_chunks"], 1), dtype=torch.int32, device=dev)
-                p["offsets"] = torch.empty(p["n_chunks"] + 1, dtype=torch.int64, device=dev)
-            workers = _worker_streams(dev)
+                p["scratch"] = scratch_all[bs:bs + w]
+                bs += w
+                p["n_words"] = nw_all[bn:bn + max(p["n_chunks"], 1)]
+                bn += max(p["n_chunks"], 1)
+                p["offsets"] = off_all[bo:bo + p["n_chunks"] + 1]
+                bo += p["n_chunks"] + 1
             ready = cur.record_event()
             for w in workers:
                 w.wait_event(ready)
@@ -290,12 +306,23 @@ def rans_encode_many(codes_list, levels, chunk: int = DEFAULT_CHUNK, has_half=No
                 _lib.check(lib.nq_rans_encode(_addr(p["flat"]), p["n"], p["levels"], int(p["half"]), _addr(p["freq_d"]),
                                               len(p["freq"]), chunk, _addr(p["scratch"]), _addr(p["n_words"]),
                                               _addr(p["offsets"]), ctypes.c_void_p(s.cuda_stream)), "nq_rans_encode")
+            # the next group's histograms run beside this group's encoders
+            nxt = launch_hists(groups[gi + 1]) if gi + 1 < len(groups) else None
             for w in workers:
                 cur.wait_stream(w)
-            totals = torch.stack([p["offsets"][-1] for p in plans]).cpu().tolist()
-            for p, total in zip(plans, totals):
+            totals = torch.stack([p["offsets"][-1] for p in plans])
+            if nxt is not None:
+                both = torch.cat([totals, nxt.reshape(-1)]).cpu().numpy()
+                totals_h, counts = both[:len(plans)], both[len(plans):].reshape(-1, 33)
+            else:
+                totals_h = totals.cpu().numpy()
+            ww = [(max(int(t), 1) + 3) // 4 * 4 for t in totals_h]  # 8-byte aligned slices
+            words_all = torch.empty(sum(ww), dtype=torch.int16, device=dev)
+            bw = 0
+            for p, total, w in zip(plans, totals_h, ww):
                 p["total"] = int(total)
-                p["words"] = torch.empty(max(p["total"], 1), dtype=torch.int16, device=dev)
+                p["words"] = words_all[bw:bw + w]
+                bw += w
             ready = cur.record_event()
             for w in workers:
                 w.wait_event(ready)
@@ -304,13 +331,15 @@ def rans_encode_many(codes_list, levels, chunk: int = DEFAULT_CHUNK, has_half=No
                 _lib.check(lib.nq_rans_compact(_addr(p["scratch"]), _addr(p["n_words"]), _addr(p["offsets"]), p["n"],
                                                chunk, _addr(p["words"]), ctypes.c_void_p(s.cuda_stream)),
                            "nq_rans_compact")
+            # the caller's stream waits for the compactions, so the scratch buffers
+            # (allocated on it) are reused only after them
             for w in workers:
-                cur.wait_stream(w)  # the scratch buffers go back to the allocator after this point
-        for p in plans:
-            st = RansStream(words=p["words"][:p["total"]], offsets=p["offsets"], freq=p["freq"], levels=p["levels"],
-                            has_half=p["half"], n=p["n"], chunk=chunk, shape=p["shape"])
-            st._checked = st._layout_key()
-            out.append(st)
+                cur.wait_stream(w)
+            for p in plans:
+                st = RansStream(words=p["words"][:p["total"]], offsets=p["offsets"], freq=p["freq"], levels=p["levels"],
+                                has_half=p["half"], n=p["n"], chunk=chunk, shape=p["shape"])
+                st._checked = st._layout_key()
+                out.append(st)
     return out
 
 
